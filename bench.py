@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""GPT-OSS-120B MoE-layer decode throughput on one MI355X.
+
+A step is one MoE layer forward (router GEMV + top-k softmax + routing plan,
+MXFP4 gate_up + SwiGLU, MXFP4 down + weighted combine with the residual) over
+a batch of B decode tokens, E=128 experts, H=I=2880, top-4.  Weights are
+synthetic with the BASELINE distributions (uniform e2m1 codes, e8m0 scales
+2^-8..2^-4, router ~N(0,0.02), zero non-null biases) and live in HBM; the
+timed steps rotate over `--copies` distinct weight copies and inputs so the
+256 MB MALL cannot hold a step's weights.  The K timed steps are one hipGraph
+replay; per-launch durations come from HIP events recorded on the launch
+stream inside that replay.
+
+The headline `value` is tokens/s at the largest batch (64); every batch of
+the sweep is reported under `sweep`.  `roofline` is for the dominant kernel
+(the W1 gate_up + SwiGLU launch) at the headline batch.  `cpu_baseline` is
+the C oracle (oracle/moe_oracle.c) timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "hip-kernels_amd"))
+
+E, K_TOP, H, I = 128, 4, 2880, 2880
+HBM_PEAK_GBS = 8000.0
+# algorithmic bytes per touched expert: W1 nibbles + scales + bias, W2 nibbles + scales + bias
+W1_EXPERT_BYTES = 2 * I * H // 2 + 2 * I * H // 32 + 2 * I * 2
+W2_EXPERT_BYTES = H * I // 2 + H * I // 32 + H * 2
+ROUTER_BYTES = E * H * 2 + E * 2
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def layer_bytes(U: int, T: int) -> int:
+    """Algorithmic HBM bytes of one layer forward: each touched expert's MXFP4
+    weights, scales and biases once, the router, and x / residual / out."""
+    return U * (W1_EXPERT_BYTES + W2_EXPERT_BYTES) + ROUTER_BYTES + T * H * 2 * 3
+
+
+def make_copy(g, torch, seed: int):
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    n1, s1 = g.tiled_size(2 * I, H)
+    n2, s2 = g.tiled_size(H, I)
+    w1n = torch.randint(0, 256, (E * n1,), dtype=torch.uint8, device="cuda", generator=gen)
+    w1s = torch.randint(119, 124, (E * s1,), dtype=torch.uint8, device="cuda", generator=gen)
+    w2n = torch.randint(0, 256, (E * n2,), dtype=torch.uint8, device="cuda", generator=gen)
+    w2s = torch.randint(119, 124, (E * s2,), dtype=torch.uint8, device="cuda", generator=gen)
+    rw = (torch.randn((E, H), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    rb = (torch.randn((E,), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    b1 = torch.zeros((E, 2 * I), dtype=torch.bfloat16, device="cuda")
+    b2 = torch.zeros((E, H), dtype=torch.bfloat16, device="cuda")
+    return dict(tiled=(w1n, w1s, w2n, w2s), router_w=rw, router_b=rb, b1=b1, b2=b2)
+
+
+def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int):
+    """Time `steps` graph-replayed layer forwards at batch T; returns a dict."""
+    layers = []
+    for c, wc in enumerate(copies):
+        cfg = g.default_config(E, T)
+        L = g.MoELayer().init(cfg, 0, wc["router_w"], wc["router_b"], wc["b1"], wc["b2"], tiled=wc["tiled"])
+        layers.append(L)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    n_in = max(len(copies), 8)
+    xs = [(torch.randn((T, H), device="cuda", generator=gen)).to(torch.bfloat16) for _ in range(n_in)]
+    rs = [(torch.randn((T, H), device="cuda", generator=gen)).to(torch.bfloat16) for _ in range(n_in)]
+    outs = [torch.empty((T, H), dtype=torch.bfloat16, device="cuda") for _ in range(n_in)]
+    plan = [(i % len(layers), i % n_in) for i in range(steps)]
+
+    # untimed: experts touched by each step (routing is deterministic)
+    U = []
+    for li, xi in plan:
+        layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
+        n_act = g.copy_device_to_tensor(layers[li].trace().n_active, 4, torch.int32)
+        U.append(int(n_act.item()))
+    # eager warmup
+    for i in range(warmup):
+        li, xi = plan[i % len(plan)]
+        layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
+    torch.cuda.synchronize()
+
+    # capture the K steps (with per-launch events) in one graph
+    per_layer = [sum(1 for li, _ in plan if li == j) for j in range(len(layers))]
+    for j, L in enumerate(layers):
+        L.set_profiling(per_layer[j])
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for li, xi in plan:
+            layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
+    graph.replay()  # warm replay
+    torch.cuda.synchronize()
+
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    with torch.cuda.stream(s):
+        t0.record(s)
+        graph.replay()
+        t1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_time(t1)
+
+    r_ms = w1_ms = w2_ms = 0.0
+    n_rec = 0
+    for L in layers:  # the graph's event nodes were re-recorded by the timed replay
+        r, a, b, n = L.profile_read()
+        r_ms += r
+        w1_ms += a
+        w2_ms += b
+        n_rec += n
+    for L in layers:
+        L.destroy()
+    del graph
+    ms_step = total_ms / steps
+    u_mean = sum(U) / len(U)
+    bytes_step = sum(layer_bytes(u, T) for u in U) / len(U)
+    w1_bytes = sum(u * W1_EXPERT_BYTES + T * H * 2 for u in U) / len(U)
+    res = dict(batch=T, ms_per_step=ms_step, tokens_per_s=T / (ms_step / 1e3), experts_touched=u_mean,
+               algorithmic_bytes_per_step=bytes_step, hbm_gbs=bytes_step / (ms_step / 1e3) / 1e9,
+               wall_s=wall, events_recorded=n_rec)
+    res["hbm_frac"] = res["hbm_gbs"] / HBM_PEAK_GBS
+    if n_rec == steps:
+        res["kernel_us"] = dict(route=1e3 * r_ms / steps, w1=1e3 * w1_ms / steps, w2=1e3 * w2_ms / steps)
+        res["w1_algorithmic_bytes"] = w1_bytes
+        res["w1_gbs"] = w1_bytes / (w1_ms / steps / 1e3) / 1e9
+    return res
+
+
+def cpu_baseline(seconds: float, threads: int):
+    """The oracle (C, pthreads) on GPT-OSS-120B-shaped layers at batch 64,
+    repeated until `seconds` of wall time; returns tokens/s."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import moe_data
+    import moe_oracle as orc
+    w = moe_data.make_layer(99, E, H, I, bias="zero")
+    T = 64
+    x, res = moe_data.make_tokens(99, T, H)
+    orc.moe_forward(w, x[:1], res[:1], E, K_TOP, H, I, nthreads=threads)  # warm
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        orc.moe_forward(w, x, res, E, K_TOP, H, I, nthreads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return dict(value=n * T / el, unit="tokens/s", cores=threads, kind="port",
+                sample=f"{n} oracle forwards of a GPT-OSS-120B-shaped MoE layer (E=128, H=I=2880, top-4) at "
+                       f"batch 64, {el:.1f} s, {threads} threads")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--batches", default="1,8,32,64")
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build runs the MoE block on a single MI355X "
+              f"(no expert or tensor parallelism); --gpus {args.gpus} is not supported.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import gptoss_moe as g
+
+    batches = [int(b) for b in args.batches.split(",")]
+    headline_b = max(batches)
+    log(f"building {args.copies} weight copies ({args.copies * 1.7:.1f} GB)")
+    copies = [make_copy(g, torch, 1000 + c) for c in range(args.copies)]
+    torch.cuda.synchronize()
+    sweep = {}
+    for T in batches:
+        log(f"batch {T}: {args.steps} steps")
+        sweep[T] = bench_batch(g, torch, copies, T, args.steps, args.warmup, seed=T)
+        log(json.dumps(sweep[T]))
+    head = sweep[headline_b]
+    rf = None
+    if "w1_gbs" in head:
+        rf = dict(bound="hbm", achieved=head["w1_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                  frac=head["w1_gbs"] / HBM_PEAK_GBS, traffic=None,
+                  kernel="w1_kernel (MXFP4 gate_up + SwiGLU)",
+                  algorithmic_bytes_per_launch=head["w1_algorithmic_bytes"],
+                  avg_launch_us=head["kernel_us"]["w1"])
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"cpu baseline: oracle, {threads} threads, ~{args.cpu_seconds} s")
+        cpu = cpu_baseline(args.cpu_seconds, threads)
+    line = {
+        "metric": "MoE-layer tokens/s (GPT-OSS-120B shape, decode)",
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4-weights/bf16-act/fp32-acc",
+        "data": "synthetic (BASELINE distributions), random-init weights",
+        "config": {"workload": f"gptoss120b_moe_layer_decode_b{headline_b}", "experts": E, "top_k": K_TOP,
+                   "hidden": H, "intermediate": I, "batch": headline_b, "weight_copies": args.copies,
+                   "hipgraph": True, "parallelism": "none (1 GPU)"},
+        "hbm_gbs": head["hbm_gbs"],
+        "hbm_frac_of_peak": head["hbm_frac"],
+        "roofline": rf,
+        "cpu_baseline": cpu,
+        "sweep": {str(k): v for k, v in sweep.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

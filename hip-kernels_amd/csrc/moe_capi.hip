@@ -1,0 +1,569 @@
+// moe_capi.hip -- C ABI of the gfx950 MoE block (include/gptoss_moe.h).
+//
+// The layer object mirrors gptoss::MoELayer (moe_layer.cu:607-1549): it
+// borrows the router/bias weights, owns (or borrows) the tiled MXFP4 experts
+// and owns its scratch.  A forward is two launches on the caller's stream
+// (route, experts) plus an RMSNorm launch for forward(); nothing synchronises
+// the host, so a forward can be captured in a hipGraph.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/gptoss_moe.h"
+#include "moe_kernels.h"
+#include "moe_stages.h"
+
+using namespace gxmoe;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return GPTOSS_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(GPTOSS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                     \
+  do {                                          \
+    hipError_t _e = (expr);                     \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+  } while (0)
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool valid_topk(int k) { return k == 1 || k == 2 || k == 4 || k == 8; }
+
+// Shape limits of the tiled expert kernels: K a multiple of 32 with at most 16
+// blocks per K-part, N a multiple of 64.
+int check_mxfp4_shape(int N, int K) {
+  if (N <= 0 || K <= 0) return fail(GPTOSS_ERR_INVALID, "MXFP4 matrix shape %dx%d must be positive", N, K);
+  if (K % 32 != 0) return fail(GPTOSS_ERR_INVALID, "MXFP4 K=%d is not a multiple of the 32-element block", K);
+  if (N % kTileRows != 0) return fail(GPTOSS_ERR_UNSUPPORTED, "MXFP4 N=%d is not a multiple of 64 rows", N);
+  const TiledGeom g = tiled_geom(N, K);
+  if (g.bpp > 16)
+    return fail(GPTOSS_ERR_UNSUPPORTED, "MXFP4 K=%d splits into %d parts of %d blocks (> 16 per part)", K, g.parts, g.bpp);
+  return GPTOSS_OK;
+}
+
+struct ScopedDevice {
+  int prev = -1;
+  bool changed = false;
+  hipError_t err = hipSuccess;
+  explicit ScopedDevice(int dev) {
+    err = hipGetDevice(&prev);
+    if (err == hipSuccess && prev != dev) {
+      err = hipSetDevice(dev);
+      changed = (err == hipSuccess);
+    }
+  }
+  ~ScopedDevice() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+}  // namespace
+
+struct gptoss_moe_layer {
+  bool initialized = false;
+  gptoss_moe_config cfg{};
+  int device = 0;
+  const uint16_t* norm_w = nullptr;
+  const uint16_t* router_w = nullptr;
+  const uint16_t* router_b = nullptr;
+  const uint16_t* b1 = nullptr;
+  const uint16_t* b2 = nullptr;
+  const uint8_t* w1n = nullptr;
+  const uint8_t* w1s = nullptr;
+  const uint8_t* w2n = nullptr;
+  const uint8_t* w2s = nullptr;
+  std::vector<void*> owned;
+  // scratch
+  void* logits = nullptr;
+  float* xf = nullptr;
+  int32_t* idx = nullptr;
+  float* w = nullptr;
+  int32_t* counts = nullptr;
+  int32_t* offsets = nullptr;
+  int32_t* gmap = nullptr;
+  int32_t* ptok = nullptr;
+  int32_t* active = nullptr;
+  int32_t* n_active = nullptr;
+  float* act = nullptr;
+  uint16_t* y = nullptr;
+  uint16_t* gate_up = nullptr;
+  uint16_t* normed = nullptr;
+  uint32_t* counters = nullptr;
+  int n_groups = 0;
+  bool trace_gu = false;
+  // per-launch timing (gptoss_moe_layer_set_profiling): 4 events per recorded forward
+  std::vector<hipEvent_t> prof_events;
+  int prof_capacity = 0;
+  int prof_count = 0;
+
+  void release() {
+    for (void* p : owned) (void)hipFree(p);
+    owned.clear();
+    for (hipEvent_t e : prof_events) (void)hipEventDestroy(e);
+    prof_events.clear();
+    prof_capacity = prof_count = 0;
+  }
+  int alloc(void** p, size_t bytes, const char* what) {
+    hipError_t e = hipMalloc(p, bytes < 256 ? 256 : bytes);
+    if (e != hipSuccess) return fail(GPTOSS_ERR_OOM, "hipMalloc(%zu) for %s: %s", bytes, what, hipGetErrorString(e));
+    owned.push_back(*p);
+    return GPTOSS_OK;
+  }
+};
+
+extern "C" {
+
+const char* gptoss_last_error(void) { return g_last_error.c_str(); }
+int gptoss_abi_version(void) { return GPTOSS_MOE_ABI_VERSION; }
+
+int gptoss_moe_config_default(gptoss_moe_config* cfg, int num_experts, int max_tokens) {
+  if (cfg == nullptr) return fail(GPTOSS_ERR_INVALID, "cfg is NULL");
+  cfg->hidden_size = 2880;        // config.h:12
+  cfg->num_experts = num_experts; // config.h:20 (128) or 32 for the 20B shape
+  cfg->top_k = 4;                 // config.h:21
+  cfg->intermediate_size = 2880;  // config.h:22
+  cfg->swiglu_alpha = 1.702f;     // config.h:43
+  cfg->swiglu_limit = 7.0f;       // config.h:42
+  cfg->rms_norm_eps = 1e-5f;      // config.h:39
+  cfg->logits_fp32 = 0;
+  cfg->max_tokens = max_tokens;
+  return ok();
+}
+
+int gptoss_mxfp4_tiled_size(int N, int K, size_t* nibble_bytes, size_t* scale_bytes) {
+  int rc = check_mxfp4_shape(N, K);
+  if (rc != GPTOSS_OK) return rc;
+  const TiledGeom g = tiled_geom(N, K);
+  if (nibble_bytes) *nibble_bytes = g.nib_bytes;
+  if (scale_bytes) *scale_bytes = g.scale_bytes;
+  return ok();
+}
+
+int gptoss_mxfp4_pack_tiled(const uint8_t* packed, const uint8_t* scales, int N, int K, uint8_t* tiled_nibbles,
+                            uint8_t* tiled_scales, void* stream) {
+  int rc = check_mxfp4_shape(N, K);
+  if (rc != GPTOSS_OK) return rc;
+  if (!packed || !scales || !tiled_nibbles || !tiled_scales) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  if (!aligned16(packed) || !aligned16(tiled_nibbles))
+    return fail(GPTOSS_ERR_INVALID, "MXFP4 nibble buffers must be 16-byte aligned");
+  HIP_TRY(launch_pack_tiled(packed, scales, N, K, tiled_nibbles, tiled_scales, static_cast<hipStream_t>(stream)),
+          "pack_tiled launch");
+  return ok();
+}
+
+gptoss_moe_layer* gptoss_moe_layer_create(void) {
+  g_last_error.clear();
+  return new (std::nothrow) gptoss_moe_layer();
+}
+
+void gptoss_moe_layer_destroy(gptoss_moe_layer* layer) {
+  if (layer == nullptr) return;
+  {
+    ScopedDevice sd(layer->device);
+    layer->release();
+  }
+  delete layer;
+}
+
+int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
+                          const gptoss_moe_weights* wt) {
+  if (L == nullptr || cfg == nullptr || wt == nullptr) return fail(GPTOSS_ERR_INVALID, "null argument");
+  if (L->initialized) return fail(GPTOSS_ERR_STATE, "layer already initialised");
+  const int H = cfg->hidden_size, E = cfg->num_experts, k = cfg->top_k, I = cfg->intermediate_size;
+  if (E < 1 || E > kMaxExperts) return fail(GPTOSS_ERR_UNSUPPORTED, "num_experts=%d outside [1, %d]", E, kMaxExperts);
+  if (!valid_topk(k) || k > E) return fail(GPTOSS_ERR_INVALID, "top_k=%d must be 1, 2, 4 or 8 and <= num_experts", k);
+  if (cfg->max_tokens < 1) return fail(GPTOSS_ERR_INVALID, "max_tokens=%d must be >= 1", cfg->max_tokens);
+  if (H % kTileRows != 0) return fail(GPTOSS_ERR_UNSUPPORTED, "hidden_size=%d must be a multiple of 64", H);
+  int rc = check_mxfp4_shape(2 * I, H);
+  if (rc != GPTOSS_OK) return rc;
+  rc = check_mxfp4_shape(H, I);
+  if (rc != GPTOSS_OK) return rc;
+  if (!wt->router_weight) return fail(GPTOSS_ERR_INVALID, "router_weight is NULL");
+  if (!aligned16(wt->router_weight)) return fail(GPTOSS_ERR_INVALID, "router_weight must be 16-byte aligned");
+  const bool tiled = wt->mlp1_tiled_nibbles != nullptr;
+  if (tiled) {
+    if (!wt->mlp1_tiled_scales || !wt->mlp2_tiled_nibbles || !wt->mlp2_tiled_scales)
+      return fail(GPTOSS_ERR_INVALID, "tiled weights: all four tiled buffers are required");
+  } else if (!wt->mlp1_packed || !wt->mlp1_scales || !wt->mlp2_packed || !wt->mlp2_scales) {
+    return fail(GPTOSS_ERR_INVALID, "expert weights missing (neither reference-layout tables nor tiled buffers)");
+  }
+
+  ScopedDevice sd(device_id);
+  if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
+  L->cfg = *cfg;
+  L->device = device_id;
+  L->norm_w = wt->moe_norm_weight;
+  L->router_w = wt->router_weight;
+  L->router_b = wt->router_bias;
+  L->b1 = wt->gate_up_bias;
+  L->b2 = wt->down_bias;
+
+  const TiledGeom g1 = tiled_geom(2 * I, H);
+  const TiledGeom g2 = tiled_geom(H, I);
+  if (tiled) {
+    L->w1n = wt->mlp1_tiled_nibbles;
+    L->w1s = wt->mlp1_tiled_scales;
+    L->w2n = wt->mlp2_tiled_nibbles;
+    L->w2s = wt->mlp2_tiled_scales;
+  } else {
+    void *a, *b, *c, *d;
+    if ((rc = L->alloc(&a, g1.nib_bytes * E, "W1 tiled nibbles")) ||
+        (rc = L->alloc(&b, g1.scale_bytes * E, "W1 tiled scales")) ||
+        (rc = L->alloc(&c, g2.nib_bytes * E, "W2 tiled nibbles")) ||
+        (rc = L->alloc(&d, g2.scale_bytes * E, "W2 tiled scales"))) {
+      L->release();
+      return rc;
+    }
+    L->w1n = static_cast<uint8_t*>(a);
+    L->w1s = static_cast<uint8_t*>(b);
+    L->w2n = static_cast<uint8_t*>(c);
+    L->w2s = static_cast<uint8_t*>(d);
+    for (int e = 0; e < E; ++e) {
+      if (!wt->mlp1_packed[e] || !wt->mlp1_scales[e] || !wt->mlp2_packed[e] || !wt->mlp2_scales[e] ||
+          !aligned16(wt->mlp1_packed[e]) || !aligned16(wt->mlp2_packed[e])) {
+        L->release();
+        return fail(GPTOSS_ERR_INVALID, "expert %d: null or misaligned MXFP4 pointer", e);
+      }
+      hipError_t err = launch_pack_tiled(wt->mlp1_packed[e], wt->mlp1_scales[e], 2 * I, H,
+                                         static_cast<uint8_t*>(a) + g1.nib_bytes * e,
+                                         static_cast<uint8_t*>(b) + g1.scale_bytes * e, nullptr);
+      if (err == hipSuccess)
+        err = launch_pack_tiled(wt->mlp2_packed[e], wt->mlp2_scales[e], H, I,
+                                static_cast<uint8_t*>(c) + g2.nib_bytes * e,
+                                static_cast<uint8_t*>(d) + g2.scale_bytes * e, nullptr);
+      if (err != hipSuccess) {
+        L->release();
+        return hip_fail(err, "pack_tiled");
+      }
+    }
+  }
+
+  const size_t T = static_cast<size_t>(cfg->max_tokens), S = T * k;
+  L->n_groups = static_cast<int>((T + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup);
+  const size_t n_counters = static_cast<size_t>(L->n_groups) + 1 + H / kTileRows;
+  void* p;
+#define ALLOC(field, type, bytes)                          \
+  if ((rc = L->alloc(&p, (bytes), #field)) != GPTOSS_OK) { \
+    L->release();                                          \
+    return rc;                                             \
+  }                                                        \
+  L->field = static_cast<type>(p);
+  ALLOC(logits, void*, T * E * 4)
+  ALLOC(xf, float*, T * H * 4)
+  ALLOC(idx, int32_t*, S * 4)
+  ALLOC(w, float*, S * 4)
+  ALLOC(counts, int32_t*, E * 4)
+  ALLOC(offsets, int32_t*, (E + 1) * 4)
+  ALLOC(gmap, int32_t*, S * 4)
+  ALLOC(ptok, int32_t*, S * 4)
+  ALLOC(active, int32_t*, E * 4)
+  ALLOC(n_active, int32_t*, 4)
+  ALLOC(act, float*, S * I * 4)
+  ALLOC(y, uint16_t*, S * H * 2)
+  ALLOC(counters, uint32_t*, n_counters * 4)
+  if (L->norm_w != nullptr) {
+    ALLOC(normed, uint16_t*, T * H * 2)
+  }
+#undef ALLOC
+  hipError_t err = hipMemset(L->counters, 0, n_counters * 4);
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err != hipSuccess) {
+    L->release();
+    return hip_fail(err, "layer init");
+  }
+  L->initialized = true;
+  return ok();
+}
+
+static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, uint16_t* out,
+                              int T, hipStream_t s) {
+  const gptoss_moe_config& c = L->cfg;
+  RouteArgs ra{};
+  ra.x = normed;
+  ra.W = L->router_w;
+  ra.b = L->router_b;
+  ra.T = T;
+  ra.E = c.num_experts;
+  ra.H = c.hidden_size;
+  ra.k = c.top_k;
+  ra.logits_fp32 = c.logits_fp32;
+  ra.logits = L->logits;
+  ra.xf = L->xf;
+  ra.idx = L->idx;
+  ra.w = L->w;
+  ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active};
+  ra.group_counter = L->counters;
+  ra.done_counter = L->counters + L->n_groups;
+  hipEvent_t* ev = nullptr;
+  if (L->prof_count < L->prof_capacity) ev = &L->prof_events[4 * static_cast<size_t>(L->prof_count++)];
+  if (ev) HIP_TRY(hipEventRecord(ev[0], s), "hipEventRecord");
+  HIP_TRY(launch_route(ra, s), "route launch");
+  if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
+
+  ExpertArgs ea{};
+  ea.xf = L->xf;
+  ea.w1n = L->w1n;
+  ea.w1s = L->w1s;
+  ea.b1 = L->b1;
+  ea.w2n = L->w2n;
+  ea.w2s = L->w2s;
+  ea.b2 = L->b2;
+  ea.T = T;
+  ea.E = c.num_experts;
+  ea.H = c.hidden_size;
+  ea.I = c.intermediate_size;
+  ea.k = c.top_k;
+  ea.alpha = c.swiglu_alpha;
+  ea.limit = c.swiglu_limit;
+  ea.plan = ra.plan;
+  ea.w = L->w;
+  ea.act = L->act;
+  ea.gate_up = L->trace_gu ? L->gate_up : nullptr;
+  ea.y = L->y;
+  ea.residual = residual;
+  ea.out = out;
+  ea.tile_counter = L->counters + L->n_groups + 1;
+  ea.max_active = T * c.top_k < c.num_experts ? T * c.top_k : c.num_experts;
+  HIP_TRY(launch_w1(ea, s), "w1 launch");
+  if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
+  HIP_TRY(launch_w2(ea, s), "w2 launch");
+  if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");
+  return ok();
+}
+
+static int check_forward_args(gptoss_moe_layer* L, const void* in, const void* out, int T) {
+  if (L == nullptr) return fail(GPTOSS_ERR_INVALID, "layer is NULL");
+  if (!L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
+  if (T < 0 || T > L->cfg.max_tokens)
+    return fail(GPTOSS_ERR_INVALID, "num_tokens=%d outside [0, max_tokens=%d]", T, L->cfg.max_tokens);
+  if (T > 0 && (in == nullptr || out == nullptr)) return fail(GPTOSS_ERR_INVALID, "null input/output");
+  if (T > 0 && !aligned16(in)) return fail(GPTOSS_ERR_INVALID, "input must be 16-byte aligned");
+  return GPTOSS_OK;
+}
+
+int gptoss_moe_layer_forward_prenormed(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual,
+                                       uint16_t* out, int T, void* stream) {
+  int rc = check_forward_args(L, normed, out, T);
+  if (rc != GPTOSS_OK) return rc;
+  if (T == 0) return ok();
+  ScopedDevice sd(L->device);
+  if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
+  return layer_forward_core(L, normed, residual, out, T, static_cast<hipStream_t>(stream));
+}
+
+int gptoss_moe_layer_forward(gptoss_moe_layer* L, const uint16_t* input, uint16_t* out, int T, void* stream) {
+  int rc = check_forward_args(L, input, out, T);
+  if (rc != GPTOSS_OK) return rc;
+  if (L->norm_w == nullptr) return fail(GPTOSS_ERR_STATE, "forward() needs moe_norm_weight (init passed NULL)");
+  if (T == 0) return ok();
+  ScopedDevice sd(L->device);
+  if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  HIP_TRY(launch_rmsnorm(input, L->norm_w, L->normed, T, L->cfg.hidden_size, L->cfg.rms_norm_eps, s),
+          "rmsnorm launch");
+  return layer_forward_core(L, L->normed, input, out, T, s);
+}
+
+const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* L) {
+  return L ? L->norm_w : nullptr;
+}
+
+int gptoss_moe_layer_set_trace_gate_up(gptoss_moe_layer* L, int enable) {
+  if (L == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
+  if (enable && L->gate_up == nullptr) {
+    ScopedDevice sd(L->device);
+    void* p;
+    const size_t bytes = static_cast<size_t>(L->cfg.max_tokens) * L->cfg.top_k * 2 * L->cfg.intermediate_size * 2;
+    int rc = L->alloc(&p, bytes, "gate_up trace");
+    if (rc != GPTOSS_OK) return rc;
+    L->gate_up = static_cast<uint16_t*>(p);
+  }
+  L->trace_gu = enable != 0;
+  return ok();
+}
+
+int gptoss_moe_layer_trace(const gptoss_moe_layer* L, gptoss_moe_trace* t) {
+  if (L == nullptr || t == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
+  t->logits = L->logits;
+  t->expert_indices = L->idx;
+  t->expert_weights = L->w;
+  t->expert_counts = L->counts;
+  t->expert_offsets = L->offsets;
+  t->gather_map = L->gmap;
+  t->perm_token = L->ptok;
+  t->active_experts = L->active;
+  t->n_active = L->n_active;
+  t->gate_up = L->trace_gu ? L->gate_up : nullptr;
+  t->act = L->act;
+  t->expert_out = L->y;
+  return ok();
+}
+
+int gptoss_moe_layer_set_profiling(gptoss_moe_layer* L, int max_forwards) {
+  if (L == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
+  if (max_forwards < 0) return fail(GPTOSS_ERR_INVALID, "max_forwards=%d < 0", max_forwards);
+  ScopedDevice sd(L->device);
+  for (hipEvent_t e : L->prof_events) (void)hipEventDestroy(e);
+  L->prof_events.assign(4 * static_cast<size_t>(max_forwards), nullptr);
+  for (auto& e : L->prof_events) HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+  L->prof_capacity = max_forwards;
+  L->prof_count = 0;
+  return ok();
+}
+
+int gptoss_moe_layer_profile_read(gptoss_moe_layer* L, float* route_ms, float* w1_ms, float* w2_ms, int* n_forwards) {
+  if (L == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
+  ScopedDevice sd(L->device);
+  double r = 0, a = 0, b = 0;
+  for (int i = 0; i < L->prof_count; ++i) {
+    hipEvent_t* ev = &L->prof_events[4 * static_cast<size_t>(i)];
+    float t;
+    HIP_TRY(hipEventSynchronize(ev[3]), "hipEventSynchronize");
+    HIP_TRY(hipEventElapsedTime(&t, ev[0], ev[1]), "hipEventElapsedTime");
+    r += t;
+    HIP_TRY(hipEventElapsedTime(&t, ev[1], ev[2]), "hipEventElapsedTime");
+    a += t;
+    HIP_TRY(hipEventElapsedTime(&t, ev[2], ev[3]), "hipEventElapsedTime");
+    b += t;
+  }
+  if (route_ms) *route_ms = static_cast<float>(r);
+  if (w1_ms) *w1_ms = static_cast<float>(a);
+  if (w2_ms) *w2_ms = static_cast<float>(b);
+  if (n_forwards) *n_forwards = L->prof_count;
+  return ok();
+}
+
+size_t gptoss_moe_route_scratch_bytes(int T) {
+  const size_t groups = (T > 0 ? static_cast<size_t>(T) : 1) + kRouteTokensPerGroup - 1;
+  return ((groups / kRouteTokensPerGroup + 1) * 4 + 255) & ~static_cast<size_t>(255);
+}
+
+int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b, int T, int E, int H,
+                     int k, int logits_fp32, void* logits, int32_t* idx, float* w, void* scratch, void* stream) {
+  if (T < 0) return fail(GPTOSS_ERR_INVALID, "num_tokens=%d < 0", T);
+  if (T == 0) return ok();
+  if (E < 1 || E > kMaxExperts) return fail(GPTOSS_ERR_UNSUPPORTED, "num_experts=%d outside [1, %d]", E, kMaxExperts);
+  if (!valid_topk(k) || k > E) return fail(GPTOSS_ERR_INVALID, "top_k=%d must be 1, 2, 4 or 8 and <= E", k);
+  if (H <= 0 || H % 8 != 0) return fail(GPTOSS_ERR_INVALID, "hidden=%d must be a positive multiple of 8", H);
+  if (!x || !router_w || !logits || !idx || !w || !scratch) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  if (!aligned16(x) || !aligned16(router_w)) return fail(GPTOSS_ERR_INVALID, "x and router_w must be 16-byte aligned");
+  RouteArgs ra{};
+  ra.x = x;
+  ra.W = router_w;
+  ra.b = router_b;
+  ra.T = T;
+  ra.E = E;
+  ra.H = H;
+  ra.k = k;
+  ra.logits_fp32 = logits_fp32 ? 1 : 0;
+  ra.logits = logits;
+  ra.xf = nullptr;
+  ra.idx = idx;
+  ra.w = w;
+  ra.plan = PlanBufs{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  const int groups = (T + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup;
+  ra.group_counter = static_cast<uint32_t*>(scratch);
+  ra.done_counter = static_cast<uint32_t*>(scratch) + groups;
+  HIP_TRY(launch_route(ra, static_cast<hipStream_t>(stream)), "route launch");
+  return ok();
+}
+
+int gptoss_topk_softmax_forward(const void* logits, int logits_fp32, int32_t* idx, float* w, int32_t* tpe, int T,
+                                int E, int k, void* stream) {
+  if (T < 0) return fail(GPTOSS_ERR_INVALID, "num_tokens=%d < 0", T);
+  if (T == 0) return ok();
+  if (E < 1 || E > kMaxExperts) return fail(GPTOSS_ERR_UNSUPPORTED, "num_experts=%d outside [1, %d]", E, kMaxExperts);
+  if (!valid_topk(k) || k > E) return fail(GPTOSS_ERR_INVALID, "top_k=%d must be 1, 2, 4 or 8 and <= E", k);
+  if (!logits || !idx || !w) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  HIP_TRY(launch_topk(logits, logits_fp32, T, E, k, idx, w, tpe, static_cast<hipStream_t>(stream)), "topk launch");
+  return ok();
+}
+
+int gptoss_moe_permute_plan(const int32_t* idx, int T, int k, int E, int32_t* counts, int32_t* offsets,
+                            int32_t* gather_map, int32_t* perm_token, int32_t* active, int32_t* n_active,
+                            void* stream) {
+  if (T < 0) return fail(GPTOSS_ERR_INVALID, "num_tokens=%d < 0", T);
+  if (E < 1 || E > kMaxExperts) return fail(GPTOSS_ERR_UNSUPPORTED, "num_experts=%d outside [1, %d]", E, kMaxExperts);
+  if (k < 1 || k > kMaxTopK) return fail(GPTOSS_ERR_INVALID, "top_k=%d outside [1, 8]", k);
+  if (T == 0) return ok();
+  if (!idx || !counts || !offsets || !gather_map || !perm_token || !active || !n_active)
+    return fail(GPTOSS_ERR_INVALID, "null pointer");
+  HIP_TRY(launch_plan(idx, T, k, E, PlanBufs{counts, offsets, gather_map, perm_token, active, n_active},
+                      static_cast<hipStream_t>(stream)),
+          "plan launch");
+  return ok();
+}
+
+int gptoss_moe_scatter_tokens(const uint16_t* x, const int32_t* gather_map, uint16_t* permuted, int T, int H, int k,
+                              void* stream) {
+  if (T < 0 || k < 1 || H <= 0 || H % 8 != 0) return fail(GPTOSS_ERR_INVALID, "bad shape T=%d H=%d k=%d", T, H, k);
+  if (T == 0) return ok();
+  if (!x || !gather_map || !permuted) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  if (!aligned16(x) || !aligned16(permuted)) return fail(GPTOSS_ERR_INVALID, "x/permuted must be 16-byte aligned");
+  HIP_TRY(launch_scatter(x, gather_map, permuted, T, H, k, static_cast<hipStream_t>(stream)), "scatter launch");
+  return ok();
+}
+
+int gptoss_mxfp4_gemv_forward(const uint16_t* x, int M, const uint8_t* wn, const uint8_t* ws, const uint16_t* bias,
+                              uint16_t* y, int N, int K, void* stream) {
+  int rc = check_mxfp4_shape(N, K);
+  if (rc != GPTOSS_OK) return rc;
+  if (M < 0) return fail(GPTOSS_ERR_INVALID, "M=%d < 0", M);
+  if (M == 0) return ok();
+  if (!x || !wn || !ws || !y) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  if (!aligned16(wn)) return fail(GPTOSS_ERR_INVALID, "tiled nibbles must be 16-byte aligned");
+  HIP_TRY(launch_dense_gemv(x, M, wn, ws, bias, y, N, K, static_cast<hipStream_t>(stream)), "gemv launch");
+  return ok();
+}
+
+int gptoss_swiglu_forward(const uint16_t* in, uint16_t* out, int T, int I, float alpha, float limit, void* stream) {
+  if (T < 0 || I <= 0) return fail(GPTOSS_ERR_INVALID, "bad shape T=%d I=%d", T, I);
+  if (T == 0) return ok();
+  if (!in || !out) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  HIP_TRY(launch_swiglu(in, out, T, I, alpha, limit, static_cast<hipStream_t>(stream)), "swiglu launch");
+  return ok();
+}
+
+int gptoss_moe_combine_forward(uint16_t* out, const uint16_t* y, const int32_t* gather_map, const float* w,
+                               const uint16_t* residual, int T, int H, int k, void* stream) {
+  if (T < 0 || H <= 0 || k < 1 || k > kMaxTopK) return fail(GPTOSS_ERR_INVALID, "bad shape T=%d H=%d k=%d", T, H, k);
+  if (T == 0) return ok();
+  if (!out || !y || !gather_map || !w) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  HIP_TRY(launch_combine(out, y, gather_map, w, residual, T, H, k, static_cast<hipStream_t>(stream)),
+          "combine launch");
+  return ok();
+}
+
+int gptoss_mxfp4_dequant(const uint8_t* wn, const uint8_t* ws, int N, int K, uint16_t* out, void* stream) {
+  int rc = check_mxfp4_shape(N, K);
+  if (rc != GPTOSS_OK) return rc;
+  if (!wn || !ws || !out) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  if (!aligned16(wn)) return fail(GPTOSS_ERR_INVALID, "tiled nibbles must be 16-byte aligned");
+  HIP_TRY(launch_dequant(wn, ws, N, K, out, static_cast<hipStream_t>(stream)), "dequant launch");
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// moe_device.h -- device-side helpers shared by the gfx950 MoE kernels.
+//
+// Every floating-point step here is an IEEE operation whose result is fixed
+// by its inputs (add, mul, fma, divide, rint, ldexp), so the CPU oracle that
+// performs the same sequence produces the same bits.  All HIP sources of this
+// library are compiled with -ffp-contract=off; fused multiply-adds are written
+// as __builtin_fmaf where the order of the reference needs them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gxmoe {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN with its sign.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))
+    return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// e^x by Cody-Waite reduction x = n*ln2 + r (|r| <= ln2/2, two-constant
+// split of ln 2 applied with fma) and the degree-7 Taylor polynomial of e^r
+// in Horner form, scaled by 2^n with ldexp.
+__device__ __forceinline__ float gx_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float log2e = 1.44269502162933349609375f;
+  const float ln2_hi = 0.693147182464599609375f;
+  const float ln2_lo = -1.904654323148236e-09f;
+  float n = __builtin_rintf(x * log2e);
+  float r = __builtin_fmaf(-n, ln2_hi, x);
+  r = __builtin_fmaf(-n, ln2_lo, r);
+  float p = 1.98412698e-4f;
+  p = __builtin_fmaf(p, r, 1.38888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, static_cast<int>(n));
+}
+
+// GPT-OSS clamped SwiGLU on one (gate, up) pair: gate clamped above at
+// `limit`, up clamped to [-limit, limit], out = (up + 1) * gate * sigmoid(alpha*gate).
+__device__ __forceinline__ float gx_swiglu(float g, float u, float alpha, float limit) {
+  g = __builtin_fminf(g, limit);
+  u = __builtin_fminf(__builtin_fmaxf(u, -limit), limit);
+  float e = gx_expf((-alpha) * g);
+  float glu = g / (1.0f + e);
+  return (u + 1.0f) * glu;
+}
+
+// e8m0 scale byte -> fp32 by placing the code in the exponent field
+// (code 0 -> +0, 255 -> +inf).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t code) {
+  return __uint_as_float((code & 0xffu) << 23);
+}
+
+// Two e2m1 nibbles of byte `sel` of `packed` times `scale` into two floats
+// (low nibble first), with the gfx950 scaled fp4 conversion.
+template <int sel>
+__device__ __forceinline__ void fp4x2_to_f32(uint32_t packed, float scale, float& lo, float& hi) {
+  auto v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(packed, scale, sel);
+  lo = v[0];
+  hi = v[1];
+}
+
+// Decode 8 e2m1 values (one dword) with one scale.
+__device__ __forceinline__ void decode8(uint32_t d, float scale, float* w) {
+  fp4x2_to_f32<0>(d, scale, w[0], w[1]);
+  fp4x2_to_f32<1>(d, scale, w[2], w[3]);
+  fp4x2_to_f32<2>(d, scale, w[4], w[5]);
+  fp4x2_to_f32<3>(d, scale, w[6], w[7]);
+}
+
+// 64-lane xor butterfly sum: after it every lane holds the same value, the
+// tree v[l] + v[l^m] for m = 32, 16, 8, 4, 2, 1.
+__device__ __forceinline__ float wave_butterfly_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, kWave);
+  return v;
+}
+
+}  // namespace gxmoe

@@ -1,0 +1,360 @@
+// moe_route.hip -- router GEMV + top-k softmax + device routing plan (gfx950).
+//
+// One launch replaces the reference's router GEMV/GEMM (gemv_bf16.cu:40-130,
+// cuda_utils.h:226-308), topk_softmax_forward (topk_softmax.cu:380-432),
+// moe_permute_classify (moe_permute.cu:129-179) and the host gather map
+// (moe_permute.cu:184-236, moe_layer.cu:1217-1234), with no host round trip:
+//
+//   grid (ceil(E/4), ceil(T/8)), 256 threads.  Work-group (g, tg) computes
+//   the logits of experts 4g..4g+3 for tokens 8tg..8tg+7 with the
+//   gemv_bf16_kernel summation tree.  The last work-group to finish a token
+//   group (atomic ticket) selects the top-k of its tokens; the last token
+//   group to finish builds the plan (histogram, exclusive scan, stable
+//   counting-sort gather map, permuted token list, active expert list).
+//   Tickets are reset by their last holder, so the launch is replayable
+//   (hipGraph) without a memset.
+#include <float.h>
+
+#include "moe_device.h"
+#include "moe_kernels.h"
+
+namespace gxmoe {
+
+namespace {
+
+constexpr int kRouteThreads = 256;
+
+__device__ __forceinline__ float sanitize_logit(float v) {
+  // topk_softmax.cu:47-52: NaN and +-Inf become -FLT_MAX.
+  return ((__float_as_uint(v) & 0x7f800000u) == 0x7f800000u) ? -FLT_MAX : v;
+}
+
+template <bool F32>
+__device__ __forceinline__ float load_logit(const void* row, int e) {
+  if constexpr (F32) return reinterpret_cast<const float*>(row)[e];
+  return bf16_to_f32(reinterpret_cast<const uint16_t*>(row)[e]);
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
+  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(d[i] << 16);
+    f[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+  }
+}
+
+// Top-k of one token by one wave.  Lane l holds experts l, l+64, l+128,
+// l+192.  Each round takes the largest visible logit (> -FLT_MAX) by
+// (value desc, index asc); a round with nothing visible yields (-FLT_MAX, -1),
+// the reference's padding (topk_softmax.cu:133-159).  Lane 0 then applies the
+// softmax over the k selected values in the order of the reference variant
+// (v1 sequential sum for T <= 8, v2 xor-butterfly sum otherwise).
+template <bool F32>
+__device__ void topk_one_token(const void* row, int E, int k, int variant,
+                               int32_t* out_idx, float* out_w,
+                               int32_t* tokens_per_expert, int lane) {
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    int e = lane + 64 * j;
+    v[j] = (e < E) ? sanitize_logit(load_logit<F32>(row, e)) : -FLT_MAX;
+  }
+  float sel_v[kMaxTopK];
+  int sel_i[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    sel_v[s] = -FLT_MAX;
+    sel_i[s] = -1;
+    if (s < k) {
+      float bv = -FLT_MAX;
+      int bi = -1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        float ov = __shfl_xor(bv, m, kWave);
+        int oi = __shfl_xor(bi, m, kWave);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      sel_v[s] = bv;
+      sel_i[s] = bi;
+      if (bi >= 0 && (bi & 63) == lane) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if ((bi >> 6) == j) v[j] = -FLT_MAX;
+      }
+    }
+  }
+  if (lane != 0) return;
+  if (sel_i[0] == -1) {  // topk_softmax.cu:339-346: no finite logit at all
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s)
+      if (s < k) { out_idx[s] = s; out_w[s] = 1.0f / static_cast<float>(k); }
+    if (tokens_per_expert)
+      for (int s = 0; s < k; ++s) atomicAdd(&tokens_per_expert[s], 1);
+    return;
+  }
+  float mx = -FLT_MAX;
+  float ex[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s)
+    if (s < k && sel_v[s] > mx) mx = sel_v[s];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) ex[s] = (s < k) ? gx_expf(sel_v[s] - mx) : 0.0f;
+  float sum;
+  if (variant == 1) {  // topk_softmax.cu:199-204
+    sum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s)
+      if (s < k) sum = sum + ex[s];
+  } else {  // topk_softmax.cu:358-362, the tree every lane of the butterfly ends with
+    float t[kMaxTopK];
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s) t[s] = ex[s];
+    for (int m = k >> 1; m > 0; m >>= 1) {
+      float u[kMaxTopK];
+#pragma unroll
+      for (int s = 0; s < kMaxTopK; ++s) u[s] = t[s] + t[s ^ m];
+#pragma unroll
+      for (int s = 0; s < kMaxTopK; ++s) t[s] = u[s];
+    }
+    sum = t[0];
+  }
+  float inv = 1.0f / sum;
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    if (s < k) {
+      out_idx[s] = sel_i[s];
+      out_w[s] = (sel_i[s] < 0) ? 0.0f : ex[s] * inv;
+      if (tokens_per_expert && sel_i[s] >= 0) atomicAdd(&tokens_per_expert[sel_i[s]], 1);
+    }
+  }
+}
+
+// Block-wide (256 threads) dispatch plan over the T*k slots of `idx`:
+// counts, exclusive offsets, a gather map that is stable in slot order (the
+// counting sort of moe_permute.cu:184-236), the permuted token list and the
+// ascending list of experts with at least one slot.  Slots with an index
+// outside [0, E) get gather_map = -1 and are not dispatched.
+__device__ void build_plan(const int32_t* __restrict__ idx, int T, int k, int E, PlanBufs p) {
+  __shared__ int s_off[kMaxExperts + 1];
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_run[kMaxExperts];
+  __shared__ int s_wc[4][kMaxExperts];
+  __shared__ unsigned long long s_mask[4];
+  __shared__ int s_wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
+  const int S = T * k;
+
+  s_cnt[tid] = 0;
+  s_run[tid] = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) s_wc[w][tid] = 0;
+  __syncthreads();
+  for (int s = tid; s < S; s += kRouteThreads) {
+    int e = idx[s];
+    if (e >= 0 && e < E) atomicAdd(&s_cnt[e], 1);
+  }
+  __syncthreads();
+
+  // exclusive scan of the counts (E <= 256: one value per thread)
+  const int c = (tid < E) ? s_cnt[tid] : 0;
+  int incl = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) s_wsum[warp] = incl;
+  const bool act = (tid < E) && (c > 0);
+  const unsigned long long am = __ballot(act);
+  if (lane == 0) s_mask[warp] = am;
+  __syncthreads();
+  int base = 0, abase = 0;
+  for (int w = 0; w < warp; ++w) { base += s_wsum[w]; abase += __popcll(s_mask[w]); }
+  const int excl = base + incl - c;
+  if (tid < E) {
+    s_off[tid] = excl;
+    p.counts[tid] = c;
+    p.offsets[tid] = excl;
+  }
+  if (tid == E - 1) { s_off[E] = excl + c; p.offsets[E] = excl + c; }
+  if (act) p.active[abase + __popcll(am & ((1ull << lane) - 1ull))] = tid;
+  if (tid == 0)
+    *p.n_active = __popcll(s_mask[0]) + __popcll(s_mask[1]) + __popcll(s_mask[2]) + __popcll(s_mask[3]);
+  __syncthreads();
+
+  // stable positions, 256 slots per round
+  for (int r0 = 0; r0 < S; r0 += kRouteThreads) {
+    const int s = r0 + tid;
+    const int e = (s < S) ? idx[s] : -1;
+    const bool valid = (e >= 0 && e < E);
+    unsigned long long peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const unsigned long long mb = __ballot(bit);
+      peers &= bit ? mb : ~mb;
+    }
+    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+    if (valid && rank == 0) s_wc[warp][e] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int pos = s_off[e] + s_run[e] + rank;
+      for (int w = 0; w < warp; ++w) pos += s_wc[w][e];
+      p.gather_map[s] = pos;
+      p.perm_token[pos] = s / k;
+    } else if (s < S) {
+      p.gather_map[s] = -1;
+    }
+    __syncthreads();
+    if (tid < E) {
+      s_run[tid] += s_wc[0][tid] + s_wc[1][tid] + s_wc[2][tid] + s_wc[3][tid];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) s_wc[w][tid] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+template <bool F32>
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
+  const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
+  const int e0 = blockIdx.x * kRouteExpertsPerGroup;
+  const int t0 = blockIdx.y * kRouteTokensPerGroup;
+  const int tn = min(kRouteTokensPerGroup, a.T - t0);
+  const int H = a.H, E = a.E;
+  const int KV = H >> 3;
+  __shared__ float red[kRouteTokensPerGroup][kRouteExpertsPerGroup][4];
+  __shared__ uint32_t s_ticket;
+
+  // Logits with the gemv_bf16_kernel tree (gemv_bf16.cu:57-129): thread tid
+  // chains fmaf over 8-element chunks tid, tid+256, ..., then the H%8 tail;
+  // xor butterfly per wave; the 4 wave sums are added in order from 0.
+  for (int tt = 0; tt < tn; ++tt) {
+    const uint16_t* xr = a.x + static_cast<size_t>(t0 + tt) * H;
+    float acc[kRouteExpertsPerGroup] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kv = tid; kv < KV; kv += kRouteThreads) {
+      float xs[8];
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + kv * 8), xs);
+#pragma unroll
+      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) {
+        if (e0 + ee < E) {
+          float ws[8];
+          unpack_bf16x8(*reinterpret_cast<const uint4*>(a.W + static_cast<size_t>(e0 + ee) * H + kv * 8), ws);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[ee] = __builtin_fmaf(xs[i], ws[i], acc[ee]);
+        }
+      }
+    }
+    for (int kk = KV * 8 + tid; kk < H; kk += kRouteThreads) {
+      const float xs = bf16_to_f32(xr[kk]);
+#pragma unroll
+      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee)
+        if (e0 + ee < E)
+          acc[ee] = __builtin_fmaf(xs, bf16_to_f32(a.W[static_cast<size_t>(e0 + ee) * H + kk]), acc[ee]);
+    }
+#pragma unroll
+    for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) acc[ee] = wave_butterfly_sum(acc[ee]);
+    if (lane == 0) {
+#pragma unroll
+      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) red[tt][ee][warp] = acc[ee];
+    }
+  }
+  if (blockIdx.x == 0 && a.xf != nullptr) {
+    const size_t base = static_cast<size_t>(t0) * H;
+    for (int i = tid; i < tn * H; i += kRouteThreads) a.xf[base + i] = bf16_to_f32(a.x[base + i]);
+  }
+  __syncthreads();
+  if (tid < tn * kRouteExpertsPerGroup) {
+    const int tt = tid / kRouteExpertsPerGroup, ee = tid % kRouteExpertsPerGroup, e = e0 + ee;
+    if (e < E) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v = v + red[tt][ee][w];
+      if (a.b != nullptr) v = v + bf16_to_f32(a.b[e]);
+      const size_t o = static_cast<size_t>(t0 + tt) * E + e;
+      if constexpr (F32) reinterpret_cast<float*>(a.logits)[o] = v;
+      else reinterpret_cast<uint16_t*>(a.logits)[o] = f32_to_bf16(v);
+    }
+  }
+
+  // The last expert group of this token group selects the top-k.
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_ticket = atomicAdd(&a.group_counter[blockIdx.y], 1u);
+  __syncthreads();
+  if (s_ticket != gridDim.x - 1) return;
+  __threadfence();
+  if (tid == 0) a.group_counter[blockIdx.y] = 0u;
+  const int variant = (a.T <= 8) ? 1 : 2;  // topk_softmax.cu:399
+  for (int tt = warp; tt < tn; tt += 4) {
+    const int t = t0 + tt;
+    const void* row = F32 ? static_cast<const void*>(reinterpret_cast<const float*>(a.logits) + static_cast<size_t>(t) * E)
+                          : static_cast<const void*>(reinterpret_cast<const uint16_t*>(a.logits) + static_cast<size_t>(t) * E);
+    topk_one_token<F32>(row, E, a.k, variant, a.idx + static_cast<size_t>(t) * a.k,
+                        a.w + static_cast<size_t>(t) * a.k, nullptr, lane);
+  }
+  if (a.plan.counts == nullptr) return;
+
+  // The last token group builds the plan over all T*k slots.
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_ticket = atomicAdd(a.done_counter, 1u);
+  __syncthreads();
+  if (s_ticket != gridDim.y - 1) return;
+  __threadfence();
+  if (tid == 0) *a.done_counter = 0u;
+  build_plan(a.idx, a.T, a.k, E, a.plan);
+}
+
+template <bool F32>
+__global__ __launch_bounds__(kRouteThreads) void topk_kernel(const void* logits, int T, int E, int k,
+                                                            int32_t* idx, float* w, int32_t* tpe) {
+  const int lane = threadIdx.x & 63, warp = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + warp;
+  if (t >= T) return;
+  const void* row = F32 ? static_cast<const void*>(reinterpret_cast<const float*>(logits) + static_cast<size_t>(t) * E)
+                        : static_cast<const void*>(reinterpret_cast<const uint16_t*>(logits) + static_cast<size_t>(t) * E);
+  topk_one_token<F32>(row, E, k, (T <= 8) ? 1 : 2, idx + static_cast<size_t>(t) * k,
+                      w + static_cast<size_t>(t) * k, tpe, lane);
+}
+
+__global__ __launch_bounds__(kRouteThreads) void plan_kernel(const int32_t* idx, int T, int k, int E,
+                                                            PlanBufs p) {
+  build_plan(idx, T, k, E, p);
+}
+
+}  // namespace
+
+hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
+  if (a.T <= 0) return hipSuccess;
+  dim3 grid((a.E + kRouteExpertsPerGroup - 1) / kRouteExpertsPerGroup,
+            (a.T + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup);
+  if (a.logits_fp32)
+    hipLaunchKernelGGL(route_kernel<true>, grid, dim3(kRouteThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(route_kernel<false>, grid, dim3(kRouteThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_topk(const void* logits, int logits_fp32, int T, int E, int k,
+                       int32_t* idx, float* w, int32_t* tpe, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  dim3 grid((T + 3) / 4);
+  if (logits_fp32)
+    hipLaunchKernelGGL(topk_kernel<true>, grid, dim3(kRouteThreads), 0, s, logits, T, E, k, idx, w, tpe);
+  else
+    hipLaunchKernelGGL(topk_kernel<false>, grid, dim3(kRouteThreads), 0, s, logits, T, E, k, idx, w, tpe);
+  return hipGetLastError();
+}
+
+hipError_t launch_plan(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kRouteThreads), 0, s, idx, T, k, E, plan);
+  return hipGetLastError();
+}
+
+}  // namespace gxmoe

@@ -1,0 +1,360 @@
+"""Python host binding of libgptoss_moe.so (the gfx950 GPT-OSS MoE block).
+
+Mirrors the reference's MoE operator interface (src/model/moe_layer.cu:
+1556-1615: moe_layer_create / init / forward / forward_prenormed /
+get_ffn_norm_weight / destroy) and its kernel launchers, over the C ABI
+declared in include/gptoss_moe.h.  Device memory is held in torch tensors
+(plumbing only); every computation runs in the HIP library, and importing
+this module without the built library raises immediately.
+
+bf16 tensors are passed as torch.bfloat16 (or their int16/uint16 bit views).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgptoss_moe.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C hip-kernels_amd)")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+GPTOSS_OK = 0
+GPTOSS_ERR_INVALID = 1
+GPTOSS_ERR_UNSUPPORTED = 2
+GPTOSS_ERR_HIP = 3
+GPTOSS_ERR_STATE = 4
+GPTOSS_ERR_OOM = 5
+
+
+class GptossError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[gptoss_moe status {code}] {msg}")
+        self.code = code
+
+
+class ValueErrorG(GptossError, ValueError):
+    """Invalid argument (status GPTOSS_ERR_INVALID); also a ValueError, as the
+    reference bindings map argument errors to ValueError (bindings.cpp:105-116)."""
+
+
+class MoeConfig(ctypes.Structure):
+    _fields_ = [("hidden_size", _I), ("num_experts", _I), ("top_k", _I), ("intermediate_size", _I),
+                ("swiglu_alpha", _F), ("swiglu_limit", _F), ("rms_norm_eps", _F), ("logits_fp32", _I),
+                ("max_tokens", _I)]
+
+
+class MoeWeights(ctypes.Structure):
+    _fields_ = [("moe_norm_weight", _P), ("router_weight", _P), ("router_bias", _P),
+                ("gate_up_bias", _P), ("down_bias", _P),
+                ("mlp1_packed", ctypes.POINTER(_P)), ("mlp1_scales", ctypes.POINTER(_P)),
+                ("mlp2_packed", ctypes.POINTER(_P)), ("mlp2_scales", ctypes.POINTER(_P)),
+                ("mlp1_tiled_nibbles", _P), ("mlp1_tiled_scales", _P),
+                ("mlp2_tiled_nibbles", _P), ("mlp2_tiled_scales", _P)]
+
+
+class MoeTrace(ctypes.Structure):
+    _fields_ = [("logits", _P), ("expert_indices", _P), ("expert_weights", _P), ("expert_counts", _P),
+                ("expert_offsets", _P), ("gather_map", _P), ("perm_token", _P), ("active_experts", _P),
+                ("n_active", _P), ("gate_up", _P), ("act", _P), ("expert_out", _P)]
+
+
+def _sig(name, args, res=_I):
+    f = getattr(_lib, name)
+    f.argtypes = args
+    f.restype = res
+    return f
+
+
+_sig("gptoss_last_error", [], ctypes.c_char_p)
+_sig("gptoss_abi_version", [])
+_sig("gptoss_moe_config_default", [ctypes.POINTER(MoeConfig), _I, _I])
+_sig("gptoss_mxfp4_tiled_size", [_I, _I, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)])
+_sig("gptoss_mxfp4_pack_tiled", [_P, _P, _I, _I, _P, _P, _P])
+_sig("gptoss_moe_layer_create", [], _P)
+_sig("gptoss_moe_layer_init", [_P, ctypes.POINTER(MoeConfig), _I, ctypes.POINTER(MoeWeights)])
+_sig("gptoss_moe_layer_forward", [_P, _P, _P, _I, _P])
+_sig("gptoss_moe_layer_forward_prenormed", [_P, _P, _P, _P, _I, _P])
+_sig("gptoss_moe_layer_get_ffn_norm_weight", [_P], _P)
+_sig("gptoss_moe_layer_destroy", [_P], None)
+_sig("gptoss_moe_layer_trace", [_P, ctypes.POINTER(MoeTrace)])
+_sig("gptoss_moe_layer_set_trace_gate_up", [_P, _I])
+_sig("gptoss_moe_layer_set_profiling", [_P, _I])
+_sig("gptoss_moe_layer_profile_read", [_P, ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_F),
+                                        ctypes.POINTER(_I)])
+_sig("gptoss_moe_route_scratch_bytes", [_I], _SZ)
+_sig("gptoss_moe_route", [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P])
+_sig("gptoss_topk_softmax_forward", [_P, _I, _P, _P, _P, _I, _I, _I, _P])
+_sig("gptoss_moe_permute_plan", [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P])
+_sig("gptoss_moe_scatter_tokens", [_P, _P, _P, _I, _I, _I, _P])
+_sig("gptoss_mxfp4_gemv_forward", [_P, _I, _P, _P, _P, _P, _I, _I, _P])
+_sig("gptoss_swiglu_forward", [_P, _P, _I, _I, _F, _F, _P])
+_sig("gptoss_moe_combine_forward", [_P, _P, _P, _P, _P, _I, _I, _I, _P])
+_sig("gptoss_mxfp4_dequant", [_P, _P, _I, _I, _P, _P])
+
+lib = _lib
+
+
+def check(rc: int) -> None:
+    if rc != GPTOSS_OK:
+        msg = _lib.gptoss_last_error().decode()
+        if rc == GPTOSS_ERR_INVALID:
+            raise ValueErrorG(rc, msg)
+        raise GptossError(rc, msg)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def default_config(num_experts: int = 128, max_tokens: int = 64, logits_fp32: bool = False) -> MoeConfig:
+    cfg = MoeConfig()
+    check(_lib.gptoss_moe_config_default(ctypes.byref(cfg), num_experts, max_tokens))
+    cfg.logits_fp32 = 1 if logits_fp32 else 0
+    return cfg
+
+
+def tiled_size(N: int, K: int):
+    nb = _SZ()
+    sb = _SZ()
+    check(_lib.gptoss_mxfp4_tiled_size(N, K, ctypes.byref(nb), ctypes.byref(sb)))
+    return nb.value, sb.value
+
+
+def pack_tiled(packed: torch.Tensor, scales: torch.Tensor, N: int, K: int, out_nib=None, out_sc=None, stream=None):
+    """Reference-layout MXFP4 [N][K/2] + [N][K/32] (uint8, device) -> tiled layout."""
+    nb, sb = tiled_size(N, K)
+    if out_nib is None:
+        out_nib = torch.empty(nb, dtype=torch.uint8, device=packed.device)
+    if out_sc is None:
+        out_sc = torch.empty(sb, dtype=torch.uint8, device=packed.device)
+    check(_lib.gptoss_mxfp4_pack_tiled(_ptr(packed), _ptr(scales), N, K, _ptr(out_nib), _ptr(out_sc),
+                                       _stream(stream)))
+    return out_nib, out_sc
+
+
+@dataclass
+class Trace:
+    logits: int
+    expert_indices: int
+    expert_weights: int
+    expert_counts: int
+    expert_offsets: int
+    gather_map: int
+    perm_token: int
+    active_experts: int
+    n_active: int
+    gate_up: int
+    act: int
+    expert_out: int
+
+
+class MoELayer:
+    """gptoss::MoELayer replacement (moe_layer.cu:607-1549) on one GPU.
+
+    init() takes either the reference per-expert MXFP4 tables (lists of device
+    tensors, packed and tiled by the library) or pre-tiled expert-major
+    buffers (borrowed).  Tensors passed to init() must outlive the layer."""
+
+    def __init__(self):
+        self._h = _lib.gptoss_moe_layer_create()
+        if not self._h:
+            raise GptossError(GPTOSS_ERR_OOM, "gptoss_moe_layer_create failed")
+        self._keep = []
+        self.cfg = None
+
+    def init(self, cfg: MoeConfig, device_id: int, router_weight, router_bias=None, gate_up_bias=None,
+             down_bias=None, moe_norm_weight=None, mlp1=None, mlp2=None, tiled=None) -> "MoELayer":
+        """mlp1/mlp2: (list of packed tensors, list of scale tensors) per expert.
+        tiled: (w1_nibbles, w1_scales, w2_nibbles, w2_scales) expert-major buffers."""
+        wt = MoeWeights()
+        wt.moe_norm_weight = _ptr(moe_norm_weight)
+        wt.router_weight = _ptr(router_weight)
+        wt.router_bias = _ptr(router_bias)
+        wt.gate_up_bias = _ptr(gate_up_bias)
+        wt.down_bias = _ptr(down_bias)
+        if tiled is not None:
+            wt.mlp1_tiled_nibbles, wt.mlp1_tiled_scales, wt.mlp2_tiled_nibbles, wt.mlp2_tiled_scales = (
+                _ptr(t) for t in tiled)
+        else:
+            arrs = []
+            for lst in (mlp1[0], mlp1[1], mlp2[0], mlp2[1]):
+                a = (_P * len(lst))(*[_ptr(t) for t in lst])
+                arrs.append(a)
+            self._keep.append(arrs)
+            wt.mlp1_packed = ctypes.cast(arrs[0], ctypes.POINTER(_P))
+            wt.mlp1_scales = ctypes.cast(arrs[1], ctypes.POINTER(_P))
+            wt.mlp2_packed = ctypes.cast(arrs[2], ctypes.POINTER(_P))
+            wt.mlp2_scales = ctypes.cast(arrs[3], ctypes.POINTER(_P))
+        check(_lib.gptoss_moe_layer_init(self._h, ctypes.byref(cfg), device_id, ctypes.byref(wt)))
+        self.cfg = cfg
+        return self
+
+    def forward(self, x, out=None, stream=None):
+        """out = x + MoE(RMSNorm(x)) (moe_layer_forward)."""
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        check(_lib.gptoss_moe_layer_forward(self._h, _ptr(x), _ptr(out), T, _stream(stream)))
+        return out
+
+    def forward_prenormed(self, normed, residual=None, out=None, stream=None):
+        """out = residual + MoE(normed) (moe_layer_forward_prenormed)."""
+        T = normed.shape[0]
+        if out is None:
+            out = torch.empty_like(normed)
+        check(_lib.gptoss_moe_layer_forward_prenormed(self._h, _ptr(normed), _ptr(residual), _ptr(out), T,
+                                                      _stream(stream)))
+        return out
+
+    def get_ffn_norm_weight(self) -> int:
+        return _lib.gptoss_moe_layer_get_ffn_norm_weight(self._h) or 0
+
+    def set_trace_gate_up(self, enable: bool) -> None:
+        check(_lib.gptoss_moe_layer_set_trace_gate_up(self._h, 1 if enable else 0))
+
+    def set_profiling(self, max_forwards: int) -> None:
+        check(_lib.gptoss_moe_layer_set_profiling(self._h, max_forwards))
+
+    def profile_read(self):
+        """(route_ms, w1_ms, w2_ms, n_forwards) summed over the recorded forwards."""
+        r, a, b, n = _F(), _F(), _F(), _I()
+        check(_lib.gptoss_moe_layer_profile_read(self._h, ctypes.byref(r), ctypes.byref(a), ctypes.byref(b),
+                                                 ctypes.byref(n)))
+        return r.value, a.value, b.value, n.value
+
+    def trace(self) -> Trace:
+        t = MoeTrace()
+        check(_lib.gptoss_moe_layer_trace(self._h, ctypes.byref(t)))
+        return Trace(*[getattr(t, f[0]) or 0 for f in MoeTrace._fields_])
+
+    def destroy(self) -> None:
+        if self._h:
+            _lib.gptoss_moe_layer_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+# device buffer readback (for traces, which are raw device pointers)
+# ---------------------------------------------------------------------------
+_hip = None
+
+
+def copy_device_to_tensor(ptr: int, nbytes: int, dtype=torch.uint8, device="cuda") -> torch.Tensor:
+    """Copy `nbytes` at device pointer `ptr` into a new device tensor (hipMemcpy D2D)."""
+    global _hip
+    if _hip is None:
+        # same SONAME as the runtime torch loaded, so this binds to that instance
+        _hip = ctypes.CDLL("libamdhip64.so.7")
+        _hip.hipMemcpy.argtypes = [_P, _P, _SZ, _I]
+        _hip.hipMemcpy.restype = _I
+    out = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if nbytes:
+        rc = _hip.hipMemcpy(out.data_ptr(), ptr, nbytes, 3)  # hipMemcpyDeviceToDevice
+        if rc != 0:
+            raise GptossError(GPTOSS_ERR_HIP, f"hipMemcpy failed ({rc})")
+    return out.view(dtype)
+
+
+# ---------------------------------------------------------------------------
+# stage entry points
+# ---------------------------------------------------------------------------
+def route(x, router_w, router_b, top_k: int, logits_fp32: bool = False, stream=None):
+    T, H = x.shape
+    E = router_w.shape[0]
+    dev = x.device
+    logits = torch.empty((T, E), dtype=torch.float32 if logits_fp32 else torch.bfloat16, device=dev)
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    scratch = torch.zeros(_lib.gptoss_moe_route_scratch_bytes(T), dtype=torch.uint8, device=dev)
+    check(_lib.gptoss_moe_route(_ptr(x), _ptr(router_w), _ptr(router_b), T, E, H, top_k, 1 if logits_fp32 else 0,
+                                _ptr(logits), _ptr(idx), _ptr(w), _ptr(scratch), _stream(stream)))
+    return logits, idx, w
+
+
+def topk_softmax(logits, top_k: int, tokens_per_expert=None, stream=None):
+    T, E = logits.shape
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=logits.device)
+    check(_lib.gptoss_topk_softmax_forward(_ptr(logits), 1 if logits.dtype == torch.float32 else 0, _ptr(idx),
+                                           _ptr(w), _ptr(tokens_per_expert), T, E, top_k, _stream(stream)))
+    return idx, w
+
+
+def permute_plan(idx, num_experts: int, stream=None):
+    T, k = idx.shape
+    dev = idx.device
+    S = T * k
+    counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    gmap = torch.empty(S, dtype=torch.int32, device=dev)
+    ptok = torch.full((S,), -1, dtype=torch.int32, device=dev)
+    active = torch.full((num_experts,), -1, dtype=torch.int32, device=dev)
+    n_active = torch.empty(1, dtype=torch.int32, device=dev)
+    check(_lib.gptoss_moe_permute_plan(_ptr(idx), T, k, num_experts, _ptr(counts), _ptr(offsets), _ptr(gmap),
+                                       _ptr(ptok), _ptr(active), _ptr(n_active), _stream(stream)))
+    return dict(counts=counts, offsets=offsets, gather_map=gmap, perm_token=ptok, active=active, n_active=n_active)
+
+
+def scatter_tokens(x, gather_map, top_k: int, stream=None):
+    T, H = x.shape
+    out = torch.zeros((T * top_k, H), dtype=x.dtype, device=x.device)
+    check(_lib.gptoss_moe_scatter_tokens(_ptr(x), _ptr(gather_map), _ptr(out), T, H, top_k, _stream(stream)))
+    return out
+
+
+def mxfp4_gemv(x, tiled_nib, tiled_sc, bias, N: int, K: int, stream=None):
+    M = x.shape[0]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    check(_lib.gptoss_mxfp4_gemv_forward(_ptr(x), M, _ptr(tiled_nib), _ptr(tiled_sc), _ptr(bias), _ptr(y), N, K,
+                                         _stream(stream)))
+    return y
+
+
+def swiglu(gate_up, alpha: float = 1.702, limit: float = 7.0, stream=None):
+    T, N2 = gate_up.shape
+    out = torch.empty((T, N2 // 2), dtype=gate_up.dtype, device=gate_up.device)
+    check(_lib.gptoss_swiglu_forward(_ptr(gate_up), _ptr(out), T, N2 // 2, alpha, limit, _stream(stream)))
+    return out
+
+
+def combine(expert_out, gather_map, weights, residual, T: int, H: int, top_k: int, stream=None):
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=expert_out.device)
+    check(_lib.gptoss_moe_combine_forward(_ptr(out), _ptr(expert_out), _ptr(gather_map), _ptr(weights),
+                                          _ptr(residual), T, H, top_k, _stream(stream)))
+    return out
+
+
+def dequant(tiled_nib, tiled_sc, N: int, K: int, stream=None):
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=tiled_nib.device)
+    check(_lib.gptoss_mxfp4_dequant(_ptr(tiled_nib), _ptr(tiled_sc), N, K, _ptr(out), _stream(stream)))
+    return out

@@ -1,0 +1,199 @@
+/*
+ * gptoss_moe.h -- C ABI of the MI355X (gfx950) GPT-OSS MoE block.
+ *
+ * Drop-in boundary for the MoE hot path of the reference engine
+ * (Jayluci4/hip-kernels).  Every entry point takes plain pointers and sizes;
+ * device pointers are HIP device memory of the current device, `stream` is
+ * a hipStream_t (NULL = the null stream).  Every call returns a status code
+ * (GPTOSS_OK = 0) and records a message readable with gptoss_last_error() on
+ * the calling thread; nothing aborts the process (the reference aborts on
+ * every HIP error, include/cuda_utils.h:17-35).
+ *
+ * Numerics: fp32 accumulation; bf16 rounding at the reference's points
+ * (logits, gate_up, SwiGLU output, expert output, layer output); expert
+ * indices chosen by (logit desc, index asc) as topk_softmax.cu:60-72.
+ *
+ * bf16 values are passed as uint16_t bit patterns.
+ */
+#ifndef GPTOSS_MOE_H
+#define GPTOSS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GPTOSS_MOE_ABI_VERSION 1
+
+enum {
+  GPTOSS_OK = 0,
+  GPTOSS_ERR_INVALID = 1,      /* bad argument (shape, null pointer, k > 8, ...) */
+  GPTOSS_ERR_UNSUPPORTED = 2,  /* valid but not supported by this build (shape limits) */
+  GPTOSS_ERR_HIP = 3,          /* a HIP runtime call failed */
+  GPTOSS_ERR_STATE = 4,        /* object not initialised / already initialised */
+  GPTOSS_ERR_OOM = 5           /* device allocation failed */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* gptoss_last_error(void);
+int gptoss_abi_version(void);
+
+/* MoE shape and constants.  Replaces the compile-time ModelConfig MoE fields
+ * (include/config.h:20-23, 40-43, 53, 57): E and k are runtime values here, so
+ * the 20B (E=32) and 120B (E=128) shapes run from one library. */
+typedef struct gptoss_moe_config {
+  int hidden_size;        /* H (2880) */
+  int num_experts;        /* E (128 for 120B, 32 for 20B) */
+  int top_k;              /* k (4); 1, 2, 4 or 8 */
+  int intermediate_size;  /* I (2880); gate_up rows = 2I, interleaved gate/up */
+  float swiglu_alpha;     /* 1.702 (config.h:43) */
+  float swiglu_limit;     /* 7.0   (config.h:42) */
+  float rms_norm_eps;     /* 1e-5  (config.h:39), used by forward() only */
+  int logits_fp32;        /* 0: bf16 router logits (reference), 1: fp32 logits */
+  int max_tokens;         /* largest T a forward call may pass (scratch sizing) */
+} gptoss_moe_config;
+
+/* Fill `cfg` with the GPT-OSS constants for `num_experts` experts. */
+int gptoss_moe_config_default(gptoss_moe_config* cfg, int num_experts, int max_tokens);
+
+/* ---- MXFP4 weight layout (src/memory) ----------------------------------
+ * Reference layout of one expert matrix [N rows, K inputs]
+ * (weight_loader.cu:782-842, fused_mxfp4_gemv.cu:13-15): packed [N][K/2]
+ * bytes, low nibble = even k; scales [N][K/32] e8m0 bytes.
+ * The kernels read a tiled layout: per 64-row tile, K/32 blocks of
+ * [64 rows][16 bytes]; scales grouped per (tile, K-part, row). */
+int gptoss_mxfp4_tiled_size(int N, int K, size_t* nibble_bytes, size_t* scale_bytes);
+int gptoss_mxfp4_pack_tiled(const uint8_t* packed, const uint8_t* scales, int N, int K,
+                            uint8_t* tiled_nibbles, uint8_t* tiled_scales, void* stream);
+
+/* ---- Layer object: replaces gptoss::MoELayer and moe_layer_* -------------
+ * (src/model/moe_layer.cu:1556-1615). */
+typedef struct gptoss_moe_layer gptoss_moe_layer;
+
+typedef struct gptoss_moe_weights {
+  const uint16_t* moe_norm_weight;  /* [H] bf16, used by forward() (may be NULL otherwise) */
+  const uint16_t* router_weight;    /* [E][H] bf16 (mlp.router.weight) */
+  const uint16_t* router_bias;      /* [E] bf16 or NULL */
+  const uint16_t* gate_up_bias;     /* [E][2I] bf16 or NULL */
+  const uint16_t* down_bias;        /* [E][H] bf16 or NULL */
+  /* Either: reference-layout experts, host arrays of E device pointers
+   * (MXFP4Weight tables of moe_layer.cu:585-589); the layer packs them into
+   * its own tiled copy at init. */
+  const uint8_t* const* mlp1_packed;  /* [E] -> [2I][H/2] */
+  const uint8_t* const* mlp1_scales;  /* [E] -> [2I][H/32] */
+  const uint8_t* const* mlp2_packed;  /* [E] -> [H][I/2] */
+  const uint8_t* const* mlp2_scales;  /* [E] -> [H][I/32] */
+  /* Or: already tiled, expert-major contiguous buffers (borrowed, not copied):
+   * E x gptoss_mxfp4_tiled_size(2I, H) and E x gptoss_mxfp4_tiled_size(H, I). */
+  const uint8_t* mlp1_tiled_nibbles;
+  const uint8_t* mlp1_tiled_scales;
+  const uint8_t* mlp2_tiled_nibbles;
+  const uint8_t* mlp2_tiled_scales;
+} gptoss_moe_weights;
+
+gptoss_moe_layer* gptoss_moe_layer_create(void);                    /* moe_layer_create */
+int gptoss_moe_layer_init(gptoss_moe_layer* layer, const gptoss_moe_config* cfg, int device_id,
+                          const gptoss_moe_weights* weights);       /* moe_layer_init */
+/* out = input + MoE(RMSNorm(input))  (moe_layer_forward, moe_layer.cu:982-1005) */
+int gptoss_moe_layer_forward(gptoss_moe_layer* layer, const uint16_t* input, uint16_t* output,
+                             int num_tokens, void* stream);
+/* out = residual + MoE(normed)  (moe_layer_forward_prenormed, moe_layer.cu:960-980);
+ * residual may be NULL (out = MoE(normed)). */
+int gptoss_moe_layer_forward_prenormed(gptoss_moe_layer* layer, const uint16_t* normed,
+                                       const uint16_t* residual, uint16_t* output,
+                                       int num_tokens, void* stream);
+const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* layer);
+void gptoss_moe_layer_destroy(gptoss_moe_layer* layer);           /* moe_layer_destroy */
+
+/* Device views of the layer's scratch after the last forward on `stream`
+ * (valid until the next forward): routing and per-slot intermediates in the
+ * permuted (expert-sorted) order.  Any output pointer may be NULL. */
+typedef struct gptoss_moe_trace {
+  const void* logits;         /* [T][E] bf16 or fp32 (cfg.logits_fp32) */
+  const int32_t* expert_indices;  /* [T][k] */
+  const float* expert_weights;    /* [T][k] */
+  const int32_t* expert_counts;   /* [E] */
+  const int32_t* expert_offsets;  /* [E+1] */
+  const int32_t* gather_map;      /* [T*k] slot -> permuted row, -1 if dropped */
+  const int32_t* perm_token;      /* [T*k] permuted row -> token */
+  const int32_t* active_experts;  /* [E] ascending, first n_active valid */
+  const int32_t* n_active;        /* [1] */
+  const uint16_t* gate_up;        /* [T*k][2I] bf16 (only if trace_gate_up was enabled) */
+  const float* act;               /* [T*k][I] SwiGLU output (bf16 values held in fp32) */
+  const uint16_t* expert_out;     /* [T*k][H] bf16 */
+} gptoss_moe_trace;
+int gptoss_moe_layer_trace(const gptoss_moe_layer* layer, gptoss_moe_trace* trace);
+/* Also write the bf16 gate_up intermediate on the next forwards (debug). */
+int gptoss_moe_layer_set_trace_gate_up(gptoss_moe_layer* layer, int enable);
+
+/* Per-launch timing, the role of the reference's PROF regions
+ * (include/profiler.h:20-30, src/engine/profiler.cu:106-360): with
+ * max_forwards > 0 the next max_forwards forwards record HIP events on their
+ * stream around the route, W1 and W2 launches.  profile_read waits for them
+ * and returns the summed milliseconds per launch and the count of recorded
+ * forwards.  Forwards captured in a hipGraph record the same events again on
+ * every replay, so profile_read after a replay reads that replay.  Calling
+ * set_profiling again re-arms; max_forwards = 0 turns recording off. */
+int gptoss_moe_layer_set_profiling(gptoss_moe_layer* layer, int max_forwards);
+int gptoss_moe_layer_profile_read(gptoss_moe_layer* layer, float* route_ms, float* w1_ms,
+                                  float* w2_ms, int* n_forwards);
+
+/* ---- Stage entry points (the reference's kernel launchers) --------------- */
+
+/* Router + top-k softmax in one launch: replaces gemv_bf16_forward (T == 1,
+ * gemv_bf16.cu:236-247) / gemm_bf16_lt (T > 1, cuda_utils.h:226-308) plus
+ * topk_softmax_forward (topk_softmax.cu:380).  logits: [T][E] bf16 if
+ * logits_fp32 == 0 else fp32.  Needs a scratch of gptoss_moe_route_scratch_bytes(T)
+ * zero-filled bytes that the call leaves zero-filled again. */
+size_t gptoss_moe_route_scratch_bytes(int num_tokens);
+int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
+                     int num_tokens, int num_experts, int hidden, int top_k, int logits_fp32,
+                     void* logits, int32_t* expert_indices, float* expert_weights,
+                     void* scratch, void* stream);
+
+/* topk_softmax_forward (topk_softmax.cu:380-432) on given logits; bf16 logits
+ * unless logits_fp32.  tokens_per_expert may be NULL (atomic histogram). */
+int gptoss_topk_softmax_forward(const void* logits, int logits_fp32, int32_t* expert_indices,
+                                float* expert_weights, int32_t* tokens_per_expert,
+                                int num_tokens, int num_experts, int top_k, void* stream);
+
+/* moe_permute_classify + moe_compute_gather_map_cpu (moe_permute.cu:129-236)
+ * on the device: per-expert counts, offsets[E+1], stable gather map,
+ * permuted token list, active expert list and its length. */
+int gptoss_moe_permute_plan(const int32_t* expert_indices, int num_tokens, int top_k,
+                            int num_experts, int32_t* counts, int32_t* offsets,
+                            int32_t* gather_map, int32_t* perm_token, int32_t* active_experts,
+                            int32_t* n_active, void* stream);
+
+/* moe_scatter_tokens (moe_permute.cu:241-259): permuted[gather_map[s]] = x[s/k]. */
+int gptoss_moe_scatter_tokens(const uint16_t* x, const int32_t* gather_map, uint16_t* permuted,
+                              int num_tokens, int hidden, int top_k, void* stream);
+
+/* fused_mxfp4_gemv_forward (fused_mxfp4_gemv.cu:452-464) generalised to M rows:
+ * y[m][n] = bf16(sum_k x[m][k] * W[n][k] + bias[n]) with W in the tiled layout. */
+int gptoss_mxfp4_gemv_forward(const uint16_t* x, int M, const uint8_t* tiled_nibbles,
+                              const uint8_t* tiled_scales, const uint16_t* bias, uint16_t* y,
+                              int N, int K, void* stream);
+
+/* swiglu_forward (swiglu.cu:178-211): interleaved [T][2I] -> [T][I]. */
+int gptoss_swiglu_forward(const uint16_t* gate_up, uint16_t* out, int num_tokens,
+                          int intermediate, float alpha, float limit, void* stream);
+
+/* moe_combine_forward (moe_combine.cu:175-204), single GPU (no remote rows):
+ * out[t] = bf16(sum_k w[t,k] * expert_out[gather_map[t,k]] + residual[t]). */
+int gptoss_moe_combine_forward(uint16_t* out, const uint16_t* expert_out,
+                               const int32_t* gather_map, const float* expert_weights,
+                               const uint16_t* residual, int num_tokens, int hidden,
+                               int top_k, void* stream);
+
+/* mxfp4_dequant_batched (mxfp4_dequant.cu:353-375) for one tiled matrix:
+ * out[n][k] = bf16(e2m1 * 2^(scale-127)), row-major [N][K]. */
+int gptoss_mxfp4_dequant(const uint8_t* tiled_nibbles, const uint8_t* tiled_scales, int N, int K,
+                         uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GPTOSS_MOE_H */

@@ -1,0 +1,109 @@
+"""CPU tests of the C ABI library (no GPU needed): it loads, exports every
+function declared in include/gptoss_moe.h, and rejects bad arguments with a
+status code and a message instead of aborting (the reference aborts,
+include/cuda_utils.h:17-35).  None of these calls reaches a kernel launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gptoss_moe.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gptoss_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def g():
+    import gptoss_moe
+    return gptoss_moe
+
+
+def test_exports_every_declared_symbol(g):
+    names = declared_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(g.lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version_and_defaults(g):
+    assert g.lib.gptoss_abi_version() == 1
+    cfg = g.default_config(128, 64)
+    assert (cfg.hidden_size, cfg.num_experts, cfg.top_k, cfg.intermediate_size) == (2880, 128, 4, 2880)
+    assert abs(cfg.swiglu_alpha - 1.702) < 1e-6 and cfg.swiglu_limit == 7.0
+    assert g.lib.gptoss_moe_config_default(None, 128, 1) == g.GPTOSS_ERR_INVALID
+    assert b"NULL" in g.lib.gptoss_last_error()
+
+
+def test_tiled_size_and_shape_errors(g):
+    nb, sb = g.tiled_size(5760, 2880)
+    assert nb == 5760 * 1440                     # nibbles are only permuted
+    assert sb == 90 * 6 * 64 * 16                # 15 scales per (tile, part, row), padded to 16
+    nb, sb = g.tiled_size(2880, 2880)
+    assert nb == 2880 * 1440 and sb == 45 * 6 * 64 * 16
+    with pytest.raises(ValueError):
+        g.tiled_size(64, 33)                     # K not a multiple of the MXFP4 block
+    with pytest.raises(g.GptossError) as e:
+        g.tiled_size(63, 64)
+    assert e.value.code == g.GPTOSS_ERR_UNSUPPORTED
+
+
+def test_layer_state_errors(g):
+    L = g.MoELayer()
+    with pytest.raises(g.GptossError) as e:
+        L.forward_prenormed(_FakeT(1), None, out=_FakeT(1))
+    assert e.value.code == g.GPTOSS_ERR_STATE
+    cfg = g.default_config(128, 8)
+    cfg.top_k = 3
+    with pytest.raises(ValueError, match="top_k"):
+        L.init(cfg, 0, router_weight=_FakeT(1), mlp1=([], []), mlp2=([], []))
+    cfg = g.default_config(300, 8)
+    with pytest.raises(g.GptossError) as e:
+        L.init(cfg, 0, router_weight=_FakeT(1), mlp1=([], []), mlp2=([], []))
+    assert e.value.code == g.GPTOSS_ERR_UNSUPPORTED
+    cfg = g.default_config(128, 0)
+    with pytest.raises(ValueError, match="max_tokens"):
+        L.init(cfg, 0, router_weight=_FakeT(1), mlp1=([], []), mlp2=([], []))
+    cfg = g.default_config(128, 8)
+    with pytest.raises(ValueError, match="router_weight"):
+        L.init(cfg, 0, router_weight=None, mlp1=([], []), mlp2=([], []))
+    with pytest.raises(ValueError, match="aligned"):
+        L.init(cfg, 0, router_weight=_FakeT(2), mlp1=([], []), mlp2=([], []))
+    L.destroy()
+
+
+def test_stage_argument_errors(g):
+    lib = g.lib
+    assert lib.gptoss_moe_route(None, None, None, 0, 128, 2880, 4, 0, None, None, None, None, None) == g.GPTOSS_OK
+    assert lib.gptoss_moe_route(None, None, None, 4, 128, 2880, 3, 0, None, None, None, None, None) == \
+        g.GPTOSS_ERR_INVALID
+    assert b"top_k" in lib.gptoss_last_error()
+    assert lib.gptoss_moe_route(None, None, None, 4, 128, 2881, 4, 0, None, None, None, None, None) == \
+        g.GPTOSS_ERR_INVALID
+    assert lib.gptoss_topk_softmax_forward(None, 0, None, None, None, 4, 128, 9, None) == g.GPTOSS_ERR_INVALID
+    assert lib.gptoss_moe_permute_plan(None, 4, 4, 999, None, None, None, None, None, None, None) == \
+        g.GPTOSS_ERR_UNSUPPORTED
+    assert lib.gptoss_mxfp4_gemv_forward(None, 1, None, None, None, None, 64, 48, None) == g.GPTOSS_ERR_INVALID
+    assert lib.gptoss_swiglu_forward(None, None, -1, 4, 1.702, 7.0, None) == g.GPTOSS_ERR_INVALID
+    assert lib.gptoss_moe_combine_forward(None, None, None, None, None, 2, 64, 9, None) == g.GPTOSS_ERR_INVALID
+    assert lib.gptoss_mxfp4_dequant(None, None, 64, 64, None, None) == g.GPTOSS_ERR_INVALID
+    assert lib.gptoss_moe_route_scratch_bytes(4096) >= (4096 // 8 + 1) * 4
+
+
+class _FakeT:
+    """Stand-in with a data_ptr() for argument-validation tests (never dereferenced)."""
+
+    def __init__(self, addr):
+        self._a = addr * 4096 + (0 if addr % 2 else 8)
+
+    def data_ptr(self):
+        return self._a
+
+    @property
+    def shape(self):
+        return (1, 2880)

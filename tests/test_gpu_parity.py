@@ -1,0 +1,390 @@
+"""GPU parity tests: the HIP library (through its C ABI) against the CPU oracle.
+
+Tolerance: outputs within max-abs 2e-2 and mean-rel
+1e-3 of the reference on bf16 outputs, expert indices bit-exact.  The kernels
+follow the oracle's summation order, so every comparison below first asserts
+the strict result -- bit-identical bf16 / fp32 / int32 -- and the north-star
+tolerance is therefore met with margin zero.  Inputs are seeded synthetic
+data with the BASELINE distributions (tests/moe_data.py).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import moe_data
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS_TOL = 2e-2
+MEAN_REL_TOL = 1e-3
+
+
+def say(*a):
+    print("[gpu-test]", *a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+    return torch
+
+
+def dev(a, torch):
+    """numpy -> device tensor (uint16 arrays become bfloat16)."""
+    if a is None:
+        return None
+    if a.dtype == np.uint16:
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def assert_bf16_parity(got, ref, what):
+    c = moe_data.compare_bf16(got, ref)
+    say(what, c)
+    assert c["max_abs"] <= MAX_ABS_TOL and c["mean_rel"] <= MEAN_REL_TOL, (what, c)
+    assert c["mismatches"] == 0, (what, c)
+
+
+# ---------------------------------------------------------------------------
+# building blocks
+# ---------------------------------------------------------------------------
+def test_pack_and_dequant_all_codes_and_scales(gpu, orc, torch_mod):
+    """Every e2m1 code times every e8m0 scale code (incl. 0 -> +-0, 255 -> inf
+    and fp32-denormal products) through the gfx950 scaled fp4 conversion."""
+    torch = torch_mod
+    N, K = 256, 32
+    packed = np.zeros((N, 16), np.uint8)
+    packed[:, :8] = np.array([0x10, 0x32, 0x54, 0x76, 0x98, 0xBA, 0xDC, 0xFE], np.uint8)
+    packed[:, 8:] = np.arange(8 * N, dtype=np.uint32).reshape(N, 8).astype(np.uint8)
+    scales = np.arange(256, dtype=np.uint8).reshape(N, 1)
+    nib, sc = gpu.pack_tiled(dev(packed, torch), dev(scales, torch), N, K)
+    out = host(gpu.dequant(nib, sc, N, K))
+    ref = orc.mxfp4_dequant(packed, scales, N, K)
+    bad = np.argwhere(out != ref)
+    say("dequant mismatches", len(bad), bad[:8].tolist())
+    assert len(bad) == 0
+
+
+def test_swiglu_grid(gpu, orc, torch_mod):
+    torch = torch_mod
+    g = np.linspace(-40, 40, 2001, dtype=np.float32)
+    u = np.linspace(-12, 12, 97, dtype=np.float32)
+    G, U = np.meshgrid(g, u, indexing="ij")
+    gu = np.stack([G.reshape(-1), U.reshape(-1)], axis=1).reshape(97, -1)  # rows of interleaved pairs
+    gu = moe_data.bf16(gu)
+    extra = moe_data.bf16(np.array([[np.inf, 0, -np.inf, 0, 7.0, 7.0, -7.0, -7.0, 1e-30, 3.0, -88.0, 1.0]], np.float32))
+    for arr in (gu, extra):
+        I = arr.shape[1] // 2
+        out = host(gpu.swiglu(dev(arr, torch)))
+        ref = orc.swiglu_rows(arr, I)
+        assert np.array_equal(out, ref), np.argwhere(out != ref)[:8]
+
+
+def _crafted_logits(T, E, seed):
+    rng = np.random.default_rng(seed)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    q = T // 3
+    lg[:q] = np.round(lg[:q] * 4) / 4             # exact ties
+    if T > 6:
+        lg[q, :] = np.nan                          # degenerate token
+        lg[q + 1, ::5] = np.inf
+        lg[q + 2, :] = -np.inf
+        lg[q + 2, :3] = 0.5                        # only three visible
+        lg[q + 3, ::2] = -0.0
+        lg[q + 3, 1::2] = 0.0                      # +-0 ties
+    return lg
+
+
+@pytest.mark.parametrize("T", [1, 5, 8, 9, 300])
+@pytest.mark.parametrize("k", [1, 2, 4, 8])
+@pytest.mark.parametrize("fp32", [False, True])
+def test_topk_softmax(gpu, orc, torch_mod, T, k, fp32):
+    torch = torch_mod
+    E = 128
+    lg = _crafted_logits(T, E, 100 + T + k)
+    if fp32:
+        logits_np, lf = lg, lg
+        logits = dev(lg, torch)
+    else:
+        logits_np = moe_data.bf16(lg)
+        lf = orc.bf16_to_f32(logits_np)
+        logits = dev(logits_np, torch)
+    tpe = torch.zeros(E, dtype=torch.int32, device="cuda")
+    idx, w = gpu.topk_softmax(logits, k, tokens_per_expert=tpe)
+    ridx, rw = orc.topk_softmax(lf, k)
+    assert np.array_equal(host(idx), ridx)
+    assert np.array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+    hist = np.bincount(ridx[ridx >= 0], minlength=E)
+    assert np.array_equal(host(tpe), hist)
+
+
+@pytest.mark.parametrize("T,fp32", [(1, False), (8, False), (64, False), (9, True), (4096, True)])
+def test_route_router_topk(gpu, orc, torch_mod, T, fp32):
+    """Router GEMV (gemv_bf16 tree) + top-k in one launch; T=4096 fp32 is
+    logits bit-exact, indices bit-exact, weights bit-exact."""
+    torch = torch_mod
+    E, H, k = 128, 2880, 4
+    rng = np.random.default_rng(T)
+    x = moe_data.bf16(rng.normal(0, 1, (T, H)))
+    W = moe_data.bf16(rng.normal(0, 0.02, (E, H)))
+    b = moe_data.bf16(rng.normal(0, 0.02, E))
+    say("route", T, fp32)
+    logits, idx, w = gpu.route(dev(x, torch), dev(W, torch), dev(b, torch), k, logits_fp32=fp32)
+    ref_l = orc.router(x, W, b, logits_fp32=fp32)
+    got_l = host(logits)
+    if fp32:
+        assert np.array_equal(got_l.view(np.uint32), ref_l.view(np.uint32))
+        lf = ref_l
+    else:
+        assert np.array_equal(got_l, ref_l)
+        lf = orc.bf16_to_f32(ref_l)
+    ridx, rw = orc.topk_softmax(lf, k)
+    assert np.array_equal(host(idx), ridx)
+    assert np.array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+    # repeat: the launch's tickets reset themselves
+    logits2, idx2, w2 = gpu.route(dev(x, torch), dev(W, torch), dev(b, torch), k, logits_fp32=fp32)
+    assert np.array_equal(host(idx2), ridx)
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 4, 128), (64, 4, 128), (4096, 4, 128), (33, 2, 8), (7, 8, 32)])
+def test_permute_plan(gpu, orc, torch_mod, T, k, E):
+    torch = torch_mod
+    rng = np.random.default_rng(T + E)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    if T > 8:
+        idx[::9, -1] = -1
+    p = gpu.permute_plan(dev(idx, torch), E)
+    r = orc.plan(idx, E)
+    for n in ("counts", "offsets", "gather_map"):
+        assert np.array_equal(host(p[n]), r[n]), n
+    nv = int((idx >= 0).sum())
+    assert np.array_equal(host(p["perm_token"])[:nv], r["perm_token"][:nv])
+    n = int(host(p["n_active"])[0])
+    assert n == r["n_active"] and np.array_equal(host(p["active"])[:n], r["active"])
+    # scatter of the reference (moe_permute.cu:84-124) from the same map
+    H = 64
+    x = moe_data.bf16(rng.normal(0, 1, (T, H)))
+    perm = host(gpu.scatter_tokens(dev(x, torch), p["gather_map"], k))
+    gm = r["gather_map"]
+    for s in range(T * k):
+        if gm[s] >= 0:
+            assert np.array_equal(perm[gm[s]], x[s // k])
+
+
+@pytest.mark.parametrize("N,K,M", [(5760, 2880, 1), (2880, 2880, 9), (128, 64, 3), (64, 96, 17), (192, 192, 8)])
+def test_dense_mxfp4_gemv(gpu, orc, torch_mod, N, K, M):
+    torch = torch_mod
+    rng = np.random.default_rng(N * 7 + K + M)
+    x = moe_data.bf16(rng.normal(0, 1, (M, K)))
+    packed = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    scales = rng.integers(119, 124, (N, K // 32), dtype=np.uint8)
+    bias = moe_data.bf16(rng.normal(0, 0.5, N))
+    nib, sc = gpu.pack_tiled(dev(packed, torch), dev(scales, torch), N, K)
+    y = host(gpu.mxfp4_gemv(dev(x, torch), nib, sc, dev(bias, torch), N, K))
+    ref = orc.mxfp4_gemv(x, packed, scales, bias, N, K)
+    assert_bf16_parity(y, ref, f"gemv {N}x{K} M={M}")
+
+
+def test_combine(gpu, orc, torch_mod):
+    torch = torch_mod
+    rng = np.random.default_rng(9)
+    T, k, H = 37, 4, 2880
+    y = moe_data.bf16(rng.normal(0, 40, (T * k, H)))
+    res = moe_data.bf16(rng.normal(0, 1, (T, H)))
+    gm = rng.permutation(T * k).astype(np.int32)
+    gm[::11] = -1
+    w = rng.dirichlet(np.ones(k), T).astype(np.float32)
+    out = host(gpu.combine(dev(y, torch), dev(gm, torch), dev(w, torch), dev(res, torch), T, H, k))
+    assert np.array_equal(out, orc.combine(y, gm, w, res, T, k, H))
+    out = host(gpu.combine(dev(y, torch), dev(gm, torch), dev(w, torch), None, T, H, k))
+    assert np.array_equal(out, orc.combine(y, gm, w, None, T, k, H))
+
+
+# ---------------------------------------------------------------------------
+# the fused layer
+# ---------------------------------------------------------------------------
+class DeviceLayer:
+    def __init__(self, gpu, torch, w, E, k, H, I, max_tokens, norm_w=None, via_tables=True):
+        self.torch = torch
+        self.t = {n: dev(w[n], torch) for n in w if w[n] is not None}
+        cfg = gpu.default_config(E, max_tokens)
+        cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, k
+        self.norm = dev(norm_w, torch) if norm_w is not None else None
+        self.layer = gpu.MoELayer()
+        if via_tables:
+            mlp1 = ([self.t["w1_packed"][e] for e in range(E)], [self.t["w1_scales"][e] for e in range(E)])
+            mlp2 = ([self.t["w2_packed"][e] for e in range(E)], [self.t["w2_scales"][e] for e in range(E)])
+            self.layer.init(cfg, 0, self.t["router_w"], self.t.get("router_b"), self.t.get("w1_bias"),
+                            self.t.get("w2_bias"), moe_norm_weight=self.norm, mlp1=mlp1, mlp2=mlp2)
+        else:
+            n1, s1 = gpu.tiled_size(2 * I, H)
+            n2, s2 = gpu.tiled_size(H, I)
+            tiled = [torch.empty(E * n, dtype=torch.uint8, device="cuda") for n in (n1, s1, n2, s2)]
+            for e in range(E):
+                gpu.pack_tiled(self.t["w1_packed"][e], self.t["w1_scales"][e], 2 * I, H,
+                               tiled[0][e * n1:(e + 1) * n1], tiled[1][e * s1:(e + 1) * s1])
+                gpu.pack_tiled(self.t["w2_packed"][e], self.t["w2_scales"][e], H, I,
+                               tiled[2][e * n2:(e + 1) * n2], tiled[3][e * s2:(e + 1) * s2])
+            self.tiled = tiled
+            self.layer.init(cfg, 0, self.t["router_w"], self.t.get("router_b"), self.t.get("w1_bias"),
+                            self.t.get("w2_bias"), moe_norm_weight=self.norm, tiled=tiled)
+
+
+def _trace_arrays(gpu, layer, T, k, E, H, I, torch, with_gate_up):
+    tr = layer.trace()
+    S = T * k
+    rd = lambda p, n, dt: gpu.copy_device_to_tensor(p, n * np.dtype(dt).itemsize).cpu().numpy().view(dt)  # noqa
+    out = dict(idx=rd(tr.expert_indices, S, np.int32).reshape(T, k), w=rd(tr.expert_weights, S, np.float32).reshape(T, k),
+               gather_map=rd(tr.gather_map, S, np.int32), act=rd(tr.act, S * I, np.float32).reshape(S, I),
+               y=rd(tr.expert_out, S * H, np.uint16).reshape(S, H))
+    if with_gate_up:
+        out["gate_up"] = rd(tr.gate_up, S * 2 * I, np.uint16).reshape(S, 2 * I)
+    return out
+
+
+@pytest.mark.parametrize("T", [1, 5, 8, 9, 40])
+@pytest.mark.parametrize("bias", ["random", "none"])
+def test_layer_small_with_intermediates(gpu, orc, torch_mod, T, bias):
+    torch = torch_mod
+    E, k, H, I = 8, 2, 128, 128
+    w = moe_data.make_layer(20 + T, E, H, I, bias=bias)
+    x, res = moe_data.make_tokens(20 + T, T, H)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=64)
+    L.layer.set_trace_gate_up(True)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    torch.cuda.synchronize()
+    ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    got = _trace_arrays(gpu, L.layer, T, k, E, H, I, torch, True)
+    assert np.array_equal(got["idx"], tr["idx"])
+    assert np.array_equal(got["w"].view(np.uint32), tr["w"].view(np.uint32))
+    assert np.array_equal(got["gather_map"], tr["gather_map"])
+    assert np.array_equal(got["gate_up"], tr["gate_up"])
+    assert np.array_equal(orc.f32_to_bf16(got["act"]), tr["act"])
+    assert np.array_equal(got["y"], tr["y"])
+    assert_bf16_parity(out, ref, f"layer small T={T} bias={bias}")
+
+
+def test_layer_golden_fixture(gpu, torch_mod):
+    """The committed fixture (tests/golden/moe_tiny.npz) reproduced on the GPU."""
+    torch = torch_mod
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "moe_tiny.npz"))
+    E, k, H, I = (int(v) for v in d["shape"])
+    w = {n: d[n] for n in ("router_w", "router_b", "w1_packed", "w1_scales", "w1_bias", "w2_packed",
+                           "w2_scales", "w2_bias")}
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=8, via_tables=False)
+    out = host(L.layer.forward_prenormed(dev(d["x"], torch), dev(d["residual"], torch)))
+    assert_bf16_parity(out, d["out"], "golden fixture")
+
+
+def test_layer_forward_with_rmsnorm(gpu, orc, torch_mod):
+    torch = torch_mod
+    E, k, H, I, T = 16, 4, 192, 128, 11
+    w = moe_data.make_layer(31, E, H, I)
+    x, _ = moe_data.make_tokens(31, T, H)
+    norm_w = moe_data.bf16(np.random.default_rng(31).normal(1.0, 0.1, H))
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=16, norm_w=norm_w)
+    out = host(L.layer.forward(dev(x, torch)))
+    normed = orc.rmsnorm(x, norm_w)
+    ref = orc.moe_forward(w, normed, x, E, k, H, I)
+    assert_bf16_parity(out, ref, "forward (rmsnorm + moe)")
+
+
+def test_layer_edge_cases(gpu, orc, torch_mod):
+    torch = torch_mod
+    E, k, H, I = 8, 8, 64, 64
+    w = moe_data.make_layer(41, E, H, I)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=4)
+    x, res = moe_data.make_tokens(41, 4, H)
+    # T = 0 is a no-op; T above max_tokens is rejected
+    L.layer.forward_prenormed(dev(x, torch)[:0], None, out=torch.empty((0, H), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError):
+        L.layer.forward_prenormed(dev(moe_data.make_tokens(1, 5, H)[0], torch), None)
+    # k == E: every expert active for every token; residual NULL
+    out = host(L.layer.forward_prenormed(dev(x, torch), None))
+    ref = orc.moe_forward(w, x, None, E, k, H, I)
+    assert_bf16_parity(out, ref, "k == E, no residual")
+
+
+def test_layer_graph_replay(gpu, orc, torch_mod):
+    """A forward captured in a HIP graph, replayed with new inputs, matches
+    eager results bit for bit on every replay (no memset in the captured work)."""
+    torch = torch_mod
+    E, k, H, I, T = 16, 4, 128, 128, 8
+    w = moe_data.make_layer(51, E, H, I)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T)
+    xs = [moe_data.make_tokens(60 + i, T, H) for i in range(4)]
+    eager = []
+    for x, res in xs:
+        eager.append(host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch))))
+    sx = dev(xs[0][0], torch)
+    sr = dev(xs[0][1], torch)
+    so = torch.empty_like(sx)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        L.layer.forward_prenormed(sx, sr, out=so)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        L.layer.forward_prenormed(sx, sr, out=so)
+    for rep in range(3):
+        for i, (x, res) in enumerate(xs):
+            sx.copy_(dev(x, torch))
+            sr.copy_(dev(res, torch))
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(host(so), eager[i]), (rep, i)
+    assert np.array_equal(eager[1], orc.moe_forward(w, xs[1][0], xs[1][1], E, k, H, I))
+
+
+# ---------------------------------------------------------------------------
+# GPT-OSS shapes (BASELINE configs 0 and 2)
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def gptoss120(gpu, torch_mod):
+    say("building GPT-OSS-120B-shaped layer (E=128, H=I=2880)")
+    E, k, H, I = 128, 4, 2880, 2880
+    w = moe_data.make_layer(1234, E, H, I, bias="zero")
+    L = DeviceLayer(gpu, torch_mod, w, E, k, H, I, max_tokens=64, via_tables=True)
+    torch_mod.cuda.synchronize()
+    return w, L
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 64])
+def test_gptoss120b_decode_parity(gpu, orc, torch_mod, gptoss120, T):
+    torch = torch_mod
+    w, L = gptoss120
+    E, k, H, I = 128, 4, 2880, 2880
+    x, res = moe_data.make_tokens(500 + T, T, H)
+    say("120B decode T", T)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    got = _trace_arrays(gpu, L.layer, T, k, E, H, I, torch, False)
+    assert np.array_equal(got["idx"], tr["idx"])
+    assert np.array_equal(got["w"].view(np.uint32), tr["w"].view(np.uint32))
+    assert np.array_equal(got["y"], tr["y"])
+    assert_bf16_parity(out, ref, f"120B decode T={T}")
+    out2 = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    assert np.array_equal(out, out2)  # run-to-run deterministic
+
+
+def test_gptoss20b_decode_parity(gpu, orc, torch_mod):
+    """BASELINE config 0 shape: E=32, k=4, H=I=2880, T=1, zero (non-null) biases."""
+    torch = torch_mod
+    E, k, H, I, T = 32, 4, 2880, 2880, 1
+    w = moe_data.make_layer(77, E, H, I, bias="zero")
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=1, via_tables=False)
+    x, res = moe_data.make_tokens(77, T, H)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    ref = orc.moe_forward(w, x, res, E, k, H, I)
+    assert_bf16_parity(out, ref, "20B decode T=1")
