@@ -78,12 +78,24 @@ __device__ __forceinline__ void fp4x2_to_f32(uint32_t packed, float scale, float
   hi = v[1];
 }
 
-// Decode 8 e2m1 values (one dword) with one scale.
-__device__ __forceinline__ void decode8(uint32_t d, float scale, float* w) {
-  fp4x2_to_f32<0>(d, scale, w[0], w[1]);
-  fp4x2_to_f32<1>(d, scale, w[2], w[3]);
-  fp4x2_to_f32<2>(d, scale, w[4], w[5]);
-  fp4x2_to_f32<3>(d, scale, w[6], w[7]);
+// Decode 8 e2m1 values (one dword, low nibble first) with the e8m0 scale
+// `code`.  For codes 1..254 the gfx950 scaled conversion returns
+// e2m1 * 2^(code-127) exactly (denormal results included).  Codes 0 and 255
+// are decoded as the reference's register path does (code << 23 as the
+// scale: +0 and +inf, fused_mxfp4_gemv.cu:42-45): the conversion runs with
+// scale 1 (exact e2m1 values) and the IEEE product with the scale follows.
+__device__ __forceinline__ void decode8(uint32_t d, uint32_t code, float* w) {
+  const float scale = e8m0_to_f32(code);
+  const bool special = ((code & 0xffu) - 1u) >= 254u;
+  const float cs = special ? 1.0f : scale;
+  fp4x2_to_f32<0>(d, cs, w[0], w[1]);
+  fp4x2_to_f32<1>(d, cs, w[2], w[3]);
+  fp4x2_to_f32<2>(d, cs, w[4], w[5]);
+  fp4x2_to_f32<3>(d, cs, w[6], w[7]);
+  if (__builtin_expect(special, 0)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = w[j] * scale;
+  }
 }
 
 // 64-lane xor butterfly sum: after it every lane holds the same value, the

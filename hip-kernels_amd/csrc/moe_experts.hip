@@ -63,11 +63,11 @@ __device__ __forceinline__ void part_dot(const u32x4 (&nib)[kMaxBpp], const uint
 #pragma unroll
   for (int i = 0; i < kMaxBpp; ++i) {
     if (i < bpp) {
-      const float scale = e8m0_to_f32(sc[i >> 2] >> (8 * (i & 3)));
+      const uint32_t code = (sc[i >> 2] >> (8 * (i & 3))) & 0xffu;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         float wf[8];
-        decode8(nib[i][d], scale, wf);
+        decode8(nib[i][d], code, wf);
 #pragma unroll
         for (int m = 0; m < kTokChunk; ++m) {
           if (m < mc) {
@@ -97,7 +97,7 @@ __device__ __forceinline__ void load_part(const uint8_t* __restrict__ nib_base, 
     if (q * 4 < g.bpp) sc[q] = s32[q];
 }
 
-__global__ __launch_bounds__(kTileRows * kMaxParts) __attribute__((amdgpu_waves_per_eu(4))) void w1_kernel(
+__global__ __launch_bounds__(kTileRows * kMaxParts) __attribute__((amdgpu_waves_per_eu(3))) void w1_kernel(
     const float* __restrict__ xf, const uint8_t* __restrict__ w1n, const uint8_t* __restrict__ w1s,
     const uint16_t* __restrict__ b1, const int32_t* __restrict__ n_active_p, const int32_t* __restrict__ active,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_token, float* __restrict__ act,
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kTileRows * kMaxParts) __attribute__((amdgpu_waves_
   }
 }
 
-__global__ __launch_bounds__(kTileRows * kMaxParts) __attribute__((amdgpu_waves_per_eu(4))) void w2_kernel(
+__global__ __launch_bounds__(kTileRows * kMaxParts) __attribute__((amdgpu_waves_per_eu(3))) void w2_kernel(
     const float* __restrict__ act, const uint8_t* __restrict__ w2n, const uint8_t* __restrict__ w2s,
     const uint16_t* __restrict__ b2, const int32_t* __restrict__ n_active_p, const int32_t* __restrict__ active,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ gather_map, const float* __restrict__ w,

@@ -42,12 +42,12 @@ __global__ __launch_bounds__(kTileRows * kMaxParts) void dense_gemv_kernel(
   for (int m = 0; m < kRows; ++m) acc[m] = 0.0f;
   for (int i = 0; i < g.bpp; ++i) {
     const u32x4 blk = src[static_cast<size_t>(i) * kTileRows];
-    const float scale = e8m0_to_f32(sc[i]);
+    const uint32_t code = sc[i];
     const int kb = (p * g.bpp + i) * 32;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       float wf[8];
-      decode8(blk[d], scale, wf);
+      decode8(blk[d], code, wf);
 #pragma unroll
       for (int m = 0; m < kRows; ++m) {
         if (m < mc) {
@@ -127,12 +127,12 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ wn, const uint8_t* __
     const size_t tile = row / kTileRows, lane = row % kTileRows;
     const u32x4 blk = reinterpret_cast<const u32x4*>(wn)[(tile * g.nb + b) * kTileRows + lane];
     const size_t p = b / g.bpp, i = b % g.bpp;
-    const float scale = e8m0_to_f32(ws[((tile * g.parts + p) * kTileRows + lane) * g.spad + i]);
+    const uint32_t code = ws[((tile * g.parts + p) * kTileRows + lane) * g.spad + i];
     uint16_t* o = out + row * g.K + b * 32;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       float wf[8];
-      decode8(blk[d], scale, wf);
+      decode8(blk[d], code, wf);
 #pragma unroll
       for (int c = 0; c < 8; ++c) o[d * 8 + c] = f32_to_bf16(wf[c]);
     }
