@@ -98,7 +98,6 @@ struct gptoss_moe_layer {
   std::vector<void*> owned;
   // scratch
   void* logits = nullptr;
-  float* xf = nullptr;
   int32_t* idx = nullptr;
   float* w = nullptr;
   int32_t* counts = nullptr;
@@ -107,11 +106,11 @@ struct gptoss_moe_layer {
   int32_t* ptok = nullptr;
   int32_t* active = nullptr;
   int32_t* n_active = nullptr;
-  float* act = nullptr;
+  uint16_t* act = nullptr;
   uint16_t* y = nullptr;
   uint16_t* gate_up = nullptr;
   uint16_t* normed = nullptr;
-  uint32_t* counters = nullptr;
+  void* route_scratch = nullptr;
   int n_groups = 0;
   bool trace_gu = false;
   // per-launch timing (gptoss_moe_layer_set_profiling): 4 events per recorded forward
@@ -263,7 +262,7 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
 
   const size_t T = static_cast<size_t>(cfg->max_tokens), S = T * k;
   L->n_groups = static_cast<int>((T + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup);
-  const size_t n_counters = static_cast<size_t>(L->n_groups) + 1 + H / kTileRows;
+  const size_t route_bytes = route_scratch_bytes(static_cast<int>(T), E, k);
   void* p;
 #define ALLOC(field, type, bytes)                          \
   if ((rc = L->alloc(&p, (bytes), #field)) != GPTOSS_OK) { \
@@ -272,7 +271,6 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   }                                                        \
   L->field = static_cast<type>(p);
   ALLOC(logits, void*, T * E * 4)
-  ALLOC(xf, float*, T * H * 4)
   ALLOC(idx, int32_t*, S * 4)
   ALLOC(w, float*, S * 4)
   ALLOC(counts, int32_t*, E * 4)
@@ -281,14 +279,14 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   ALLOC(ptok, int32_t*, S * 4)
   ALLOC(active, int32_t*, E * 4)
   ALLOC(n_active, int32_t*, 4)
-  ALLOC(act, float*, S * I * 4)
+  ALLOC(act, uint16_t*, S * I * 2)
   ALLOC(y, uint16_t*, S * H * 2)
-  ALLOC(counters, uint32_t*, n_counters * 4)
+  ALLOC(route_scratch, void*, route_bytes)
   if (L->norm_w != nullptr) {
     ALLOC(normed, uint16_t*, T * H * 2)
   }
 #undef ALLOC
-  hipError_t err = hipMemset(L->counters, 0, n_counters * 4);
+  hipError_t err = hipMemset(L->route_scratch, 0, route_bytes);
   if (err == hipSuccess) err = hipDeviceSynchronize();
   if (err != hipSuccess) {
     L->release();
@@ -311,12 +309,11 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ra.k = c.top_k;
   ra.logits_fp32 = c.logits_fp32;
   ra.logits = L->logits;
-  ra.xf = L->xf;
+  ra.xf = nullptr;
   ra.idx = L->idx;
   ra.w = L->w;
   ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active};
-  ra.group_counter = L->counters;
-  ra.done_counter = L->counters + L->n_groups;
+  route_scratch_carve(L->route_scratch, L->cfg.max_tokens, c.num_experts, c.top_k, ra);
   hipEvent_t* ev = nullptr;
   if (L->prof_count < L->prof_capacity) ev = &L->prof_events[4 * static_cast<size_t>(L->prof_count++)];
   if (ev) HIP_TRY(hipEventRecord(ev[0], s), "hipEventRecord");
@@ -324,7 +321,7 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
 
   ExpertArgs ea{};
-  ea.xf = L->xf;
+  ea.x = normed;
   ea.w1n = L->w1n;
   ea.w1s = L->w1s;
   ea.b1 = L->b1;
@@ -345,11 +342,11 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ea.y = L->y;
   ea.residual = residual;
   ea.out = out;
-  ea.tile_counter = L->counters + L->n_groups + 1;
   ea.max_active = T * c.top_k < c.num_experts ? T * c.top_k : c.num_experts;
   HIP_TRY(launch_w1(ea, s), "w1 launch");
   if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
   HIP_TRY(launch_w2(ea, s), "w2 launch");
+  HIP_TRY(launch_combine_slots(ea, s), "combine launch");
   if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");
   return ok();
 }
@@ -456,9 +453,9 @@ int gptoss_moe_layer_profile_read(gptoss_moe_layer* L, float* route_ms, float* w
   return ok();
 }
 
-size_t gptoss_moe_route_scratch_bytes(int T) {
-  const size_t groups = (T > 0 ? static_cast<size_t>(T) : 1) + kRouteTokensPerGroup - 1;
-  return ((groups / kRouteTokensPerGroup + 1) * 4 + 255) & ~static_cast<size_t>(255);
+size_t gptoss_moe_route_scratch_bytes(int T, int E, int k) {
+  if (T < 0 || E < 1 || k < 1) return 0;
+  return route_scratch_bytes(T, E, k);
 }
 
 int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b, int T, int E, int H,
@@ -484,9 +481,7 @@ int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t
   ra.idx = idx;
   ra.w = w;
   ra.plan = PlanBufs{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-  const int groups = (T + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup;
-  ra.group_counter = static_cast<uint32_t*>(scratch);
-  ra.done_counter = static_cast<uint32_t*>(scratch) + groups;
+  route_scratch_carve(scratch, T, E, k, ra);
   HIP_TRY(launch_route(ra, static_cast<hipStream_t>(stream)), "route launch");
   return ok();
 }

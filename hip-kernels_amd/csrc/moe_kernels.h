@@ -58,7 +58,13 @@ struct RouteArgs {
   PlanBufs plan;           // plan outputs (all may be null to skip the plan)
   uint32_t* group_counter; // [ceil(T/8)] zero at rest
   uint32_t* done_counter;  // [1] zero at rest
+  float* xchg_logits;      // [T][E] fp32 exchange (the logits as rounded)
+  int32_t* xchg_idx;       // [T][k] exchange of the selections (T > 8)
 };
+
+// Bytes of route scratch: counters, then the exchange buffers (256-aligned).
+size_t route_scratch_bytes(int T, int E, int k);
+void route_scratch_carve(void* scratch, int T, int E, int k, RouteArgs& a);
 hipError_t launch_route(const RouteArgs& a, hipStream_t s);
 
 // Standalone top-k softmax over given logits (bf16 or fp32).
@@ -69,7 +75,7 @@ hipError_t launch_topk(const void* logits, int logits_fp32, int T, int E, int k,
 hipError_t launch_plan(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s);
 
 struct ExpertArgs {
-  const float* xf;            // [T][H] fp32 copy of the expert input
+  const uint16_t* x;          // [T][H] bf16 expert input (the normed activations)
   const uint8_t* w1n;         // tiled W1 nibbles, [E] x geom1.nib_bytes
   const uint8_t* w1s;         // tiled W1 scales,  [E] x geom1.scale_bytes
   const uint16_t* b1;         // [E][2I] or null
@@ -80,18 +86,18 @@ struct ExpertArgs {
   float alpha, limit;
   PlanBufs plan;
   const float* w;             // [T][k] routing weights
-  float* act;                 // [T*k][I] fp32 (bf16-exact) SwiGLU output
+  uint16_t* act;              // [T*k][I] bf16 SwiGLU output (permuted order)
   uint16_t* gate_up;          // [T*k][2I] bf16 or null (debug output)
   uint16_t* y;                // [T*k][H] bf16 expert outputs
   const uint16_t* residual;   // [T][H] or null
   uint16_t* out;              // [T][H]
-  uint32_t* tile_counter;     // [H/64] zero at rest
   int max_active;             // grid bound on active experts: min(E, T*k)
 };
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
 // The two launches of launch_experts, for callers that time them separately.
 hipError_t launch_w1(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_w2(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_combine_slots(const ExpertArgs& a, hipStream_t s);
 
 // Row-major MXFP4 [N][K/2] + [N][K/32] -> tiled layout.
 hipError_t launch_pack_tiled(const uint8_t* packed, const uint8_t* scales, int N, int K,

@@ -10,9 +10,11 @@
 //   gemv_bf16_kernel summation tree.  The last work-group to finish a token
 //   group (atomic ticket) selects the top-k of its tokens; the last token
 //   group to finish builds the plan (histogram, exclusive scan, stable
-//   counting-sort gather map, permuted token list, active expert list).
-//   Tickets are reset by their last holder, so the launch is replayable
-//   (hipGraph) without a memset.
+//   counting-sort gather map, permuted token list, active expert list); with
+//   a single token group (T <= 8) the selecting work-group builds it from
+//   LDS directly.  Values crossing work-groups go through write-through
+//   exchange buffers (no L2 flush).  Tickets are reset by their last holder,
+//   so the launch is replayable (hipGraph) without a memset.
 #include <float.h>
 
 #include "moe_device.h"
@@ -29,11 +31,43 @@ __device__ __forceinline__ float sanitize_logit(float v) {
   return ((__float_as_uint(v) & 0x7f800000u) == 0x7f800000u) ? -FLT_MAX : v;
 }
 
-template <bool F32>
-__device__ __forceinline__ float load_logit(const void* row, int e) {
-  if constexpr (F32) return reinterpret_cast<const float*>(row)[e];
-  return bf16_to_f32(reinterpret_cast<const uint16_t*>(row)[e]);
+// Cross-work-group exchange without cache maintenance: agent-scope relaxed
+// stores and loads write through / read past the per-XCD L2, so a writer
+// that waits for its stores (vmcnt 0) before taking a ticket, and a reader
+// that loads only after holding the last ticket, see each other's data.
+__device__ __forceinline__ void st_xchg(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void st_xchg(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_xchg(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_xchg(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+__device__ __forceinline__ uint32_t take_ticket(uint32_t* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_ticket(uint32_t* counter) {
+  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Logit loaders for the top-k: a user buffer (bf16 or fp32) or the fp32
+// exchange row (already rounded as the logits are).
+struct LogitsUser {
+  const void* row;
+  bool f32;
+  __device__ float operator()(int e) const {
+    return f32 ? reinterpret_cast<const float*>(row)[e] : bf16_to_f32(reinterpret_cast<const uint16_t*>(row)[e]);
+  }
+};
+struct LogitsXchg {
+  const float* row;
+  __device__ float operator()(int e) const { return ld_xchg(row + e); }
+};
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   const uint32_t d[4] = {v.x, v.y, v.z, v.w};
@@ -50,15 +84,15 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
 // the reference's padding (topk_softmax.cu:133-159).  Lane 0 then applies the
 // softmax over the k selected values in the order of the reference variant
 // (v1 sequential sum for T <= 8, v2 xor-butterfly sum otherwise).
-template <bool F32>
-__device__ void topk_one_token(const void* row, int E, int k, int variant,
-                               int32_t* out_idx, float* out_w,
-                               int32_t* tokens_per_expert, int lane) {
+template <typename Loader>
+__device__ __forceinline__ void topk_one_token(const Loader& load, int E, int k, int variant,
+                                               int32_t* out_idx, float* out_w,
+                                               int32_t* tokens_per_expert, int32_t* lds_idx, int lane) {
   float v[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     int e = lane + 64 * j;
-    v[j] = (e < E) ? sanitize_logit(load_logit<F32>(row, e)) : -FLT_MAX;
+    v[j] = (e < E) ? sanitize_logit(load(e)) : -FLT_MAX;
   }
   float sel_v[kMaxTopK];
   int sel_i[kMaxTopK];
@@ -91,7 +125,11 @@ __device__ void topk_one_token(const void* row, int E, int k, int variant,
   if (sel_i[0] == -1) {  // topk_softmax.cu:339-346: no finite logit at all
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) { out_idx[s] = s; out_w[s] = 1.0f / static_cast<float>(k); }
+      if (s < k) {
+        out_idx[s] = s;
+        out_w[s] = 1.0f / static_cast<float>(k);
+        if (lds_idx) lds_idx[s] = s;
+      }
     if (tokens_per_expert)
       for (int s = 0; s < k; ++s) atomicAdd(&tokens_per_expert[s], 1);
     return;
@@ -128,6 +166,7 @@ __device__ void topk_one_token(const void* row, int E, int k, int variant,
     if (s < k) {
       out_idx[s] = sel_i[s];
       out_w[s] = (sel_i[s] < 0) ? 0.0f : ex[s] * inv;
+      if (lds_idx) lds_idx[s] = sel_i[s];
       if (tokens_per_expert && sel_i[s] >= 0) atomicAdd(&tokens_per_expert[sel_i[s]], 1);
     }
   }
@@ -138,7 +177,8 @@ __device__ void topk_one_token(const void* row, int E, int k, int variant,
 // counting sort of moe_permute.cu:184-236), the permuted token list and the
 // ascending list of experts with at least one slot.  Slots with an index
 // outside [0, E) get gather_map = -1 and are not dispatched.
-__device__ void build_plan(const int32_t* __restrict__ idx, int T, int k, int E, PlanBufs p) {
+template <typename IdxFn>
+__device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
   __shared__ int s_off[kMaxExperts + 1];
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_run[kMaxExperts];
@@ -154,7 +194,7 @@ __device__ void build_plan(const int32_t* __restrict__ idx, int T, int k, int E,
   for (int w = 0; w < 4; ++w) s_wc[w][tid] = 0;
   __syncthreads();
   for (int s = tid; s < S; s += kRouteThreads) {
-    int e = idx[s];
+    int e = idx(s);
     if (e >= 0 && e < E) atomicAdd(&s_cnt[e], 1);
   }
   __syncthreads();
@@ -189,7 +229,7 @@ __device__ void build_plan(const int32_t* __restrict__ idx, int T, int k, int E,
   // stable positions, 256 slots per round
   for (int r0 = 0; r0 < S; r0 += kRouteThreads) {
     const int s = r0 + tid;
-    const int e = (s < S) ? idx[s] : -1;
+    const int e = (s < S) ? idx(s) : -1;
     const bool valid = (e >= 0 && e < E);
     unsigned long long peers = __ballot(valid);
 #pragma unroll
@@ -263,10 +303,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
       for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) red[tt][ee][warp] = acc[ee];
     }
   }
-  if (blockIdx.x == 0 && a.xf != nullptr) {
-    const size_t base = static_cast<size_t>(t0) * H;
-    for (int i = tid; i < tn * H; i += kRouteThreads) a.xf[base + i] = bf16_to_f32(a.x[base + i]);
-  }
   __syncthreads();
   if (tid < tn * kRouteExpertsPerGroup) {
     const int tt = tid / kRouteExpertsPerGroup, ee = tid % kRouteExpertsPerGroup, e = e0 + ee;
@@ -276,38 +312,50 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
       for (int w = 0; w < 4; ++w) v = v + red[tt][ee][w];
       if (a.b != nullptr) v = v + bf16_to_f32(a.b[e]);
       const size_t o = static_cast<size_t>(t0 + tt) * E + e;
-      if constexpr (F32) reinterpret_cast<float*>(a.logits)[o] = v;
-      else reinterpret_cast<uint16_t*>(a.logits)[o] = f32_to_bf16(v);
+      if constexpr (F32) {
+        reinterpret_cast<float*>(a.logits)[o] = v;
+      } else {
+        const uint16_t h = f32_to_bf16(v);
+        reinterpret_cast<uint16_t*>(a.logits)[o] = h;
+        v = bf16_to_f32(h);
+      }
+      st_xchg(a.xchg_logits + o, v);
     }
   }
 
   // The last expert group of this token group selects the top-k.
-  __threadfence();
+  wait_stores();
   __syncthreads();
-  if (tid == 0) s_ticket = atomicAdd(&a.group_counter[blockIdx.y], 1u);
+  if (tid == 0) s_ticket = take_ticket(&a.group_counter[blockIdx.y]);
   __syncthreads();
   if (s_ticket != gridDim.x - 1) return;
-  __threadfence();
-  if (tid == 0) a.group_counter[blockIdx.y] = 0u;
+  if (tid == 0) reset_ticket(&a.group_counter[blockIdx.y]);
   const int variant = (a.T <= 8) ? 1 : 2;  // topk_softmax.cu:399
+  const bool one_group = gridDim.y == 1;
+  __shared__ int32_t s_idx[kRouteTokensPerGroup * kMaxTopK];
   for (int tt = warp; tt < tn; tt += 4) {
     const int t = t0 + tt;
-    const void* row = F32 ? static_cast<const void*>(reinterpret_cast<const float*>(a.logits) + static_cast<size_t>(t) * E)
-                          : static_cast<const void*>(reinterpret_cast<const uint16_t*>(a.logits) + static_cast<size_t>(t) * E);
-    topk_one_token<F32>(row, E, a.k, variant, a.idx + static_cast<size_t>(t) * a.k,
-                        a.w + static_cast<size_t>(t) * a.k, nullptr, lane);
+    topk_one_token(LogitsXchg{a.xchg_logits + static_cast<size_t>(t) * E}, E, a.k, variant,
+                   a.idx + static_cast<size_t>(t) * a.k, a.w + static_cast<size_t>(t) * a.k, nullptr,
+                   one_group ? s_idx + tt * a.k : nullptr, lane);
+    if (!one_group && lane == 0)
+      for (int s2 = 0; s2 < a.k; ++s2) st_xchg(a.xchg_idx + static_cast<size_t>(t) * a.k + s2, a.idx[static_cast<size_t>(t) * a.k + s2]);
   }
   if (a.plan.counts == nullptr) return;
+  if (one_group) {  // T <= 8: this work-group holds every token's selection
+    __syncthreads();
+    build_plan([&](int s2) { return s_idx[s2]; }, a.T, a.k, E, a.plan);
+    return;
+  }
 
   // The last token group builds the plan over all T*k slots.
-  __threadfence();
+  wait_stores();
   __syncthreads();
-  if (tid == 0) s_ticket = atomicAdd(a.done_counter, 1u);
+  if (tid == 0) s_ticket = take_ticket(a.done_counter);
   __syncthreads();
   if (s_ticket != gridDim.y - 1) return;
-  __threadfence();
-  if (tid == 0) *a.done_counter = 0u;
-  build_plan(a.idx, a.T, a.k, E, a.plan);
+  if (tid == 0) reset_ticket(a.done_counter);
+  build_plan([&](int s2) { return ld_xchg(a.xchg_idx + s2); }, a.T, a.k, E, a.plan);
 }
 
 template <bool F32>
@@ -318,16 +366,34 @@ __global__ __launch_bounds__(kRouteThreads) void topk_kernel(const void* logits,
   if (t >= T) return;
   const void* row = F32 ? static_cast<const void*>(reinterpret_cast<const float*>(logits) + static_cast<size_t>(t) * E)
                         : static_cast<const void*>(reinterpret_cast<const uint16_t*>(logits) + static_cast<size_t>(t) * E);
-  topk_one_token<F32>(row, E, k, (T <= 8) ? 1 : 2, idx + static_cast<size_t>(t) * k,
-                      w + static_cast<size_t>(t) * k, tpe, lane);
+  topk_one_token(LogitsUser{row, F32}, E, k, (T <= 8) ? 1 : 2, idx + static_cast<size_t>(t) * k,
+                 w + static_cast<size_t>(t) * k, tpe, nullptr, lane);
 }
 
 __global__ __launch_bounds__(kRouteThreads) void plan_kernel(const int32_t* idx, int T, int k, int E,
                                                             PlanBufs p) {
-  build_plan(idx, T, k, E, p);
+  build_plan([&](int s) { return idx[s]; }, T, k, E, p);
 }
 
 }  // namespace
+
+static size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+size_t route_scratch_bytes(int T, int E, int k) {
+  const size_t groups = (static_cast<size_t>(T > 0 ? T : 1) + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup;
+  return align256((groups + 1) * 4) + align256(static_cast<size_t>(T) * E * 4) + align256(static_cast<size_t>(T) * k * 4);
+}
+
+void route_scratch_carve(void* scratch, int T, int E, int k, RouteArgs& a) {
+  const size_t groups = (static_cast<size_t>(T > 0 ? T : 1) + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup;
+  char* p = static_cast<char*>(scratch);
+  a.group_counter = reinterpret_cast<uint32_t*>(p);
+  a.done_counter = a.group_counter + groups;
+  p += align256((groups + 1) * 4);
+  a.xchg_logits = reinterpret_cast<float*>(p);
+  p += align256(static_cast<size_t>(T) * E * 4);
+  a.xchg_idx = reinterpret_cast<int32_t*>(p);
+}
 
 hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
   if (a.T <= 0) return hipSuccess;

@@ -93,7 +93,7 @@ _sig("gptoss_moe_layer_set_trace_gate_up", [_P, _I])
 _sig("gptoss_moe_layer_set_profiling", [_P, _I])
 _sig("gptoss_moe_layer_profile_read", [_P, ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_F),
                                         ctypes.POINTER(_I)])
-_sig("gptoss_moe_route_scratch_bytes", [_I], _SZ)
+_sig("gptoss_moe_route_scratch_bytes", [_I, _I, _I], _SZ)
 _sig("gptoss_moe_route", [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P])
 _sig("gptoss_topk_softmax_forward", [_P, _I, _P, _P, _P, _I, _I, _I, _P])
 _sig("gptoss_moe_permute_plan", [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P])
@@ -295,7 +295,7 @@ def route(x, router_w, router_b, top_k: int, logits_fp32: bool = False, stream=N
     logits = torch.empty((T, E), dtype=torch.float32 if logits_fp32 else torch.bfloat16, device=dev)
     idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
     w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
-    scratch = torch.zeros(_lib.gptoss_moe_route_scratch_bytes(T), dtype=torch.uint8, device=dev)
+    scratch = torch.zeros(_lib.gptoss_moe_route_scratch_bytes(T, E, top_k), dtype=torch.uint8, device=dev)
     check(_lib.gptoss_moe_route(_ptr(x), _ptr(router_w), _ptr(router_b), T, E, H, top_k, 1 if logits_fp32 else 0,
                                 _ptr(logits), _ptr(idx), _ptr(w), _ptr(scratch), _stream(stream)))
     return logits, idx, w

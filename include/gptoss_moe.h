@@ -121,7 +121,7 @@ typedef struct gptoss_moe_trace {
   const int32_t* active_experts;  /* [E] ascending, first n_active valid */
   const int32_t* n_active;        /* [1] */
   const uint16_t* gate_up;        /* [T*k][2I] bf16 (only if trace_gate_up was enabled) */
-  const float* act;               /* [T*k][I] SwiGLU output (bf16 values held in fp32) */
+  const uint16_t* act;            /* [T*k][I] bf16 SwiGLU output */
   const uint16_t* expert_out;     /* [T*k][H] bf16 */
 } gptoss_moe_trace;
 int gptoss_moe_layer_trace(const gptoss_moe_layer* layer, gptoss_moe_trace* trace);
@@ -145,9 +145,10 @@ int gptoss_moe_layer_profile_read(gptoss_moe_layer* layer, float* route_ms, floa
 /* Router + top-k softmax in one launch: replaces gemv_bf16_forward (T == 1,
  * gemv_bf16.cu:236-247) / gemm_bf16_lt (T > 1, cuda_utils.h:226-308) plus
  * topk_softmax_forward (topk_softmax.cu:380).  logits: [T][E] bf16 if
- * logits_fp32 == 0 else fp32.  Needs a scratch of gptoss_moe_route_scratch_bytes(T)
- * zero-filled bytes that the call leaves zero-filled again. */
-size_t gptoss_moe_route_scratch_bytes(int num_tokens);
+ * logits_fp32 == 0 else fp32.  Needs a device scratch of
+ * gptoss_moe_route_scratch_bytes(T, E, k) bytes whose first 256-byte-aligned
+ * counter block is zero-filled; the call leaves it zero-filled again. */
+size_t gptoss_moe_route_scratch_bytes(int num_tokens, int num_experts, int top_k);
 int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
                      int num_tokens, int num_experts, int hidden, int top_k, int logits_fp32,
                      void* logits, int32_t* expert_indices, float* expert_weights,
