@@ -106,6 +106,7 @@ struct gptoss_moe_layer {
   int32_t* ptok = nullptr;
   int32_t* active = nullptr;
   int32_t* n_active = nullptr;
+  int32_t* tasks = nullptr;
   uint16_t* act = nullptr;
   uint16_t* y = nullptr;
   uint16_t* gate_up = nullptr;
@@ -279,6 +280,7 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   ALLOC(ptok, int32_t*, S * 4)
   ALLOC(active, int32_t*, E * 4)
   ALLOC(n_active, int32_t*, 4)
+  ALLOC(tasks, int32_t*, static_cast<size_t>(E) * kTaskInts * 4)
   ALLOC(act, uint16_t*, S * I * 2)
   ALLOC(y, uint16_t*, S * H * 2)
   ALLOC(route_scratch, void*, route_bytes)
@@ -312,7 +314,7 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ra.xf = nullptr;
   ra.idx = L->idx;
   ra.w = L->w;
-  ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active};
+  ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks};
   route_scratch_carve(L->route_scratch, L->cfg.max_tokens, c.num_experts, c.top_k, ra);
   hipEvent_t* ev = nullptr;
   if (L->prof_count < L->prof_capacity) ev = &L->prof_events[4 * static_cast<size_t>(L->prof_count++)];
@@ -480,7 +482,7 @@ int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t
   ra.xf = nullptr;
   ra.idx = idx;
   ra.w = w;
-  ra.plan = PlanBufs{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  ra.plan = PlanBufs{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   route_scratch_carve(scratch, T, E, k, ra);
   HIP_TRY(launch_route(ra, static_cast<hipStream_t>(stream)), "route launch");
   return ok();
@@ -506,7 +508,7 @@ int gptoss_moe_permute_plan(const int32_t* idx, int T, int k, int E, int32_t* co
   if (T == 0) return ok();
   if (!idx || !counts || !offsets || !gather_map || !perm_token || !active || !n_active)
     return fail(GPTOSS_ERR_INVALID, "null pointer");
-  HIP_TRY(launch_plan(idx, T, k, E, PlanBufs{counts, offsets, gather_map, perm_token, active, n_active},
+  HIP_TRY(launch_plan(idx, T, k, E, PlanBufs{counts, offsets, gather_map, perm_token, active, n_active, nullptr},
                       static_cast<hipStream_t>(stream)),
           "plan launch");
   return ok();

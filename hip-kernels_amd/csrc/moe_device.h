@@ -98,6 +98,23 @@ __device__ __forceinline__ void decode8(uint32_t d, uint32_t code, float* w) {
   }
 }
 
+// decode8 for a scale known to come from a code in 1..254 (scale = its
+// e8m0_to_f32 value): the conversion alone is exact.
+__device__ __forceinline__ void decode8_regular(uint32_t d, float scale, float* w) {
+  fp4x2_to_f32<0>(d, scale, w[0], w[1]);
+  fp4x2_to_f32<1>(d, scale, w[2], w[3]);
+  fp4x2_to_f32<2>(d, scale, w[4], w[5]);
+  fp4x2_to_f32<3>(d, scale, w[6], w[7]);
+}
+
+// True if any byte of `v` selected by `mask` (0xff per selected byte) is an
+// e8m0 code outside 1..254 (0x00 or 0xff).
+__device__ __forceinline__ bool has_special_code(uint32_t v, uint32_t mask) {
+  const uint32_t x = (v & mask) | (0x01010101u & ~mask);  // unselected bytes read as code 1
+  const uint32_t y = ~x;
+  return (((x - 0x01010101u) & ~x & 0x80808080u) | ((y - 0x01010101u) & ~y & 0x80808080u)) != 0u;
+}
+
 // 64-lane xor butterfly sum: after it every lane holds the same value, the
 // tree v[l] + v[l^m] for m = 32, 16, 8, 4, 2, 1.
 __device__ __forceinline__ float wave_butterfly_sum(float v) {

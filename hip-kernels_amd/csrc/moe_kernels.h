@@ -13,6 +13,8 @@ constexpr int kRouteTokensPerGroup = 8;
 constexpr int kRouteExpertsPerGroup = 4;
 constexpr int kTileRows = 64;     // rows of an MXFP4 tile (one per lane)
 constexpr int kMaxParts = 6;      // K-parts of the canonical dot (waves per tile)
+constexpr int kTaskInts = 16;     // ints per expert task record
+constexpr int kTaskTokens = 12;   // token ids held inline in a task record
 
 // Number of contiguous K-parts of the canonical expert dot for K inputs:
 // the largest p <= 6 dividing K/32.
@@ -43,6 +45,11 @@ struct PlanBufs {
   int32_t* perm_token;  // [T*k]
   int32_t* active;      // [E]
   int32_t* n_active;    // [1]
+  // [E][kTaskInts] or null: record j describes the j-th active expert as
+  // {expert, offset, count, 0, token ids of its first kTaskTokens slots};
+  // records j >= n_active hold expert -1.  One load gives an expert kernel
+  // everything it needs to start streaming weights and activations.
+  int32_t* tasks;
 };
 
 struct RouteArgs {

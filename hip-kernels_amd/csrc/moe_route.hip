@@ -183,6 +183,7 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_run[kMaxExperts];
   __shared__ int s_wc[4][kMaxExperts];
+  __shared__ int s_aidx[kMaxExperts];
   __shared__ unsigned long long s_mask[4];
   __shared__ int s_wsum[4];
   const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
@@ -221,9 +222,21 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
     p.offsets[tid] = excl;
   }
   if (tid == E - 1) { s_off[E] = excl + c; p.offsets[E] = excl + c; }
-  if (act) p.active[abase + __popcll(am & ((1ull << lane) - 1ull))] = tid;
-  if (tid == 0)
-    *p.n_active = __popcll(s_mask[0]) + __popcll(s_mask[1]) + __popcll(s_mask[2]) + __popcll(s_mask[3]);
+  const int aidx = abase + __popcll(am & ((1ull << lane) - 1ull));
+  const int nact = __popcll(s_mask[0]) + __popcll(s_mask[1]) + __popcll(s_mask[2]) + __popcll(s_mask[3]);
+  if (act) {
+    p.active[aidx] = tid;
+    s_aidx[tid] = aidx;
+    if (p.tasks) {
+      int32_t* t = p.tasks + static_cast<size_t>(aidx) * kTaskInts;
+      t[0] = tid;
+      t[1] = excl;
+      t[2] = c;
+      t[3] = 0;
+    }
+  }
+  if (p.tasks && tid < E && tid >= nact) p.tasks[static_cast<size_t>(tid) * kTaskInts] = -1;
+  if (tid == 0) *p.n_active = nact;
   __syncthreads();
 
   // stable positions, 256 slots per round
@@ -246,6 +259,8 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
       for (int w = 0; w < warp; ++w) pos += s_wc[w][e];
       p.gather_map[s] = pos;
       p.perm_token[pos] = s / k;
+      if (p.tasks && pos - s_off[e] < kTaskTokens)
+        p.tasks[static_cast<size_t>(s_aidx[e]) * kTaskInts + 4 + (pos - s_off[e])] = s / k;
     } else if (s < S) {
       p.gather_map[s] = -1;
     }
