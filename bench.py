@@ -1,20 +1,23 @@
 #!/usr/bin/env python3
-"""GPT-OSS-120B MoE-layer decode throughput on one MI355X (BASELINE config 2).
+"""GPT-OSS-120B MoE-layer decode throughput on one MI355X.
 
 A step is one MoE layer forward (router GEMV + top-k softmax + routing plan,
 MXFP4 gate_up + SwiGLU, MXFP4 down + weighted combine with the residual) over
 a batch of B decode tokens, E=128 experts, H=I=2880, top-4.  Weights are
-synthetic with the BASELINE distributions (uniform e2m1 codes, e8m0 scales
-2^-8..2^-4, router ~N(0,0.02), zero non-null biases) and live in HBM; the
-timed steps rotate over `--copies` distinct weight copies and inputs so the
-256 MB MALL cannot hold a step's weights.  The K timed steps are one hipGraph
-replay; per-launch durations come from HIP events recorded on the launch
-stream inside that replay.
+synthetic (uniform e2m1 codes, e8m0 scales 2^-8..2^-4, router ~N(0,0.02),
+zero non-null biases) and live in HBM; the timed steps rotate over
+`--copies` distinct weight copies and inputs so the 256 MB MALL cannot hold
+a step's weights.  The K timed steps are one hipGraph replay (wall interval
+from events around the replay).  Per-launch durations come from a second,
+eager pass of the same K steps in which the library records HIP events on
+its launch stream around each launch (events cannot be timed inside a graph
+replay on this runtime).
 
 The headline `value` is tokens/s at the largest batch (64); every batch of
 the sweep is reported under `sweep`.  `roofline` is for the dominant kernel
-(the W1 gate_up + SwiGLU launch) at the headline batch.  `cpu_baseline` is
-the C oracle (oracle/moe_oracle.c) timed on this host on a bounded sample.
+(the gate_up + SwiGLU launch) at the headline batch; its `traffic` is read
+from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary.  `cpu_baseline`
+is the C oracle (oracle/moe_oracle.c) timed on this host on a bounded sample.
 """
 from __future__ import annotations
 
@@ -61,8 +64,10 @@ def make_copy(g, torch, seed: int):
     return dict(tiled=(w1n, w1s, w2n, w2s), router_w=rw, router_b=rb, b1=b1, b2=b2)
 
 
-def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int):
-    """Time `steps` graph-replayed layer forwards at batch T; returns a dict."""
+def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, graph_timing: bool = True):
+    """Time `steps` graph-replayed layer forwards at batch T; returns a dict.
+    Without graph_timing the headline interval is the eager pass (profiler
+    runs that count per-dispatch hardware counters)."""
     layers = []
     for c, wc in enumerate(copies):
         cfg = g.default_config(E, T)
@@ -90,23 +95,33 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int):
 
     # headline: the K steps captured in one hipGraph, timed over one replay
     s = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=s):
-        for li, xi in plan:
-            layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
-    graph.replay()  # warm replay
-    torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    wall0 = time.perf_counter()
-    with torch.cuda.stream(s):
-        t0.record(s)
-        graph.replay()
-        t1.record(s)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
+    if graph_timing:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for li, xi in plan:
+                layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
+        graph.replay()  # warm replay
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        with torch.cuda.stream(s):
+            t0.record(s)
+            graph.replay()
+            t1.record(s)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        del graph
+    else:
+        wall0 = time.perf_counter()
+        with torch.cuda.stream(s):
+            t0.record(s)
+            for li, xi in plan:
+                layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
+            t1.record(s)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
     total_ms = t0.elapsed_time(t1)
-    del graph
 
     # per-launch durations: the same K steps eagerly, with HIP events recorded
     # by the library on the launch stream around each launch.  A bounded sleep
@@ -149,6 +164,34 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int):
     return res
 
 
+def profiled_traffic(name: str):
+    """HBM bytes per launch of the headline kernel as measured by the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by the copy calibration);
+    None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(torch, mib: int = 256, reps: int = 4):
+    """A plain device-to-device copy of `mib` MiB, `reps` times: the known-size
+    workload that scales the profiler's FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": mib << 20, "launches": reps}), flush=True)
+
+
 def cpu_baseline(seconds: float, threads: int):
     """The oracle (C, pthreads) on GPT-OSS-120B-shaped layers at batch 64,
     repeated until `seconds` of wall time; returns tokens/s."""
@@ -183,6 +226,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time the eager launches instead of a hipGraph replay (profiler counter runs)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy (scales FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -191,6 +238,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
     import gptoss_moe as g
 
     batches = [int(b) for b in args.batches.split(",")]
@@ -201,14 +251,17 @@ def main():
     sweep = {}
     for T in batches:
         log(f"batch {T}: {args.steps} steps")
-        sweep[T] = bench_batch(g, torch, copies, T, args.steps, args.warmup, seed=T)
+        sweep[T] = bench_batch(g, torch, copies, T, args.steps, args.warmup, seed=T, graph_timing=not args.no_graph)
         log(json.dumps(sweep[T]))
     head = sweep[headline_b]
     rf = None
     if "w1_gbs" in head:
+        traffic = profiled_traffic("expert_stream_gate_up_b64_traffic.md") if headline_b == 64 else None
         rf = dict(bound="hbm", achieved=head["w1_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                  frac=head["w1_gbs"] / HBM_PEAK_GBS, traffic=None,
-                  kernel="w1_kernel (MXFP4 gate_up + SwiGLU)",
+                  frac=head["w1_gbs"] / HBM_PEAK_GBS, traffic=traffic,
+                  kernel="expert_stream_kernel<gated> (MXFP4 gate_up + bias + SwiGLU)",
+                  traffic_source="profiles/expert_stream_gate_up_b64_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                 "copy-calibrated)" if traffic else None,
                   algorithmic_bytes_per_launch=head["w1_algorithmic_bytes"],
                   avg_launch_us=head["kernel_us"]["w1"])
     cpu = None
@@ -231,7 +284,7 @@ def main():
         "data": "synthetic (BASELINE distributions), random-init weights",
         "config": {"workload": f"gptoss120b_moe_layer_decode_b{headline_b}", "experts": E, "top_k": K_TOP,
                    "hidden": H, "intermediate": I, "batch": headline_b, "weight_copies": args.copies,
-                   "hipgraph": True, "parallelism": "none (1 GPU)"},
+                   "hipgraph": not args.no_graph, "parallelism": "none (1 GPU)"},
         "hbm_gbs": head["hbm_gbs"],
         "hbm_frac_of_peak": head["hbm_frac"],
         "roofline": rf,

@@ -107,3 +107,39 @@ class _FakeT:
     @property
     def shape(self):
         return (1, 2880)
+
+
+# The reference's C++ operator interface as its callers declare it
+# (engine.cu:175-196, transformer.cu:106-121; defined at moe_layer.cu:1556-1615),
+# written out as demangled signatures.
+REFERENCE_OPERATOR_SIGNATURES = {
+    "gptoss::moe_layer_create()",
+    "gptoss::moe_layer_destroy(gptoss::MoELayer*)",
+    "gptoss::moe_layer_forward(gptoss::MoELayer*, __hip_bfloat16 const*, __hip_bfloat16*, int, ihipStream_t*)",
+    "gptoss::moe_layer_forward_prenormed(gptoss::MoELayer*, __hip_bfloat16 const*, __hip_bfloat16 const*, "
+    "__hip_bfloat16*, int, ihipStream_t*)",
+    "gptoss::moe_layer_get_ffn_norm_weight(gptoss::MoELayer*)",
+    "gptoss::moe_layer_init(gptoss::MoELayer*, int, int, int, gptoss::EPComm*, gptoss::CublasHandle const*, "
+    "gptoss::CublasHandle const*, ihipStream_t*, ihipStream_t*, __hip_bfloat16 const*, __hip_bfloat16 const*, "
+    "__hip_bfloat16 const*, __hip_bfloat16 const*, __hip_bfloat16 const*, gptoss::MXFP4Weight*, "
+    "gptoss::MXFP4Weight*, " + ", ".join(
+        ["__hip_bfloat16*", "__hip_bfloat16*", "int*", "float*", "int*", "__hip_bfloat16*", "int*", "int*", "int*",
+         "int*"] + ["__hip_bfloat16*"] * 9) + ", ncclComm*)",
+}
+
+
+def test_cpp_operator_shim_exports_reference_signatures():
+    """libgptoss_moe_compat.so exports the reference's gptoss::moe_layer_*
+    with identical signatures (so identical mangled names for its callers)."""
+    import shutil
+    import subprocess
+    lib = os.path.join(ROOT, "hip-kernels_amd", "libgptoss_moe_compat.so")
+    assert os.path.exists(lib), "build the library first (make -C hip-kernels_amd)"
+    if shutil.which("nm") is None or shutil.which("c++filt") is None:
+        pytest.skip("binutils nm/c++filt not available")
+    names = subprocess.run(["nm", "-D", "--defined-only", lib], check=True, capture_output=True, text=True).stdout
+    mangled = [ln.split()[-1] for ln in names.splitlines() if "gptoss" in ln]
+    demangled = set(subprocess.run(["c++filt"], input="\n".join(mangled), check=True, capture_output=True,
+                                   text=True).stdout.split("\n")) - {""}
+    missing = REFERENCE_OPERATOR_SIGNATURES - demangled
+    assert not missing, missing

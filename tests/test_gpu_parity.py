@@ -388,3 +388,64 @@ def test_gptoss20b_decode_parity(gpu, orc, torch_mod):
     out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
     ref = orc.moe_forward(w, x, res, E, k, H, I)
     assert_bf16_parity(out, ref, "20B decode T=1")
+
+
+# ---------------------------------------------------------------------------
+# The reference's C++ operator (gptoss::moe_layer_*, moe_layer.cu:1556-1615)
+# through libgptoss_moe_compat.so, called by its mangled names as the
+# reference's engine would link them.
+# ---------------------------------------------------------------------------
+_SHIM = {
+    "create": "_ZN6gptoss16moe_layer_createEv",
+    "destroy": "_ZN6gptoss17moe_layer_destroyEPNS_8MoELayerE",
+    "init": "_ZN6gptoss14moe_layer_initEPNS_8MoELayerEiiiPNS_6EPCommEPKNS_12CublasHandleES6_P12ihipStream_tS8_"
+            "PK14__hip_bfloat16SB_SB_SB_SB_PNS_11MXFP4WeightESD_PS9_SE_PiPfSF_SE_SF_SF_SF_SF_SE_SE_SE_SE_SE_SE_SE_"
+            "SE_SE_P8ncclComm",
+    "prenormed": "_ZN6gptoss27moe_layer_forward_prenormedEPNS_8MoELayerEPK14__hip_bfloat16S4_PS2_iP12ihipStream_t",
+}
+
+
+def test_cpp_operator_shim_matches_c_abi(gpu, torch_mod, gptoss120):
+    import ctypes
+    torch = torch_mod
+    w, L = gptoss120
+    E, H = 128, 2880
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(gpu.LIB_PATH), "libgptoss_moe_compat.so"))
+    create = getattr(lib, _SHIM["create"])
+    create.restype = ctypes.c_void_p
+    destroy = getattr(lib, _SHIM["destroy"])
+    destroy.argtypes = [ctypes.c_void_p]
+    init = getattr(lib, _SHIM["init"])
+    init.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 12 + \
+        [ctypes.c_void_p] * 19 + [ctypes.c_void_p]
+    init.restype = None
+    fwd = getattr(lib, _SHIM["prenormed"])
+    fwd.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p]
+    fwd.restype = None
+
+    class MXFP4Weight(ctypes.Structure):  # moe_layer.cu:585-589
+        _fields_ = [("packed", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("num_elements", ctypes.c_int)]
+
+    mlp1 = (MXFP4Weight * E)()
+    mlp2 = (MXFP4Weight * E)()
+    for e in range(E):
+        mlp1[e] = MXFP4Weight(L.t["w1_packed"][e].data_ptr(), L.t["w1_scales"][e].data_ptr(), 2 * H * H)
+        mlp2[e] = MXFP4Weight(L.t["w2_packed"][e].data_ptr(), L.t["w2_scales"][e].data_ptr(), H * H)
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    layer = create()
+    assert layer
+    init(layer, 0, 0, 0, None, None, None, None, None, None, ptr(L.t["router_w"]), ptr(L.t.get("router_b")),
+         ptr(L.t.get("w1_bias")), ptr(L.t.get("w2_bias")), ctypes.cast(mlp1, ctypes.c_void_p),
+         ctypes.cast(mlp2, ctypes.c_void_p), *([None] * 19), None)
+    try:
+        for T in (1, 8):
+            say("C++ operator shim, T", T)
+            x, res = moe_data.make_tokens(900 + T, T, H)
+            dx, dr = dev(x, torch), dev(res, torch)
+            out = torch.empty_like(dx)
+            fwd(layer, dx.data_ptr(), dr.data_ptr(), out.data_ptr(), T, torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            want = host(L.layer.forward_prenormed(dx, dr))
+            assert np.array_equal(host(out), want), T
+    finally:
+        destroy(layer)
