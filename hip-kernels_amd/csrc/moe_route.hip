@@ -78,22 +78,27 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   }
 }
 
-// Top-k of one token by one wave.  Lane l holds experts l, l+64, l+128,
-// l+192.  Each round takes the largest visible logit (> -FLT_MAX) by
-// (value desc, index asc); a round with nothing visible yields (-FLT_MAX, -1),
-// the reference's padding (topk_softmax.cu:133-159).  Lane 0 then applies the
-// softmax over the k selected values in the order of the reference variant
-// (v1 sequential sum for T <= 8, v2 xor-butterfly sum otherwise).
+// Lane l's four logits (experts l, l+64, l+128, l+192); -FLT_MAX past E.
 template <typename Loader>
-__device__ __forceinline__ void topk_one_token(const Loader& load, int E, int k, int variant,
-                                               int32_t* out_idx, float* out_w,
-                                               int32_t* tokens_per_expert, int32_t* lds_idx, int lane) {
-  float v[4];
+__device__ __forceinline__ void load_token_logits(const Loader& load, int E, int lane, float (&v)[4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     int e = lane + 64 * j;
-    v[j] = (e < E) ? sanitize_logit(load(e)) : -FLT_MAX;
+    v[j] = (e < E) ? load(e) : -FLT_MAX;
   }
+}
+
+// Top-k of one token by one wave from its lanes' logits v (as loaded by
+// load_token_logits; sanitised here).  Each round takes the largest visible
+// logit (> -FLT_MAX) by (value desc, index asc); a round with nothing visible
+// yields (-FLT_MAX, -1), the reference's padding (topk_softmax.cu:133-159).
+// Lane 0 then applies the softmax over the k selected values in the order of
+// the reference variant (v1 sequential sum for T <= 8, v2 xor-butterfly sum
+// otherwise).
+__device__ __forceinline__ void topk_select(float (&v)[4], int k, int variant, int32_t* out_idx, float* out_w,
+                                            int32_t* tokens_per_expert, int32_t* lds_idx, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = sanitize_logit(v[j]);
   float sel_v[kMaxTopK];
   int sel_i[kMaxTopK];
 #pragma unroll
@@ -172,6 +177,15 @@ __device__ __forceinline__ void topk_one_token(const Loader& load, int E, int k,
   }
 }
 
+template <typename Loader>
+__device__ __forceinline__ void topk_one_token(const Loader& load, int E, int k, int variant,
+                                               int32_t* out_idx, float* out_w,
+                                               int32_t* tokens_per_expert, int32_t* lds_idx, int lane) {
+  float v[4];
+  load_token_logits(load, E, lane, v);
+  topk_select(v, k, variant, out_idx, out_w, tokens_per_expert, lds_idx, lane);
+}
+
 // Block-wide (256 threads) dispatch plan over the T*k slots of `idx`:
 // counts, exclusive offsets, a gather map that is stable in slot order (the
 // counting sort of moe_permute.cu:184-236), the permuted token list and the
@@ -189,13 +203,16 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
   const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
   const int S = T * k;
 
+  // slot tid's expert is read once and reused by the rank pass below
+  const int e_first = (tid < S) ? idx(tid) : -1;
+  auto slot_expert = [&](int s) { return s == tid ? e_first : idx(s); };
   s_cnt[tid] = 0;
   s_run[tid] = 0;
 #pragma unroll
   for (int w = 0; w < 4; ++w) s_wc[w][tid] = 0;
   __syncthreads();
   for (int s = tid; s < S; s += kRouteThreads) {
-    int e = idx(s);
+    int e = slot_expert(s);
     if (e >= 0 && e < E) atomicAdd(&s_cnt[e], 1);
   }
   __syncthreads();
@@ -242,7 +259,7 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
   // stable positions, 256 slots per round
   for (int r0 = 0; r0 < S; r0 += kRouteThreads) {
     const int s = r0 + tid;
-    const int e = (s < S) ? idx(s) : -1;
+    const int e = (s < S) ? slot_expert(s) : -1;
     const bool valid = (e >= 0 && e < E);
     unsigned long long peers = __ballot(valid);
 #pragma unroll
@@ -274,7 +291,51 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
   }
 }
 
-template <bool F32>
+// The H%8 tail of the router chains (gemv_bf16.cu:118-125), after the chunks.
+__device__ __forceinline__ void router_tail(const uint16_t* xr, const RouteArgs& a, int e0, int KV, int tid,
+                                            float (&acc)[kRouteExpertsPerGroup]) {
+  const int H = a.H, E = a.E;
+  for (int kk = KV * 8 + tid; kk < H; kk += kRouteThreads) {
+    const float xs = bf16_to_f32(xr[kk]);
+#pragma unroll
+    for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee)
+      if (e0 + ee < E) acc[ee] = __builtin_fmaf(xs, bf16_to_f32(a.W[static_cast<size_t>(e0 + ee) * H + kk]), acc[ee]);
+  }
+}
+
+// Logits of one token with the gemv_bf16_kernel tree (gemv_bf16.cu:57-129):
+// thread tid chains fmaf over 8-element chunks tid, tid+256, ... (NJ of
+// them at most), then the H%8 tail.  xs_chunk(j) / ws_chunk(ee, j) give chunk
+// tid + 256 j.
+template <int NJ, typename XFn, typename WFn>
+__device__ __forceinline__ void router_chains(XFn xs_chunk, WFn ws_chunk, const uint16_t* xr, const RouteArgs& a,
+                                              int e0, int KV, int tid, float (&acc)[kRouteExpertsPerGroup]) {
+  const int E = a.E;
+#pragma unroll
+  for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) acc[ee] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (tid + kRouteThreads * j < KV) {
+      float xs[8];
+      unpack_bf16x8(xs_chunk(j), xs);
+#pragma unroll
+      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) {
+        if (e0 + ee < E) {
+          float ws[8];
+          unpack_bf16x8(ws_chunk(ee, j), ws);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[ee] = __builtin_fmaf(xs[i], ws[i], acc[ee]);
+        }
+      }
+    }
+  }
+  router_tail(xr, a, e0, KV, tid, acc);
+}
+
+// NJ > 0: every thread holds at most NJ chunks (H <= 2048 * NJ); all of the
+// work-group's router and token loads are issued before the first FMA.
+// NJ == 0: any H, one chunk in flight at a time.
+template <bool F32, int NJ>
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
   const int e0 = blockIdx.x * kRouteExpertsPerGroup;
@@ -285,31 +346,55 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
   __shared__ float red[kRouteTokensPerGroup][kRouteExpertsPerGroup][4];
   __shared__ uint32_t s_ticket;
 
-  // Logits with the gemv_bf16_kernel tree (gemv_bf16.cu:57-129): thread tid
-  // chains fmaf over 8-element chunks tid, tid+256, ..., then the H%8 tail;
-  // xor butterfly per wave; the 4 wave sums are added in order from 0.
-  for (int tt = 0; tt < tn; ++tt) {
+  // Logits: per token, the chains of router_chains; xor butterfly per wave;
+  // the 4 wave sums are added in order from 0.
+  constexpr int kNJ = NJ > 0 ? NJ : 1;
+  uint4 wv[kRouteExpertsPerGroup][kNJ];
+  uint4 xv[kRouteTokensPerGroup][kNJ];
+  if constexpr (NJ > 0) {
+#pragma unroll
+    for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int kv = tid + kRouteThreads * j;
+        wv[ee][j] = (kv < KV && e0 + ee < E)
+                        ? *reinterpret_cast<const uint4*>(a.W + static_cast<size_t>(e0 + ee) * H + kv * 8)
+                        : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+    for (int tt = 0; tt < kRouteTokensPerGroup; ++tt)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int kv = tid + kRouteThreads * j;
+        xv[tt][j] = (tt < tn && kv < KV)
+                        ? *reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(t0 + tt) * H + kv * 8)
+                        : make_uint4(0, 0, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int tt = 0; tt < kRouteTokensPerGroup; ++tt) {
+    if (tt >= tn) break;
     const uint16_t* xr = a.x + static_cast<size_t>(t0 + tt) * H;
-    float acc[kRouteExpertsPerGroup] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int kv = tid; kv < KV; kv += kRouteThreads) {
-      float xs[8];
-      unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + kv * 8), xs);
+    float acc[kRouteExpertsPerGroup];
+    if constexpr (NJ > 0) {
+      router_chains<NJ>([&](int j) { return xv[tt][j]; }, [&](int ee, int j) { return wv[ee][j]; }, xr, a, e0, KV,
+                        tid, acc);
+    } else {
+      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) acc[ee] = 0.0f;
+      for (int kv = tid; kv < KV; kv += kRouteThreads) {
+        float xs[8];
+        unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + kv * 8), xs);
 #pragma unroll
-      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) {
-        if (e0 + ee < E) {
-          float ws[8];
-          unpack_bf16x8(*reinterpret_cast<const uint4*>(a.W + static_cast<size_t>(e0 + ee) * H + kv * 8), ws);
+        for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) {
+          if (e0 + ee < E) {
+            float ws[8];
+            unpack_bf16x8(*reinterpret_cast<const uint4*>(a.W + static_cast<size_t>(e0 + ee) * H + kv * 8), ws);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[ee] = __builtin_fmaf(xs[i], ws[i], acc[ee]);
+            for (int i = 0; i < 8; ++i) acc[ee] = __builtin_fmaf(xs[i], ws[i], acc[ee]);
+          }
         }
       }
-    }
-    for (int kk = KV * 8 + tid; kk < H; kk += kRouteThreads) {
-      const float xs = bf16_to_f32(xr[kk]);
-#pragma unroll
-      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee)
-        if (e0 + ee < E)
-          acc[ee] = __builtin_fmaf(xs, bf16_to_f32(a.W[static_cast<size_t>(e0 + ee) * H + kk]), acc[ee]);
+      router_tail(xr, a, e0, KV, tid, acc);
     }
 #pragma unroll
     for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) acc[ee] = wave_butterfly_sum(acc[ee]);
@@ -348,13 +433,25 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
   const int variant = (a.T <= 8) ? 1 : 2;  // topk_softmax.cu:399
   const bool one_group = gridDim.y == 1;
   __shared__ int32_t s_idx[kRouteTokensPerGroup * kMaxTopK];
-  for (int tt = warp; tt < tn; tt += 4) {
-    const int t = t0 + tt;
-    topk_one_token(LogitsXchg{a.xchg_logits + static_cast<size_t>(t) * E}, E, a.k, variant,
-                   a.idx + static_cast<size_t>(t) * a.k, a.w + static_cast<size_t>(t) * a.k, nullptr,
-                   one_group ? s_idx + tt * a.k : nullptr, lane);
-    if (!one_group && lane == 0)
-      for (int s2 = 0; s2 < a.k; ++s2) st_xchg(a.xchg_idx + static_cast<size_t>(t) * a.k + s2, a.idx[static_cast<size_t>(t) * a.k + s2]);
+  // Wave w selects tokens w and w + 4; both rows' logits are loaded first.
+  static_assert(kRouteTokensPerGroup == 8, "two tokens per wave");
+  float lv[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int tt = warp + 4 * h;
+    if (tt < tn) load_token_logits(LogitsXchg{a.xchg_logits + static_cast<size_t>(t0 + tt) * E}, E, lane, lv[h]);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int tt = warp + 4 * h;
+    if (tt < tn) {
+      const int t = t0 + tt;
+      topk_select(lv[h], a.k, variant, a.idx + static_cast<size_t>(t) * a.k, a.w + static_cast<size_t>(t) * a.k,
+                  nullptr, one_group ? s_idx + tt * a.k : nullptr, lane);
+      if (!one_group && lane == 0)
+        for (int s2 = 0; s2 < a.k; ++s2)
+          st_xchg(a.xchg_idx + static_cast<size_t>(t) * a.k + s2, a.idx[static_cast<size_t>(t) * a.k + s2]);
+    }
   }
   if (a.plan.counts == nullptr) return;
   if (one_group) {  // T <= 8: this work-group holds every token's selection
@@ -414,10 +511,17 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
   if (a.T <= 0) return hipSuccess;
   dim3 grid((a.E + kRouteExpertsPerGroup - 1) / kRouteExpertsPerGroup,
             (a.T + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup);
-  if (a.logits_fp32)
-    hipLaunchKernelGGL(route_kernel<true>, grid, dim3(kRouteThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(route_kernel<false>, grid, dim3(kRouteThreads), 0, s, a);
+  // chunks of 8 inputs per thread: 2 covers H <= 4096 (GPT-OSS: 2880)
+  const int nj = ((a.H >> 3) + kRouteThreads - 1) / kRouteThreads;
+  if (a.logits_fp32) {
+    if (nj <= 1) hipLaunchKernelGGL((route_kernel<true, 1>), grid, dim3(kRouteThreads), 0, s, a);
+    else if (nj == 2) hipLaunchKernelGGL((route_kernel<true, 2>), grid, dim3(kRouteThreads), 0, s, a);
+    else hipLaunchKernelGGL((route_kernel<true, 0>), grid, dim3(kRouteThreads), 0, s, a);
+  } else {
+    if (nj <= 1) hipLaunchKernelGGL((route_kernel<false, 1>), grid, dim3(kRouteThreads), 0, s, a);
+    else if (nj == 2) hipLaunchKernelGGL((route_kernel<false, 2>), grid, dim3(kRouteThreads), 0, s, a);
+    else hipLaunchKernelGGL((route_kernel<false, 0>), grid, dim3(kRouteThreads), 0, s, a);
+  }
   return hipGetLastError();
 }
 
