@@ -150,6 +150,7 @@ int gptoss_moe_config_default(gptoss_moe_config* cfg, int num_experts, int max_t
   cfg->rms_norm_eps = 1e-5f;      // config.h:39
   cfg->logits_fp32 = 0;
   cfg->max_tokens = max_tokens;
+  cfg->prefill_min_tokens = 128;
   return ok();
 }
 
@@ -196,6 +197,8 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   if (E < 1 || E > kMaxExperts) return fail(GPTOSS_ERR_UNSUPPORTED, "num_experts=%d outside [1, %d]", E, kMaxExperts);
   if (!valid_topk(k) || k > E) return fail(GPTOSS_ERR_INVALID, "top_k=%d must be 1, 2, 4 or 8 and <= num_experts", k);
   if (cfg->max_tokens < 1) return fail(GPTOSS_ERR_INVALID, "max_tokens=%d must be >= 1", cfg->max_tokens);
+  if (cfg->prefill_min_tokens < 0)
+    return fail(GPTOSS_ERR_INVALID, "prefill_min_tokens=%d must be >= 0", cfg->prefill_min_tokens);
   if (H % kTileRows != 0) return fail(GPTOSS_ERR_UNSUPPORTED, "hidden_size=%d must be a multiple of 64", H);
   int rc = check_mxfp4_shape(2 * I, H);
   if (rc != GPTOSS_OK) return rc;
@@ -298,6 +301,79 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   return ok();
 }
 
+// Expert products and combine after the plan (decode: exact weight-streaming
+// kernels; prefill: grouped matrix-core GEMMs).  w: routing weights [T][k].
+static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, const float* w,
+                         uint16_t* out, int T, hipStream_t s, hipEvent_t* ev) {
+  const gptoss_moe_config& c = L->cfg;
+  ExpertArgs ea{};
+  ea.x = normed;
+  ea.w1n = L->w1n;
+  ea.w1s = L->w1s;
+  ea.b1 = L->b1;
+  ea.w2n = L->w2n;
+  ea.w2s = L->w2s;
+  ea.b2 = L->b2;
+  ea.T = T;
+  ea.E = c.num_experts;
+  ea.H = c.hidden_size;
+  ea.I = c.intermediate_size;
+  ea.k = c.top_k;
+  ea.alpha = c.swiglu_alpha;
+  ea.limit = c.swiglu_limit;
+  ea.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks};
+  ea.w = w;
+  ea.act = L->act;
+  ea.gate_up = L->trace_gu ? L->gate_up : nullptr;
+  ea.y = L->y;
+  ea.residual = residual;
+  ea.out = out;
+  ea.max_active = T * c.top_k < c.num_experts ? T * c.top_k : c.num_experts;
+  if (c.prefill_min_tokens > 0 && T >= c.prefill_min_tokens) {
+    GroupedArgs g{};
+    g.x = normed;
+    g.row_index = L->ptok;
+    g.offsets = L->offsets;
+    g.E = c.num_experts;
+    g.rows = T * c.top_k;
+    g.wn = L->w1n;
+    g.ws = L->w1s;
+    g.N = 2 * c.intermediate_size;
+    g.K = c.hidden_size;
+    g.bias = L->b1;
+    g.out = L->act;
+    g.gate_up = ea.gate_up;
+    g.gated = 1;
+    g.alpha = c.swiglu_alpha;
+    g.limit = c.swiglu_limit;
+    HIP_TRY(launch_grouped_mxfp4(g, s), "grouped gate_up launch");
+    if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
+    g.x = L->act;
+    g.row_index = nullptr;
+    g.wn = L->w2n;
+    g.ws = L->w2s;
+    g.N = c.hidden_size;
+    g.K = c.intermediate_size;
+    g.bias = L->b2;
+    g.out = L->y;
+    g.gate_up = nullptr;
+    g.gated = 0;
+    HIP_TRY(launch_grouped_mxfp4(g, s), "grouped down launch");
+  } else {
+    HIP_TRY(launch_w1(ea, s), "w1 launch");
+    if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
+    HIP_TRY(launch_w2(ea, s), "w2 launch");
+  }
+  HIP_TRY(launch_combine_slots(ea, s), "combine launch");
+  if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");
+  return ok();
+}
+
+static hipEvent_t* next_prof_events(gptoss_moe_layer* L) {
+  if (L->prof_count < L->prof_capacity) return &L->prof_events[4 * static_cast<size_t>(L->prof_count++)];
+  return nullptr;
+}
+
 static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, uint16_t* out,
                               int T, hipStream_t s) {
   const gptoss_moe_config& c = L->cfg;
@@ -316,41 +392,11 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ra.w = L->w;
   ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks};
   route_scratch_carve(L->route_scratch, L->cfg.max_tokens, c.num_experts, c.top_k, ra);
-  hipEvent_t* ev = nullptr;
-  if (L->prof_count < L->prof_capacity) ev = &L->prof_events[4 * static_cast<size_t>(L->prof_count++)];
+  hipEvent_t* ev = next_prof_events(L);
   if (ev) HIP_TRY(hipEventRecord(ev[0], s), "hipEventRecord");
   HIP_TRY(launch_route(ra, s), "route launch");
   if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
-
-  ExpertArgs ea{};
-  ea.x = normed;
-  ea.w1n = L->w1n;
-  ea.w1s = L->w1s;
-  ea.b1 = L->b1;
-  ea.w2n = L->w2n;
-  ea.w2s = L->w2s;
-  ea.b2 = L->b2;
-  ea.T = T;
-  ea.E = c.num_experts;
-  ea.H = c.hidden_size;
-  ea.I = c.intermediate_size;
-  ea.k = c.top_k;
-  ea.alpha = c.swiglu_alpha;
-  ea.limit = c.swiglu_limit;
-  ea.plan = ra.plan;
-  ea.w = L->w;
-  ea.act = L->act;
-  ea.gate_up = L->trace_gu ? L->gate_up : nullptr;
-  ea.y = L->y;
-  ea.residual = residual;
-  ea.out = out;
-  ea.max_active = T * c.top_k < c.num_experts ? T * c.top_k : c.num_experts;
-  HIP_TRY(launch_w1(ea, s), "w1 launch");
-  if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
-  HIP_TRY(launch_w2(ea, s), "w2 launch");
-  HIP_TRY(launch_combine_slots(ea, s), "combine launch");
-  if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");
-  return ok();
+  return layer_experts(L, normed, residual, L->w, out, T, s, ev);
 }
 
 static int check_forward_args(gptoss_moe_layer* L, const void* in, const void* out, int T) {
@@ -384,6 +430,25 @@ int gptoss_moe_layer_forward(gptoss_moe_layer* L, const uint16_t* input, uint16_
   HIP_TRY(launch_rmsnorm(input, L->norm_w, L->normed, T, L->cfg.hidden_size, L->cfg.rms_norm_eps, s),
           "rmsnorm launch");
   return layer_forward_core(L, L->normed, input, out, T, s);
+}
+
+int gptoss_moe_layer_forward_routed(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual,
+                                    const int32_t* idx, const float* w, uint16_t* out, int T, void* stream) {
+  int rc = check_forward_args(L, normed, out, T);
+  if (rc != GPTOSS_OK) return rc;
+  if (T == 0) return ok();
+  if (idx == nullptr || w == nullptr) return fail(GPTOSS_ERR_INVALID, "null expert indices / weights");
+  ScopedDevice sd(L->device);
+  if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const gptoss_moe_config& c = L->cfg;
+  hipEvent_t* ev = next_prof_events(L);
+  if (ev) HIP_TRY(hipEventRecord(ev[0], s), "hipEventRecord");
+  HIP_TRY(launch_plan(idx, T, c.top_k, c.num_experts,
+                      PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks}, s),
+          "plan launch");
+  if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
+  return layer_experts(L, normed, residual, w, out, T, s, ev);
 }
 
 const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* L) {
@@ -551,6 +616,41 @@ int gptoss_moe_combine_forward(uint16_t* out, const uint16_t* y, const int32_t* 
   if (!out || !y || !gather_map || !w) return fail(GPTOSS_ERR_INVALID, "null pointer");
   HIP_TRY(launch_combine(out, y, gather_map, w, residual, T, H, k, static_cast<hipStream_t>(stream)),
           "combine launch");
+  return ok();
+}
+
+int gptoss_moe_grouped_mxfp4_gemm(const uint16_t* x, const int32_t* row_index, const int32_t* offsets, int E,
+                                  int rows, const uint8_t* nib, const uint8_t* sc, const uint16_t* bias, int N, int K,
+                                  int swiglu, float alpha, float limit, uint16_t* out, uint16_t* gate_up,
+                                  void* stream) {
+  int rc = check_mxfp4_shape(N, K);
+  if (rc != GPTOSS_OK) return rc;
+  if (E < 1 || E > kMaxExperts) return fail(GPTOSS_ERR_UNSUPPORTED, "num_experts=%d outside [1, %d]", E, kMaxExperts);
+  if (rows < 0) return fail(GPTOSS_ERR_INVALID, "rows=%d < 0", rows);
+  if (rows == 0) return ok();
+  if (!x || !offsets || !nib || !sc || !out) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  if (!aligned16(x) || !aligned16(out) || (gate_up && !aligned16(gate_up)) || !aligned16(nib))
+    return fail(GPTOSS_ERR_INVALID, "x, out, gate_up and the nibbles must be 16-byte aligned");
+  if (bias && (reinterpret_cast<uintptr_t>(bias) & 7u))
+    return fail(GPTOSS_ERR_INVALID, "bias must be 8-byte aligned");
+  if (swiglu && N % 2 != 0) return fail(GPTOSS_ERR_INVALID, "swiglu needs an even N");
+  GroupedArgs g{};
+  g.x = x;
+  g.row_index = row_index;
+  g.offsets = offsets;
+  g.E = E;
+  g.rows = rows;
+  g.wn = nib;
+  g.ws = sc;
+  g.N = N;
+  g.K = K;
+  g.bias = bias;
+  g.out = out;
+  g.gate_up = swiglu ? gate_up : nullptr;
+  g.gated = swiglu != 0;
+  g.alpha = alpha;
+  g.limit = limit;
+  HIP_TRY(launch_grouped_mxfp4(g, static_cast<hipStream_t>(stream)), "grouped gemm launch");
   return ok();
 }
 

@@ -106,6 +106,29 @@ hipError_t launch_w1(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_w2(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_combine_slots(const ExpertArgs& a, hipStream_t s);
 
+// Grouped MXFP4 product on the matrix cores (prefill): for each expert e and
+// permuted position p in [offsets[e], offsets[e+1]),
+//   y[p][n] = bf16(sum_k x[row(p)][k] * W_e[n][k] + bias[e][n]),
+// row(p) = row_index[p] (or p when row_index is null).  gated: out[p][n/2] =
+// bf16(SwiGLU(y[p][n], y[p][n+1])) for even n (gate_up optionally gets y);
+// else out[p][n] = y[p][n].  rows bounds offsets[E] (the grid is sized by it).
+struct GroupedArgs {
+  const uint16_t* x;
+  const int32_t* row_index;
+  const int32_t* offsets;
+  int E, rows;
+  const uint8_t* wn;   // tiled nibbles, [E] x tiled_geom(N, K).nib_bytes
+  const uint8_t* ws;   // tiled scales
+  int N, K;
+  const uint16_t* bias;
+  uint16_t* out;
+  uint16_t* gate_up;
+  int gated;
+  float alpha, limit;
+};
+bool grouped_supported(int N, int K, int E);
+hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s);
+
 // Row-major MXFP4 [N][K/2] + [N][K/32] -> tiled layout.
 hipError_t launch_pack_tiled(const uint8_t* packed, const uint8_t* scales, int N, int K,
                              uint8_t* tiled_nib, uint8_t* tiled_scales, hipStream_t s);

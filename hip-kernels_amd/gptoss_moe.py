@@ -52,7 +52,7 @@ class ValueErrorG(GptossError, ValueError):
 class MoeConfig(ctypes.Structure):
     _fields_ = [("hidden_size", _I), ("num_experts", _I), ("top_k", _I), ("intermediate_size", _I),
                 ("swiglu_alpha", _F), ("swiglu_limit", _F), ("rms_norm_eps", _F), ("logits_fp32", _I),
-                ("max_tokens", _I)]
+                ("max_tokens", _I), ("prefill_min_tokens", _I)]
 
 
 class MoeWeights(ctypes.Structure):
@@ -86,6 +86,7 @@ _sig("gptoss_moe_layer_create", [], _P)
 _sig("gptoss_moe_layer_init", [_P, ctypes.POINTER(MoeConfig), _I, ctypes.POINTER(MoeWeights)])
 _sig("gptoss_moe_layer_forward", [_P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_prenormed", [_P, _P, _P, _P, _I, _P])
+_sig("gptoss_moe_layer_forward_routed", [_P, _P, _P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_get_ffn_norm_weight", [_P], _P)
 _sig("gptoss_moe_layer_destroy", [_P], None)
 _sig("gptoss_moe_layer_trace", [_P, ctypes.POINTER(MoeTrace)])
@@ -102,6 +103,7 @@ _sig("gptoss_mxfp4_gemv_forward", [_P, _I, _P, _P, _P, _P, _I, _I, _P])
 _sig("gptoss_swiglu_forward", [_P, _P, _I, _I, _F, _F, _P])
 _sig("gptoss_moe_combine_forward", [_P, _P, _P, _P, _P, _I, _I, _I, _P])
 _sig("gptoss_mxfp4_dequant", [_P, _P, _I, _I, _P, _P])
+_sig("gptoss_moe_grouped_mxfp4_gemm", [_P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _F, _F, _P, _P, _P])
 
 lib = _lib
 
@@ -130,10 +132,13 @@ def _stream(stream):
     return stream.cuda_stream
 
 
-def default_config(num_experts: int = 128, max_tokens: int = 64, logits_fp32: bool = False) -> MoeConfig:
+def default_config(num_experts: int = 128, max_tokens: int = 64, logits_fp32: bool = False,
+                   prefill_min_tokens: int | None = None) -> MoeConfig:
     cfg = MoeConfig()
     check(_lib.gptoss_moe_config_default(ctypes.byref(cfg), num_experts, max_tokens))
     cfg.logits_fp32 = 1 if logits_fp32 else 0
+    if prefill_min_tokens is not None:
+        cfg.prefill_min_tokens = prefill_min_tokens
     return cfg
 
 
@@ -228,6 +233,16 @@ class MoELayer:
             out = torch.empty_like(normed)
         check(_lib.gptoss_moe_layer_forward_prenormed(self._h, _ptr(normed), _ptr(residual), _ptr(out), T,
                                                       _stream(stream)))
+        return out
+
+    def forward_routed(self, normed, expert_indices, expert_weights, residual=None, out=None, stream=None):
+        """out = residual + sum_k w * FFN_idx(normed) with the routing given
+        (int32 [T][k] indices, fp32 [T][k] weights, on the device)."""
+        T = normed.shape[0]
+        if out is None:
+            out = torch.empty_like(normed)
+        check(_lib.gptoss_moe_layer_forward_routed(self._h, _ptr(normed), _ptr(residual), _ptr(expert_indices),
+                                                   _ptr(expert_weights), _ptr(out), T, _stream(stream)))
         return out
 
     def get_ffn_norm_weight(self) -> int:
@@ -357,4 +372,19 @@ def combine(expert_out, gather_map, weights, residual, T: int, H: int, top_k: in
 def dequant(tiled_nib, tiled_sc, N: int, K: int, stream=None):
     out = torch.empty((N, K), dtype=torch.bfloat16, device=tiled_nib.device)
     check(_lib.gptoss_mxfp4_dequant(_ptr(tiled_nib), _ptr(tiled_sc), N, K, _ptr(out), _stream(stream)))
+    return out
+
+
+def grouped_mxfp4_gemm(x, offsets, tiled_nib, tiled_sc, N: int, K: int, rows: int, bias=None, row_index=None,
+                       swiglu: bool = False, alpha: float = 1.702, limit: float = 7.0, gate_up=None, out=None,
+                       stream=None):
+    """Grouped expert product on the matrix cores: rows p of expert e (offsets,
+    int32 [E+1] on the device) times W_e (expert-major tiled buffers); x rows
+    gathered through row_index when given.  swiglu: out is [rows][N/2]."""
+    E = offsets.numel() - 1
+    if out is None:
+        out = torch.empty((rows, N // 2 if swiglu else N), dtype=torch.bfloat16, device=x.device)
+    check(_lib.gptoss_moe_grouped_mxfp4_gemm(_ptr(x), _ptr(row_index), _ptr(offsets), E, rows, _ptr(tiled_nib),
+                                             _ptr(tiled_sc), _ptr(bias), N, K, 1 if swiglu else 0, alpha, limit,
+                                             _ptr(out), _ptr(gate_up), _stream(stream)))
     return out

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GPTOSS_MOE_ABI_VERSION 1
+#define GPTOSS_MOE_ABI_VERSION 2
 
 enum {
   GPTOSS_OK = 0,
@@ -53,6 +53,12 @@ typedef struct gptoss_moe_config {
   float rms_norm_eps;     /* 1e-5  (config.h:39), used by forward() only */
   int logits_fp32;        /* 0: bf16 router logits (reference), 1: fp32 logits */
   int max_tokens;         /* largest T a forward call may pass (scratch sizing) */
+  /* Forwards of at least this many tokens run the expert products as grouped
+   * GEMMs on the matrix cores (fp32 accumulation in the matrix core's order:
+   * within one bf16 rounding step of the canonical result, not bit-identical);
+   * smaller ones (decode) stream the weights through the exact VALU kernels.
+   * 0 = never.  Default 128. */
+  int prefill_min_tokens;
 } gptoss_moe_config;
 
 /* Fill `cfg` with the GPT-OSS constants for `num_experts` experts. */
@@ -104,6 +110,16 @@ int gptoss_moe_layer_forward(gptoss_moe_layer* layer, const uint16_t* input, uin
 int gptoss_moe_layer_forward_prenormed(gptoss_moe_layer* layer, const uint16_t* normed,
                                        const uint16_t* residual, uint16_t* output,
                                        int num_tokens, void* stream);
+/* The layer's expert half with the routing given: out = residual +
+ * sum_k w[t,k] * FFN_{idx[t,k]}(normed[t]).  This is forward_core's
+ * permute / experts / combine (moe_layer.cu:1196-1549) entered after its
+ * single-GPU top-k (moe_layer.cu:1188), for callers that route elsewhere (or inject a routing, as prefill
+ * benchmarks with skewed expert popularity do).  Indices must lie in
+ * [0, num_experts) and be distinct per token; weights are used as given. */
+int gptoss_moe_layer_forward_routed(gptoss_moe_layer* layer, const uint16_t* normed,
+                                    const uint16_t* residual, const int32_t* expert_indices,
+                                    const float* expert_weights, uint16_t* output, int num_tokens,
+                                    void* stream);
 const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* layer);
 void gptoss_moe_layer_destroy(gptoss_moe_layer* layer);           /* moe_layer_destroy */
 
@@ -188,6 +204,26 @@ int gptoss_moe_combine_forward(uint16_t* out, const uint16_t* expert_out,
                                const int32_t* gather_map, const float* expert_weights,
                                const uint16_t* residual, int num_tokens, int hidden,
                                int top_k, void* stream);
+
+/* The prefill expert products: per active expert, mxfp4_dequant_batched
+ * (mxfp4_dequant.cu:353-375) + CublasHandle::gemm_bf16_lt (cuda_utils.h:
+ * 226-308) + bias_add_rows (moe_layer.cu:171-194) [+ swiglu_forward] as issued
+ * by moe_layer.cu:1389-1487, in one grouped launch on the matrix cores:
+ *   y[p][n] = bf16(sum_k x[row(p)][k] * W_e[n][k] + bias[e][n])
+ * for every expert e and permuted row p in [offsets[e], offsets[e+1]), with
+ * row(p) = row_index[p] (a gather from token rows, e.g. the plan's
+ * perm_token) or p when row_index is NULL.  W_e is expert e of an
+ * expert-major tiled array (E x gptoss_mxfp4_tiled_size(N, K)).
+ * swiglu == 0: out[p][n] = y[p][n] ([rows][N]).  swiglu != 0: out[p][i] =
+ * bf16(SwiGLU(y[p][2i], y[p][2i+1])) ([rows][N/2], interleaved gate/up rows),
+ * and gate_up (may be NULL) receives y.  offsets (device, [E+1]) must be
+ * nondecreasing from 0 with offsets[E] <= rows.  fp32 accumulation in the
+ * matrix core's order (see prefill_min_tokens). */
+int gptoss_moe_grouped_mxfp4_gemm(const uint16_t* x, const int32_t* row_index,
+                                  const int32_t* expert_offsets, int num_experts, int rows,
+                                  const uint8_t* tiled_nibbles, const uint8_t* tiled_scales,
+                                  const uint16_t* bias, int N, int K, int swiglu, float alpha,
+                                  float limit, uint16_t* out, uint16_t* gate_up, void* stream);
 
 /* mxfp4_dequant_batched (mxfp4_dequant.cu:353-375) for one tiled matrix:
  * out[n][k] = bf16(e2m1 * 2^(scale-127)), row-major [N][K]. */

@@ -478,25 +478,13 @@ static void run_pool(void* (*fn)(void*), layer_job* J, int nthreads) {
   free(th);
 }
 
-void orc_moe_forward(const orc_cfg* cfg, const orc_weights* wt,
-                     const uint16_t* x, const uint16_t* residual, int T,
-                     uint16_t* out, orc_trace* trace, int nthreads) {
-  if (T <= 0) return;
+/* The expert half of the layer with the routing given (moe_layer.cu:
+ * 1196-1549: permute, experts, combine); idx/w are [T][k]. */
+static void moe_experts_combine(const orc_cfg* cfg, const orc_weights* wt, const uint16_t* x,
+                                const uint16_t* residual, int T, const int32_t* idx, const float* w,
+                                uint16_t* out, orc_trace* trace, int nthreads) {
   const int H = cfg->H, E = cfg->E, k = cfg->k, I = cfg->I, S = T * k;
   if (nthreads <= 0) nthreads = (int)sysconf(_SC_NPROCESSORS_ONLN);
-
-  float* lf = (float*)malloc(sizeof(float) * (size_t)T * E);
-  uint16_t* lb = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T * E);
-  if (cfg->logits_fp32) {
-    orc_router(x, wt->router_w, wt->router_b, T, E, H, NULL, lf);
-  } else {
-    orc_router(x, wt->router_w, wt->router_b, T, E, H, lb, NULL);
-    for (size_t i = 0; i < (size_t)T * E; ++i) lf[i] = bf(lb[i]);
-  }
-  int32_t* idx = (int32_t*)malloc(sizeof(int32_t) * (size_t)S);
-  float* w = (float*)malloc(sizeof(float) * (size_t)S);
-  orc_topk_softmax(lf, T, E, k, cfg->topk_variant, idx, w);
-
   int32_t* counts = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
   int32_t* offsets = (int32_t*)malloc(sizeof(int32_t) * (size_t)(E + 1));
   int32_t* gmap = (int32_t*)malloc(sizeof(int32_t) * (size_t)S);
@@ -519,17 +507,49 @@ void orc_moe_forward(const orc_cfg* cfg, const orc_weights* wt,
   orc_combine(J.y, gmap, w, residual, T, k, H, out);
 
   if (trace) {
-    if (trace->logits_bf16 && !cfg->logits_fp32)
-      memcpy(trace->logits_bf16, lb, sizeof(uint16_t) * (size_t)T * E);
-    if (trace->logits_f32) memcpy(trace->logits_f32, lf, sizeof(float) * (size_t)T * E);
-    if (trace->idx) memcpy(trace->idx, idx, sizeof(int32_t) * (size_t)S);
-    if (trace->w) memcpy(trace->w, w, sizeof(float) * (size_t)S);
     if (trace->gather_map) memcpy(trace->gather_map, gmap, sizeof(int32_t) * (size_t)S);
     if (trace->gate_up) memcpy(trace->gate_up, J.gate_up, sizeof(uint16_t) * (size_t)S * 2 * I);
     if (trace->act) memcpy(trace->act, J.act, sizeof(uint16_t) * (size_t)S * I);
     if (trace->y) memcpy(trace->y, J.y, sizeof(uint16_t) * (size_t)S * H);
   }
   free(J.gate_up); free(J.act); free(J.y);
-  free(lf); free(lb); free(idx); free(w);
   free(counts); free(offsets); free(gmap); free(ptok); free(active);
+}
+
+void orc_moe_forward(const orc_cfg* cfg, const orc_weights* wt,
+                     const uint16_t* x, const uint16_t* residual, int T,
+                     uint16_t* out, orc_trace* trace, int nthreads) {
+  if (T <= 0) return;
+  const int H = cfg->H, E = cfg->E, k = cfg->k, S = T * k;
+
+  float* lf = (float*)malloc(sizeof(float) * (size_t)T * E);
+  uint16_t* lb = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T * E);
+  if (cfg->logits_fp32) {
+    orc_router(x, wt->router_w, wt->router_b, T, E, H, NULL, lf);
+  } else {
+    orc_router(x, wt->router_w, wt->router_b, T, E, H, lb, NULL);
+    for (size_t i = 0; i < (size_t)T * E; ++i) lf[i] = bf(lb[i]);
+  }
+  int32_t* idx = (int32_t*)malloc(sizeof(int32_t) * (size_t)S);
+  float* w = (float*)malloc(sizeof(float) * (size_t)S);
+  orc_topk_softmax(lf, T, E, k, cfg->topk_variant, idx, w);
+
+  moe_experts_combine(cfg, wt, x, residual, T, idx, w, out, trace, nthreads);
+
+  if (trace) {
+    if (trace->logits_bf16 && !cfg->logits_fp32)
+      memcpy(trace->logits_bf16, lb, sizeof(uint16_t) * (size_t)T * E);
+    if (trace->logits_f32) memcpy(trace->logits_f32, lf, sizeof(float) * (size_t)T * E);
+    if (trace->idx) memcpy(trace->idx, idx, sizeof(int32_t) * (size_t)S);
+    if (trace->w) memcpy(trace->w, w, sizeof(float) * (size_t)S);
+  }
+  free(lf); free(lb); free(idx); free(w);
+}
+
+void orc_moe_forward_routed(const orc_cfg* cfg, const orc_weights* wt,
+                            const uint16_t* x, const uint16_t* residual, int T,
+                            const int32_t* idx, const float* w,
+                            uint16_t* out, orc_trace* trace, int nthreads) {
+  if (T <= 0) return;
+  moe_experts_combine(cfg, wt, x, residual, T, idx, w, out, trace, nthreads);
 }

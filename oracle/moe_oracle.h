@@ -137,6 +137,13 @@ void orc_moe_forward(const orc_cfg* cfg, const orc_weights* wt,
                      const uint16_t* x, const uint16_t* residual, int T,
                      uint16_t* out, orc_trace* trace, int nthreads);
 
+/* The expert half with the routing given (idx, w: [T][k]), as the layer after
+ * its top-k (moe_layer.cu:1196-1549).  trace->logits/idx/w are not written. */
+void orc_moe_forward_routed(const orc_cfg* cfg, const orc_weights* wt,
+                            const uint16_t* x, const uint16_t* residual, int T,
+                            const int32_t* idx, const float* w,
+                            uint16_t* out, orc_trace* trace, int nthreads);
+
 /* RMSNorm (rmsnorm.cu:47-83 semantics with an IEEE 1/sqrt): out = bf16(x*inv*w) */
 void orc_rmsnorm(const uint16_t* x, const uint16_t* w, int T, int H, float eps,
                  uint16_t* out);

@@ -75,6 +75,9 @@ def lib():
         L.orc_combine.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P]
         L.orc_moe_forward.argtypes = [ctypes.POINTER(OrcCfg), ctypes.POINTER(OrcWeights), _P, _P, _I,
                                       _P, ctypes.POINTER(OrcTrace), _I]
+        L.orc_moe_forward_routed.argtypes = [ctypes.POINTER(OrcCfg), ctypes.POINTER(OrcWeights), _P, _P, _I,
+                                             _P, _P, _P, ctypes.POINTER(OrcTrace), _I]
+        L.orc_moe_forward_routed.restype = None
         L.orc_rmsnorm.argtypes = [_P, _P, _I, _I, _F, _P]
         _lib = L
     return _lib
@@ -207,6 +210,32 @@ def moe_forward(weights: dict, x, residual, E, k, H, I, alpha=1.702, limit=7.0, 
                                                   "gate_up", "act", "y")])
     lib().orc_moe_forward(ctypes.byref(cfg), ctypes.byref(wt), _ptr(x), _ptr(residual), T, _ptr(out),
                           ctypes.byref(tr) if tr is not None else None, nthreads)
+    if trace:
+        return out, bufs
+    return out
+
+
+def moe_forward_routed(weights: dict, x, residual, idx, w, E, k, H, I, alpha=1.702, limit=7.0, nthreads=0,
+                       trace=False):
+    """The layer's expert half with the routing given (idx int32 [T][k],
+    w float32 [T][k]); weights as moe_forward (router entries unused)."""
+    T = x.shape[0]
+    cfg = OrcCfg(H, E, k, I, alpha, limit, 0, 0)
+    wt = OrcWeights(*[_ptr(weights.get(n)) for n in
+                      ("router_w", "router_b", "w1_packed", "w1_scales", "w1_bias",
+                       "w2_packed", "w2_scales", "w2_bias")])
+    idx = np.ascontiguousarray(idx, np.int32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty((T, H), np.uint16)
+    tr = None
+    bufs = {}
+    if trace:
+        S = T * k
+        bufs = dict(gather_map=np.empty(S, np.int32), gate_up=np.empty((S, 2 * I), np.uint16),
+                    act=np.empty((S, I), np.uint16), y=np.empty((S, H), np.uint16))
+        tr = OrcTrace(None, None, None, None, *[_ptr(bufs[n]) for n in ("gather_map", "gate_up", "act", "y")])
+    lib().orc_moe_forward_routed(ctypes.byref(cfg), ctypes.byref(wt), _ptr(x), _ptr(residual), T, _ptr(idx),
+                                 _ptr(w), _ptr(out), ctypes.byref(tr) if tr is not None else None, nthreads)
     if trace:
         return out, bufs
     return out

@@ -61,3 +61,43 @@ def compare_bf16(got, ref) -> dict:
     return dict(max_abs=float(d.max(initial=0.0)), mean_rel=float((d / denom).mean()) if d.size else 0.0,
                 mismatches=int((np.asarray(got) != np.asarray(ref)).sum()),
                 max_ulps=float((d / ulp_bf16(r)).max(initial=0.0)))
+
+
+def zipf_routing(seed: int, T: int, E: int, k: int, s: float = 1.1):
+    """Skewed routing (BASELINE prefill config): expert popularity
+    p(e) ~ (pi(e)+1)^-s for a seeded permutation pi, k distinct experts per
+    token drawn without replacement (Gumbel top-k, in draw order), weights =
+    softmax of k sorted N(0,1) draws, descending.  Returns int32 [T][k] and
+    float32 [T][k]."""
+    rng = np.random.default_rng([seed, 3])
+    pi = rng.permutation(E)
+    logp = -s * np.log(pi + 1.0)
+    keys = logp[None, :] + rng.gumbel(size=(T, E))
+    top = np.argpartition(-keys, k - 1, axis=1)[:, :k]
+    order = np.argsort(-np.take_along_axis(keys, top, axis=1), axis=1, kind="stable")
+    idx = np.take_along_axis(top, order, axis=1).astype(np.int32)
+    z = -np.sort(-rng.normal(size=(T, k)), axis=1)
+    w = np.exp(z - z[:, :1])
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    return idx, w
+
+
+def mfma_stats(got, ref) -> dict:
+    """Agreement of a matrix-core (reordered fp32 sum) result with the
+    canonical one: NaN positions, max-abs, mean-rel, the fraction of bf16
+    values that differ and the largest difference in bf16 ulps of the
+    reference (one rounding step = 1)."""
+    g = orc.bf16_to_f32(got).astype(np.float64)
+    r = orc.bf16_to_f32(ref).astype(np.float64)
+    nan_ok = bool(np.array_equal(np.isnan(g), np.isnan(r)))
+    f = np.isfinite(r) & np.isfinite(g)
+    inf_ok = bool(np.array_equal(g[~np.isnan(r) & ~f], r[~np.isnan(r) & ~f]))
+    d = np.abs(g[f] - r[f])
+    denom = np.maximum(np.abs(r[f]), 1e-6)
+    return dict(nan_ok=nan_ok, inf_ok=inf_ok, max_abs=float(d.max(initial=0.0)),
+                mean_rel=float((d / denom).mean()) if d.size else 0.0,
+                mismatch_frac=float((np.asarray(got) != np.asarray(ref)).mean()) if d.size else 0.0,
+                over_abs_frac=float((d > 2e-2).mean()) if d.size else 0.0,
+                max_ulps=float((d / ulp_bf16(r[f])).max(initial=0.0)),
+                # largest difference beyond one bf16 step of the reference
+                max_excess=float((d - ulp_bf16(r[f])).max(initial=0.0)))

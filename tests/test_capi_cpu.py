@@ -32,10 +32,11 @@ def test_exports_every_declared_symbol(g):
 
 
 def test_abi_version_and_defaults(g):
-    assert g.lib.gptoss_abi_version() == 1
+    assert g.lib.gptoss_abi_version() == 2
     cfg = g.default_config(128, 64)
     assert (cfg.hidden_size, cfg.num_experts, cfg.top_k, cfg.intermediate_size) == (2880, 128, 4, 2880)
     assert abs(cfg.swiglu_alpha - 1.702) < 1e-6 and cfg.swiglu_limit == 7.0
+    assert cfg.prefill_min_tokens == 128  # decode batches (<= 64) keep the exact kernels
     assert g.lib.gptoss_moe_config_default(None, 128, 1) == g.GPTOSS_ERR_INVALID
     assert b"NULL" in g.lib.gptoss_last_error()
 

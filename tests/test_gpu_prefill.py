@@ -1,0 +1,286 @@
+"""GPU parity of the prefill expert path: grouped MXFP4 GEMMs on the gfx950
+matrix cores (gptoss_moe_grouped_mxfp4_gemm and the layer with
+prefill_min_tokens <= T), against the CPU oracle and against the exact
+decode kernels.
+
+Tolerance.  The matrix core adds the exact products in its own fp32 order,
+so a value differs from the canonical one by the difference of two fp32
+sums (about sqrt(K) * 2^-24 * the partial sums, ~1e-5 here) carried through
+one bf16 rounding.  Each stage is therefore checked against the canonical
+computation of that stage on the GPU's own inputs:
+  * single-rounding outputs (gate_up; expert outputs from the GPU's own
+    activations): within one bf16 step of the reference value plus 2^-9 (the
+    fp32 reordering allowance, which matters only where cancellation leaves
+    a value near zero), differing on a small fraction of the values;
+  * the SwiGLU activations: bit-identical to the oracle's SwiGLU of the
+    GPU's own gate_up values (the epilogue is the same arithmetic);
+  * the layer output: bit-identical to the combine of the GPU's own expert
+    outputs (the same combine kernel as the exact path).
+End to end, the layer output meets the north-star mean-rel 1e-3; the
+max-abs 2e-2 bound holds except where an output moves by whole bf16 steps
+(|out| > 4 has steps >= 2^-5 > 2e-2, so one rounding that goes the other way
+exceeds 2e-2 there; an activation that does moves its whole row of expert
+outputs by up to one activation step times a weight), and the fraction of
+such outputs is bounded.
+No reordering of an fp32 sum, the reference's own hipBLASLt prefill path
+included, can keep every |out| > 4 value within 2e-2 of another order's
+result; the bounds above say how far this one goes.
+"""
+import numpy as np
+import pytest
+
+import moe_data
+from test_gpu_parity import DeviceLayer, dev, host, say
+
+pytestmark = pytest.mark.gpu
+
+MEAN_REL_TOL = 1e-3
+FLIP_FRAC = 2e-3        # fraction of single-rounding values allowed to differ
+REORDER_ABS = 2.0 ** -9  # fp32 reordering allowance beyond one bf16 step
+OUT_OVER_FRAC = 2e-3    # fraction of layer outputs allowed past 2e-2 (whole-step moves)
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+    return torch
+
+
+def check_single_rounding(got, ref, what):
+    c = moe_data.mfma_stats(got, ref)
+    say(what, c)
+    assert c["nan_ok"] and c["inf_ok"], (what, c)
+    assert c["max_excess"] <= REORDER_ABS, (what, c)
+    assert c["mismatch_frac"] <= FLIP_FRAC, (what, c)
+    assert c["mean_rel"] <= MEAN_REL_TOL, (what, c)
+    return c
+
+
+def check_layer_out(got, ref, what):
+    """End-to-end agreement of a layer output with the canonical one."""
+    c = moe_data.mfma_stats(got, ref)
+    say(what, c)
+    assert c["nan_ok"] and c["inf_ok"], (what, c)
+    assert c["mean_rel"] <= MEAN_REL_TOL, (what, c)
+    assert c["over_abs_frac"] <= OUT_OVER_FRAC, (what, c)
+    return c
+
+
+def tiled_experts(gpu, torch, packed, scales, N, K):
+    E = packed.shape[0]
+    nb, sb = gpu.tiled_size(N, K)
+    tn = torch.empty(E * nb, dtype=torch.uint8, device="cuda")
+    ts = torch.empty(E * sb, dtype=torch.uint8, device="cuda")
+    for e in range(E):
+        gpu.pack_tiled(dev(packed[e], torch), dev(scales[e], torch), N, K, tn[e * nb:(e + 1) * nb],
+                       ts[e * sb:(e + 1) * sb])
+    return tn, ts
+
+
+def grouped_case(seed, E, N, K, counts, rows_x, special=False):
+    rng = np.random.default_rng(seed)
+    packed = rng.integers(0, 256, (E, N, K // 2), dtype=np.uint8)
+    scales = rng.integers(119, 124, (E, N, K // 32), dtype=np.uint8)
+    if special:
+        # e8m0 codes 0 (scale +0) and 255 (scale +inf) on a few blocks
+        for e in range(E):
+            scales[e, rng.integers(0, N, 3), rng.integers(0, K // 32, 3)] = 0
+            scales[e, rng.integers(0, N, 2), rng.integers(0, K // 32, 2)] = 255
+    bias = moe_data.bf16(rng.normal(0, 0.5, (E, N)))
+    x = moe_data.bf16(rng.normal(0, 1, (rows_x, K)))
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    rows = int(offsets[-1])
+    row_index = rng.integers(0, rows_x, rows).astype(np.int32)
+    return packed, scales, bias, x, offsets, row_index
+
+
+def oracle_grouped(orc, packed, scales, bias, x, offsets, row_index, N, K):
+    E = packed.shape[0]
+    y = np.zeros((int(offsets[-1]), N), np.uint16)
+    for e in range(E):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if b > a:
+            y[a:b] = orc.mxfp4_gemv(x[row_index[a:b]], packed[e], scales[e], bias[e], N, K)
+    return y
+
+
+@pytest.mark.parametrize("N,K,counts", [
+    (320, 960, [0, 1, 63, 64, 65, 130, 7, 200]),   # partial n-tile, ragged m-tiles, an empty expert
+    (128, 64, [5, 0, 70]),                          # two K blocks (shorter than the load ring)
+    (192, 96, [33, 1]),                             # three K blocks
+    (256, 2880, [129, 3]),                          # the GPT-OSS K
+])
+def test_grouped_gemm_ragged(gpu, orc, torch_mod, N, K, counts):
+    torch = torch_mod
+    E = len(counts)
+    packed, scales, bias, x, offsets, row_index = grouped_case(N + K, E, N, K, counts, rows_x=97)
+    tn, ts = tiled_experts(gpu, torch, packed, scales, N, K)
+    rows = int(offsets[-1])
+    say("grouped", N, K, counts)
+    y = host(gpu.grouped_mxfp4_gemm(dev(x, torch), dev(offsets, torch), tn, ts, N, K, rows,
+                                    bias=dev(bias, torch), row_index=dev(row_index, torch)))
+    ref = oracle_grouped(orc, packed, scales, bias, x, offsets, row_index, N, K)
+    check_single_rounding(y, ref, f"grouped y N={N} K={K}")
+    # identity rows (row_index NULL) read x as the permuted rows themselves
+    xp = moe_data.bf16(np.random.default_rng(5).normal(0, 1, (rows, K)))
+    y2 = host(gpu.grouped_mxfp4_gemm(dev(xp, torch), dev(offsets, torch), tn, ts, N, K, rows, bias=None))
+    ref2 = np.zeros_like(y2)
+    for e in range(E):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if b > a:
+            ref2[a:b] = orc.mxfp4_gemv(xp[a:b], packed[e], scales[e], None, N, K)
+    check_single_rounding(y2, ref2, f"grouped y identity rows N={N} K={K}")
+
+
+@pytest.mark.parametrize("N,K,counts", [(384, 256, [3, 64, 0, 100]), (5760, 2880, [70, 2])])
+def test_grouped_gemm_swiglu(gpu, orc, torch_mod, N, K, counts):
+    torch = torch_mod
+    E = len(counts)
+    packed, scales, bias, x, offsets, row_index = grouped_case(7 * N + K, E, N, K, counts, rows_x=61)
+    tn, ts = tiled_experts(gpu, torch, packed, scales, N, K)
+    rows = int(offsets[-1])
+    gu = torch.empty((rows, N), dtype=torch.bfloat16, device="cuda")
+    act = host(gpu.grouped_mxfp4_gemm(dev(x, torch), dev(offsets, torch), tn, ts, N, K, rows,
+                                      bias=dev(bias, torch), row_index=dev(row_index, torch), swiglu=True,
+                                      gate_up=gu))
+    gu = host(gu)
+    ref_gu = oracle_grouped(orc, packed, scales, bias, x, offsets, row_index, N, K)
+    check_single_rounding(gu, ref_gu, f"grouped gate_up N={N} K={K}")
+    # the epilogue's SwiGLU is the oracle's, bit for bit, on the same gate/up values
+    assert np.array_equal(act, orc.swiglu_rows(gu, N // 2))
+
+
+def test_grouped_gemm_special_scales(gpu, orc, torch_mod):
+    """e8m0 codes 0 and 255 decode as the reference's register path (+0 and
+    +inf scales): NaN / inf positions match the oracle exactly."""
+    torch = torch_mod
+    N, K, counts = 128, 320, [40, 9]
+    packed, scales, bias, x, offsets, row_index = grouped_case(99, 2, N, K, counts, rows_x=40, special=True)
+    tn, ts = tiled_experts(gpu, torch, packed, scales, N, K)
+    rows = int(offsets[-1])
+    y = host(gpu.grouped_mxfp4_gemm(dev(x, torch), dev(offsets, torch), tn, ts, N, K, rows,
+                                    bias=dev(bias, torch), row_index=dev(row_index, torch)))
+    ref = oracle_grouped(orc, packed, scales, bias, x, offsets, row_index, N, K)
+    assert np.isnan(orc.bf16_to_f32(ref)).any()  # +inf-scaled blocks make NaN rows (inf - inf, 0 * inf)
+    check_single_rounding(y, ref, "grouped special scales")
+
+
+def test_grouped_gemm_rejects_bad_arguments(gpu, torch_mod):
+    torch = torch_mod
+    x = torch.zeros((4, 64), dtype=torch.bfloat16, device="cuda")
+    offs = torch.tensor([0, 4], dtype=torch.int32, device="cuda")
+    nb, sb = gpu.tiled_size(64, 64)
+    tn = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+    ts = torch.zeros(sb, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):
+        gpu.grouped_mxfp4_gemm(x, offs, tn, ts, 64, 48, 4)        # K not a multiple of 32
+    with pytest.raises(gpu.GptossError):
+        gpu.grouped_mxfp4_gemm(x, offs, tn, ts, 96, 64, 4)        # N not a multiple of 64
+    with pytest.raises(ValueError):
+        gpu.grouped_mxfp4_gemm(x[:, 1:], offs, tn, ts, 64, 64, 4)  # misaligned x
+
+
+def _layer_trace(gpu, layer, T, k, H, I):
+    tr = layer.trace()
+    S = T * k
+    rd = lambda p, n, dt: gpu.copy_device_to_tensor(p, n * np.dtype(dt).itemsize).cpu().numpy().view(dt)  # noqa
+    return dict(idx=rd(tr.expert_indices, S, np.int32).reshape(T, k),
+                gate_up=rd(tr.gate_up, S * 2 * I, np.uint16).reshape(S, 2 * I),
+                act=rd(tr.act, S * I, np.uint16).reshape(S, I), y=rd(tr.expert_out, S * H, np.uint16).reshape(S, H))
+
+
+def test_layer_prefill_path_vs_oracle(gpu, orc, torch_mod):
+    """Router + top-k + plan + grouped gate_up/SwiGLU + grouped down + combine
+    at T = 300 >= prefill_min_tokens, against the oracle layer."""
+    torch = torch_mod
+    E, k, H, I, T = 16, 4, 256, 320, 300
+    w = moe_data.make_layer(41, E, H, I, bias="random")
+    x, res = moe_data.make_tokens(41, T, H)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T)
+    assert L.layer.cfg.prefill_min_tokens <= T
+    L.layer.set_trace_gate_up(True)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    torch.cuda.synchronize()
+    ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    got = _layer_trace(gpu, L.layer, T, k, H, I)
+    assert np.array_equal(got["idx"], tr["idx"])
+    check_single_rounding(got["gate_up"], tr["gate_up"], "prefill layer gate_up")
+    assert np.array_equal(got["act"], orc.swiglu_rows(got["gate_up"], I))
+    # expert outputs from the GPU's own activations: one rounding step at most
+    ylocal = np.zeros_like(got["y"])
+    offs = np.concatenate([[0], np.cumsum(np.bincount(tr["idx"].ravel(), minlength=E))])
+    for e in range(E):
+        a, b = int(offs[e]), int(offs[e + 1])
+        if b > a:
+            ylocal[a:b] = orc.mxfp4_gemv(got["act"][a:b], w["w2_packed"][e], w["w2_scales"][e], w["w2_bias"][e], H, I)
+    check_single_rounding(got["y"], ylocal, "prefill layer y (same activations)")
+    assert np.array_equal(out, orc.combine(got["y"], tr["gather_map"], tr["w"], res, T, k, H))
+    check_layer_out(out, ref, "prefill layer out")
+
+
+@pytest.fixture(scope="module")
+def zipf120(gpu, torch_mod):
+    """GPT-OSS-120B-shaped layer (E=128, H=I=2880) twice over one tiled
+    weight copy: the matrix-core prefill path and the exact decode path."""
+    torch = torch_mod
+    E, k, H, I, T = 128, 4, 2880, 2880, 4096
+    say("building GPT-OSS-120B-shaped layer for T=4096 prefill")
+    w = moe_data.make_layer(4242, E, H, I, bias="zero")
+    pre = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T, via_tables=False)
+    cfg = gpu.default_config(E, T, prefill_min_tokens=0)
+    exact = gpu.MoELayer().init(cfg, 0, pre.t["router_w"], pre.t.get("router_b"), pre.t.get("w1_bias"),
+                                pre.t.get("w2_bias"), tiled=pre.tiled)
+    torch.cuda.synchronize()
+    return w, pre, exact
+
+
+def test_gptoss120b_prefill_zipf_4096(gpu, orc, torch_mod, zipf120):
+    """BASELINE prefill config: T = 4096, Zipf(1.1) expert popularity, top-4
+    distinct.  Every stage of the matrix-core path against the canonical
+    computation on its own inputs, every output against the exact decode
+    kernels (bit-identical to the oracle), and 32 sampled tokens against the
+    oracle itself."""
+    torch = torch_mod
+    w, pre, exact = zipf120
+    E, k, H, I, T = 128, 4, 2880, 2880, 4096
+    S = T * k
+    x, res = moe_data.make_tokens(4096, T, H)
+    idx, wt = moe_data.zipf_routing(4096, T, E, k)
+    dx, dr, di, dw = dev(x, torch), dev(res, torch), dev(idx, torch), dev(wt, torch)
+    pre.layer.set_trace_gate_up(True)
+    exact.set_trace_gate_up(True)
+    say("prefill T=4096 matrix-core path")
+    out_mc = host(pre.layer.forward_routed(dx, di, dw, residual=dr))
+    tr = pre.layer.trace()
+    rd = lambda p, n, dt: gpu.copy_device_to_tensor(p, n * np.dtype(dt).itemsize).cpu().numpy().view(dt)  # noqa
+    gu_mc = rd(tr.gate_up, S * 2 * I, np.uint16).reshape(S, 2 * I)
+    act_mc_dev = gpu.copy_device_to_tensor(tr.act, S * I * 2).view(torch.bfloat16).reshape(S, I)
+    act_mc = host(act_mc_dev)
+    y_mc = rd(tr.expert_out, S * H, np.uint16).reshape(S, H)
+    gm = rd(tr.gather_map, S, np.int32)
+    offs = rd(tr.expert_offsets, E + 1, np.int32)
+    say("prefill T=4096 exact path")
+    out_ex = host(exact.forward_routed(dx, di, dw, residual=dr))
+    tr_ex = exact.trace()
+    gu_ex = rd(tr_ex.gate_up, S * 2 * I, np.uint16).reshape(S, 2 * I)
+    assert np.array_equal(rd(tr_ex.gather_map, S, np.int32), gm)
+    # stage by stage
+    check_single_rounding(gu_mc, gu_ex, "zipf T=4096 gate_up")
+    assert np.array_equal(act_mc, orc.swiglu_rows(gu_mc, I))
+    n2, s2 = gpu.tiled_size(H, I)
+    y_given = np.empty_like(y_mc)
+    for e in range(E):
+        a, b = int(offs[e]), int(offs[e + 1])
+        if b > a:
+            y_given[a:b] = host(gpu.mxfp4_gemv(act_mc_dev[a:b], pre.tiled[2][e * n2:(e + 1) * n2],
+                                               pre.tiled[3][e * s2:(e + 1) * s2], pre.t["w2_bias"][e], H, I))
+    check_single_rounding(y_mc, y_given, "zipf T=4096 y (same activations)")
+    assert np.array_equal(out_mc, orc.combine(y_mc, gm, wt, res, T, k, H))
+    # end to end
+    check_layer_out(out_mc, out_ex, "zipf T=4096 matrix core vs exact (all outputs)")
+    sel = np.sort(np.random.default_rng(1).choice(T, 32, replace=False))
+    ref = orc.moe_forward_routed(w, x[sel], res[sel], idx[sel], wt[sel], E, k, H, I)
+    assert np.array_equal(out_ex[sel], ref)
+    check_layer_out(out_mc[sel], ref, "zipf T=4096 matrix core vs oracle (32 tokens)")
+    out_mc2 = host(pre.layer.forward_routed(dx, di, dw, residual=dr))
+    assert np.array_equal(out_mc, out_mc2)  # run-to-run deterministic

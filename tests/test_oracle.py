@@ -401,3 +401,30 @@ def test_golden_fixture(orc):
     assert np.array_equal(out, d["out"])
     assert np.array_equal(tr["idx"], d["idx"])
     assert np.array_equal(tr["w"], d["w"])
+
+
+def test_layer_routed_matches_forward_and_is_per_token(orc):
+    """The routed entry (expert half with the routing given) reproduces the
+    full forward on its own routing, and each token's output depends only on
+    that token: a subset of tokens run alone gives the same rows."""
+    E, k, H, I, T = 16, 4, 128, 96, 23
+    w = moe_data.make_layer(8, E, H, I, bias="random")
+    x, res = moe_data.make_tokens(8, T, H)
+    out, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    routed = orc.moe_forward_routed(w, x, res, tr["idx"], tr["w"], E, k, H, I)
+    assert np.array_equal(routed, out)
+    sel = np.array([0, 5, 6, 17, 22])
+    sub = orc.moe_forward_routed(w, x[sel], res[sel], tr["idx"][sel], tr["w"][sel], E, k, H, I)
+    assert np.array_equal(sub, out[sel])
+
+
+def test_zipf_routing_shape():
+    """Prefill routing generator: k distinct experts per token, weights a
+    descending distribution, expert loads skewed (Zipf 1.1 over 128)."""
+    idx, w = moe_data.zipf_routing(3, 4096, 128, 4)
+    assert idx.shape == (4096, 4) and idx.dtype == np.int32
+    s = np.sort(idx, axis=1)
+    assert (s[:, 1:] != s[:, :-1]).all() and idx.min() >= 0 and idx.max() < 128
+    assert np.allclose(w.sum(axis=1), 1.0, atol=1e-6) and (np.diff(w, axis=1) <= 0).all()
+    counts = np.bincount(idx.ravel(), minlength=128)
+    assert counts.sum() == 4096 * 4 and counts.max() > 2000 and counts.min() < 40
