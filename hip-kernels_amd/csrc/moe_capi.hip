@@ -9,6 +9,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -112,6 +113,11 @@ struct gptoss_moe_layer {
   uint16_t* gate_up = nullptr;
   uint16_t* normed = nullptr;
   void* route_scratch = nullptr;
+  int32_t* special1 = nullptr;  // [E] W1 / W2 scales hold e8m0 code 0 or 255
+  int32_t* special2 = nullptr;
+  int special_any1 = 0, special_any2 = 0;
+  int num_cus = 0;
+  int mc_shape[3] = {0, 0, 0};  // matrix-core decode launch shape override
   int n_groups = 0;
   bool trace_gu = false;
   // per-launch timing (gptoss_moe_layer_set_profiling): 4 events per recorded forward
@@ -151,6 +157,7 @@ int gptoss_moe_config_default(gptoss_moe_config* cfg, int num_experts, int max_t
   cfg->logits_fp32 = 0;
   cfg->max_tokens = max_tokens;
   cfg->prefill_min_tokens = 128;
+  cfg->decode_exact = 0;
   return ok();
 }
 
@@ -199,6 +206,8 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   if (cfg->max_tokens < 1) return fail(GPTOSS_ERR_INVALID, "max_tokens=%d must be >= 1", cfg->max_tokens);
   if (cfg->prefill_min_tokens < 0)
     return fail(GPTOSS_ERR_INVALID, "prefill_min_tokens=%d must be >= 0", cfg->prefill_min_tokens);
+  if (cfg->decode_exact != 0 && cfg->decode_exact != 1)
+    return fail(GPTOSS_ERR_INVALID, "decode_exact=%d must be 0 or 1", cfg->decode_exact);
   if (H % kTileRows != 0) return fail(GPTOSS_ERR_UNSUPPORTED, "hidden_size=%d must be a multiple of 64", H);
   int rc = check_mxfp4_shape(2 * I, H);
   if (rc != GPTOSS_OK) return rc;
@@ -287,12 +296,38 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   ALLOC(act, uint16_t*, S * I * 2)
   ALLOC(y, uint16_t*, S * H * 2)
   ALLOC(route_scratch, void*, route_bytes)
+  ALLOC(special1, int32_t*, E * 4)
+  ALLOC(special2, int32_t*, E * 4)
   if (L->norm_w != nullptr) {
     ALLOC(normed, uint16_t*, T * H * 2)
   }
 #undef ALLOC
   hipError_t err = hipMemset(L->route_scratch, 0, route_bytes);
+  if (err == hipSuccess) err = launch_special_scan(L->w1s, 2 * I, H, E, L->special1, nullptr);
+  if (err == hipSuccess) err = launch_special_scan(L->w2s, H, I, E, L->special2, nullptr);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&L->num_cus, hipDeviceAttributeMultiprocessorCount, device_id);
   if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err == hipSuccess) {
+    std::vector<int32_t> f1(E), f2(E);
+    err = hipMemcpy(f1.data(), L->special1, sizeof(int32_t) * E, hipMemcpyDeviceToHost);
+    if (err == hipSuccess) err = hipMemcpy(f2.data(), L->special2, sizeof(int32_t) * E, hipMemcpyDeviceToHost);
+    for (int e = 0; e < E; ++e) {
+      L->special_any1 |= f1[e] != 0;
+      L->special_any2 |= f2[e] != 0;
+    }
+  }
+  // Tuning override of the matrix-core decode launch shape: "P,D,NC" (waves
+  // per work-group, ring depth, 16-token chunks); ignored unless compiled
+  // and fitting both expert matrices.
+  if (const char* ov = getenv("GPTOSS_MOE_DECODE_SHAPE")) {
+    int P = 0, D = 0, NC = 0;
+    if (sscanf(ov, "%d,%d,%d", &P, &D, &NC) == 3 && decode_shape_valid(H / 32, P, D, NC) &&
+        decode_shape_valid(I / 32, P, D, NC)) {
+      L->mc_shape[0] = P;
+      L->mc_shape[1] = D;
+      L->mc_shape[2] = NC;
+    }
+  }
   if (err != hipSuccess) {
     L->release();
     return hip_fail(err, "layer init");
@@ -301,8 +336,9 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   return ok();
 }
 
-// Expert products and combine after the plan (decode: exact weight-streaming
-// kernels; prefill: grouped matrix-core GEMMs).  w: routing weights [T][k].
+// Expert products and combine after the plan (decode: weight-streaming
+// kernels, on the matrix cores or exact; prefill: grouped matrix-core GEMMs).
+// w: routing weights [T][k].
 static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, const float* w,
                          uint16_t* out, int T, hipStream_t s, hipEvent_t* ev) {
   const gptoss_moe_config& c = L->cfg;
@@ -329,6 +365,14 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
   ea.residual = residual;
   ea.out = out;
   ea.max_active = T * c.top_k < c.num_experts ? T * c.top_k : c.num_experts;
+  ea.special1 = L->special1;
+  ea.special2 = L->special2;
+  ea.special_any1 = L->special_any1;
+  ea.special_any2 = L->special_any2;
+  ea.num_cus = L->num_cus;
+  ea.mc_shape[0] = L->mc_shape[0];
+  ea.mc_shape[1] = L->mc_shape[1];
+  ea.mc_shape[2] = L->mc_shape[2];
   if (c.prefill_min_tokens > 0 && T >= c.prefill_min_tokens) {
     GroupedArgs g{};
     g.x = normed;
@@ -359,10 +403,14 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
     g.gate_up = nullptr;
     g.gated = 0;
     HIP_TRY(launch_grouped_mxfp4(g, s), "grouped down launch");
-  } else {
+  } else if (c.decode_exact || !decode_mc_supported(T, c.top_k, c.num_experts, c.hidden_size, c.intermediate_size)) {
     HIP_TRY(launch_w1(ea, s), "w1 launch");
     if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
     HIP_TRY(launch_w2(ea, s), "w2 launch");
+  } else {
+    HIP_TRY(launch_w1_mc(ea, s), "w1 launch");
+    if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
+    HIP_TRY(launch_w2_mc(ea, s), "w2 launch");
   }
   HIP_TRY(launch_combine_slots(ea, s), "combine launch");
   if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");

@@ -1,0 +1,520 @@
+// moe_decode.hip -- decode-path MXFP4 expert products on the gfx950 matrix
+// cores (the default decode path of the layer).
+//
+// Replaces fused_mxfp4_gemv_forward / _multi_forward (fused_mxfp4_gemv.cu:
+// 76-310) with the bias kernels (moe_layer.cu:171-194, 442-473) and
+// swiglu_forward (swiglu.cu:117-211) fused in, as issued per active expert
+// by moe_layer.cu:1316-1487:
+//
+//   mc_stream_kernel<gated>    gate_up: + bias, bf16 gate/up, clamped SwiGLU,
+//                              bf16 activations (permuted slot order)
+//   mc_stream_kernel<!gated>   down: + bias, bf16 expert outputs
+//
+// Decode is HBM-bound: every touched expert's MXFP4 weights are read once
+// and used by its few tokens.  The kernel is therefore a weight stream:
+//
+// * Work items are (active expert, 64-row tile) pairs of the routing plan's
+//   task records; a work-group of P waves takes items v, v + G, ... (G = grid,
+//   v the XCD-grouped block index, so one XCD's work-groups cover a
+//   contiguous item range and share the items' token rows in their L2).
+//   Wave p reduces over K-part p (nb / P blocks of 32); the P partial sums
+//   meet in LDS and are added in part order (deterministic).
+// * Per block, lane l issues one 16-byte nontemporal load of slot l of the
+//   tiled KiB (moe_kernels.h): dword i is the A operand of the 16x16x32 bf16
+//   product of sub-tile i (rows 16 i + l % 16, elements 8 (l/16) .. +7),
+//   one dword of the block's slot-order scales (row 16 i + l % 16 in byte i),
+//   and 16 bytes of its token column's activations (the B operand, shared by
+//   the four sub-tiles).  Decode to bf16 is the scaled fp4 conversion
+//   (exact for codes 1..254; experts holding code 0 or 255 take the exact
+//   special-code decode).
+// * Loads move through a ring of D blocks in VGPRs: consuming block i issues
+//   block i + D, which past the end of the part is block i + D - nb/P of the
+//   work-group's next step, so a wave's stream does not stop between items;
+//   a missing next step reads fixed valid data (static wait counts).
+// * Tokens: a step applies the tile to up to 16 NC of the expert's slots
+//   (NC chunks of 16 token columns); larger experts take further steps.
+//
+// Numerics: products of bf16 activations and exactly decoded weights are
+// exact; sums are fp32 in the matrix core's order and then in part order, so
+// results differ from the canonical (exact VALU) order by fp32 rounding
+// before the bf16 rounding, as the prefill path does.
+#include <type_traits>
+
+#include "moe_device.h"
+#include "moe_kernels.h"
+
+namespace gxmoe {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct McParams {
+  const uint16_t* x;          // gate_up: token rows [T][K]; down: activation rows [S][K] (slot order)
+  const uint8_t* wn;          // tiled nibbles, [E] x g.nib_bytes
+  const uint8_t* ws;          // tiled scales, [E] x g.scale_bytes (slot-order region read)
+  const uint16_t* bias;       // [E][N] or null
+  const int32_t* tasks;       // [max_active][kTaskInts] task records
+  const int32_t* n_active;    // [1]
+  const int32_t* perm_token;  // [S] slot -> token (gate_up)
+  const int32_t* special;     // [E] nonzero: the expert's scales hold code 0 or 255; null: any may
+  uint16_t* out;              // gate_up: activations [S][N/2]; down: expert outputs [S][N]
+  uint16_t* gate_up;          // [S][N] bf16 trace or null (gate_up only)
+  uint32_t wn_bytes, ws_bytes, x_bytes;  // buffer extents (each < 2^32 - 2^16)
+  int slots;                  // S = T * k (gate_up: slot -> token map length)
+  int bpp;                    // blocks per K-part: nb / P, a multiple of D
+  float alpha, limit;
+  TiledGeom g;
+};
+
+constexpr int kLdsSlots = 1024;       // slot -> token map staged in LDS up to this many slots
+constexpr int kBufWord3 = 0x00020000;  // raw buffer, dword data (gfx9 descriptor word 3)
+constexpr int kNT = 2;                 // buffer load cache policy: nontemporal (streamed once)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), kBufWord3);
+}
+
+// LDS-only work-group barrier: orders the LDS traffic of the waves without
+// waiting for their global loads (the weight stream stays in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+struct McStep {
+  int valid, q, t, cg, e, off, M, sp;
+};
+
+// Byte offsets of one step's first block in the three buffers (wave-uniform)
+// plus this lane's B-row offsets.  A missing step points past the end of
+// every buffer with zero strides: its loads return zeros and touch no memory.
+template <int NC>
+struct McSrc {
+  uint32_t a, s, b;          // soffset of block 0
+  uint32_t astr, sstr, bstr; // bytes per block (0 for a missing step)
+  uint32_t vb[NC];           // voffset of this lane's B row in chunk c
+};
+
+// kSpec: some expert's scales hold code 0 or 255, so each step checks its
+// expert's flag (a variant launched only for such weights: the check costs
+// registers in the block loop).  BPP: blocks per K-part when known at compile
+// time (a step is then straight-line code, so the compiler's load waits see
+// exactly which ring slot each block needs); 0 = a.bpp, a multiple of D.
+template <bool kGated, int P, int D, int NC, bool kSpec, int BPP>
+__global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
+  constexpr int kFr = 4 * NC;   // accumulator fragments: (sub-tile, chunk)
+  constexpr int kTok = 16 * NC; // token columns per step
+  constexpr int kRed = P > 1 ? 2 * P * kFr * kWave : 1;
+  constexpr int kOwn = (kFr + P - 1) / P;  // fragments this wave finishes
+  __shared__ int2 hdr[kMaxExperts];
+  __shared__ f32x4 red[kRed];  // [2 buffers][P][kFr][64 lanes]
+  __shared__ int32_t tok[kGated ? kLdsSlots : 1];  // slot -> token (gate_up, S <= kLdsSlots)
+
+  const TiledGeom& g = a.g;
+  const int lane = threadIdx.x & 63;
+  const int p = P > 1 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) : 0;
+  const int K = g.K, N = g.N, nb = g.nb, bpp = BPP > 0 ? BPP : a.bpp;
+  const int ntiles = N / kTileRows;
+  const int G = gridDim.x;  // a multiple of 8: block b runs on XCD b % 8
+  const int vb = static_cast<int>(blockIdx.x);
+  const int v = (vb & 7) * (G >> 3) + (vb >> 3);
+  const int nact = __builtin_amdgcn_readfirstlane(*a.n_active);
+  const int n_items = nact * ntiles;
+  if (v >= n_items) return;  // the whole work-group, before any barrier
+
+  // Task headers: {expert | special << 8 | count << 9, offset}.
+  for (int i = threadIdx.x; i < nact; i += P * kWave) {
+    const int4 h = reinterpret_cast<const int4*>(a.tasks)[static_cast<size_t>(i) * (kTaskInts / 4)];
+    const int sp = a.special ? (a.special[h.x] != 0) : 1;
+    hdr[i] = make_int2(h.x | (sp << 8) | (h.z << 9), h.y);
+  }
+  // The next step's token ids are read while the weight stream is in flight:
+  // from LDS they need no wait on the loads ahead of them (slots <=
+  // kLdsSlots, checked at launch).
+  if constexpr (kGated)
+    for (int i = threadIdx.x; i < a.slots; i += P * kWave) tok[i] = a.perm_token[i];
+  __syncthreads();
+
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(a.wn, a.wn_bytes);
+  const __amdgpu_buffer_rsrc_t rS = make_rsrc(a.ws, a.ws_bytes);
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(a.x, a.x_bytes);
+  const int lo16 = lane & 15, g16 = lane >> 4;
+  const uint32_t voffA = static_cast<uint32_t>(lane) * 16, voffS = static_cast<uint32_t>(lo16) * 4;
+
+  auto step_of = [&](int q, int cg) -> McStep {
+    McStep s;
+    s.valid = q < n_items;
+    s.q = q;
+    const int qq = s.valid ? q : 0;
+    const int j = qq / ntiles;
+    s.t = qq - j * ntiles;
+    s.cg = cg;
+    // LDS values are per-lane to the compiler: make the step scalar
+    const int hx = __builtin_amdgcn_readfirstlane(hdr[j].x);
+    s.e = hx & 0xff;
+    s.sp = (hx >> 8) & 1;
+    s.M = hx >> 9;
+    s.off = __builtin_amdgcn_readfirstlane(hdr[j].y);
+    return s;
+  };
+  auto next_of = [&](const McStep& s) -> McStep {
+    if ((s.cg + 1) * kTok < s.M) return step_of(s.q, s.cg + 1);
+    return step_of(s.q + G, 0);
+  };
+  // Input rows of the B operand for this lane's column of each chunk
+  // (clamped to the expert's last slot): gate_up gathers the slot's token,
+  // down reads the slot's activation row.
+  auto rows_of = [&](const McStep& s, int (&row)[NC]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int slot = s.valid ? s.off + min(s.cg * kTok + 16 * c + lo16, s.M - 1) : 0;
+      if constexpr (kGated) row[c] = s.valid ? tok[slot] : 0;
+      else row[c] = slot;
+    }
+  };
+  auto src_of = [&](const McStep& s, const int (&row)[NC]) -> McSrc<NC> {
+    McSrc<NC> r;
+    const uint32_t blk0 = static_cast<uint32_t>(s.t * nb + p * bpp);
+    r.a = s.valid ? static_cast<uint32_t>(s.e) * static_cast<uint32_t>(g.nib_bytes) + blk0 * 1024u : a.wn_bytes;
+    r.s = s.valid ? static_cast<uint32_t>(s.e) * static_cast<uint32_t>(g.scale_bytes) +
+                        static_cast<uint32_t>(g.mscale_off) + blk0 * 64u
+                  : a.ws_bytes;
+    r.b = s.valid ? static_cast<uint32_t>(p * bpp) * 64u : a.x_bytes;
+    r.astr = s.valid ? 1024u : 0u;
+    r.sstr = s.valid ? 64u : 0u;
+    r.bstr = s.valid ? 64u : 0u;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      r.vb[c] = s.valid ? static_cast<uint32_t>(row[c]) * static_cast<uint32_t>(K) * 2u + 16u * g16 : 0u;
+    return r;
+  };
+
+  gx_u32x4 ra[D];
+  uint32_t rs[D];
+  gx_u32x4 rb[D][NC];
+  auto issue = [&](int u, const McSrc<NC>& s, int blk) __attribute__((always_inline)) {
+    const uint32_t ub = static_cast<uint32_t>(blk);
+    ra[u] = __builtin_amdgcn_raw_buffer_load_b128(rA, voffA, s.a + ub * s.astr, kNT);
+    rs[u] = __builtin_amdgcn_raw_buffer_load_b32(rS, voffS, s.s + ub * s.sstr, kNT);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) rb[u][c] = __builtin_amdgcn_raw_buffer_load_b128(rB, s.vb[c], s.b + ub * s.bstr, 0);
+  };
+
+  McStep cur = step_of(v, 0);
+  McSrc<NC> cs;
+  {
+    int crow[NC];
+    rows_of(cur, crow);
+    cs = src_of(cur, crow);
+  }
+  // the same load order as the steady state, so the waits for the first
+  // step's blocks are as shallow as for every later step
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    issue(u, cs, u);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  f32x4 acc[4][NC];
+  int buf = 0;
+  for (;;) {
+    const McStep nxt = next_of(cur);
+    int nrow[NC];
+    rows_of(nxt, nrow);  // token ids land long before the last group needs them
+    // this step's bias for the fragments this wave finishes (issued ahead
+    // of its uses in the epilogue): fragment f = j P + p, sub-tile f % 4
+    uint2 braw[kOwn];
+    {
+      const int n0 = cur.t * kTileRows + 4 * g16;
+#pragma unroll
+      for (int j = 0; j < kOwn; ++j) {
+        const int i = (j * P + p) & 3;
+        braw[j] = a.bias ? *reinterpret_cast<const uint2*>(a.bias + static_cast<size_t>(cur.e) * N + n0 + 16 * i)
+                         : make_uint2(0u, 0u);
+      }
+    }
+    const int ncl = NC == 1 ? 1 : min(NC, (cur.M - cur.cg * kTok + 15) >> 4);  // chunks with a live column
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const McSrc<NC> ns = src_of(nxt, nrow);
+
+    // The blocks of this step; the branch on the expert's special-code flag
+    // is taken once per step, so the block loop itself has no branches.
+    auto run = [&](auto SPC) __attribute__((always_inline)) {
+      constexpr bool kSp = decltype(SPC)::value;
+      auto consume = [&](int u) __attribute__((always_inline)) {
+        const uint32_t sc = rs[u];
+        gx_bf16x8 av[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t code = (sc >> (8 * i)) & 0xffu;
+          if constexpr (kSp) av[i] = decode8_bf16_special(ra[u][i], code);
+          else av[i] = decode8_bf16(ra[u][i], __uint_as_float(code << 23));
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          if (NC == 1 || c < ncl) {
+            const gx_bf16x8 bv = __builtin_bit_cast(gx_bf16x8, rb[u][c]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv, acc[i][c], 0, 0, 0);
+          }
+        }
+      };
+      if constexpr (BPP > 0) {
+        // block i refills its slot with block i + D, of the next step past the end
+#pragma unroll
+        for (int i = 0; i < BPP; ++i) {
+          consume(i % D);
+          if (i + D < BPP) issue(i % D, cs, i + D);
+          else issue(i % D, ns, i + D - BPP);
+          __builtin_amdgcn_sched_barrier(0);  // keep the ring order: one block decoded at a time
+        }
+      } else {
+        for (int i0 = 0; i0 < bpp - D; i0 += D) {
+#pragma unroll
+          for (int u = 0; u < D; ++u) {
+            consume(u);
+            issue(u, cs, i0 + u + D);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        // last group: its refills are the next step's first D blocks
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+          consume(u);
+          issue(u, ns, u);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    if constexpr (kSpec) {
+      if (cur.sp) run(std::true_type{});
+      else run(std::false_type{});
+    } else {
+      run(std::false_type{});
+    }
+
+    // Epilogue: fragment (i, c) of lane l is rows t*64 + 16 i + 4 (l/16) + r,
+    // r = 0..3, of the step's column 16 c + l % 16.
+    auto emit = [&](int i, int c, const uint2 bb, const f32x4& sum) __attribute__((always_inline)) {
+      const int m = cur.cg * kTok + 16 * c + lo16;
+      if (m >= cur.M) return;
+      const size_t slot = static_cast<size_t>(cur.off) + m;
+      const int n = cur.t * kTileRows + 16 * i + 4 * g16;
+      uint16_t y[4];
+      y[0] = f32_to_bf16(sum[0] + bf16_to_f32(static_cast<uint16_t>(bb.x)));
+      y[1] = f32_to_bf16(sum[1] + bf16_to_f32(static_cast<uint16_t>(bb.x >> 16)));
+      y[2] = f32_to_bf16(sum[2] + bf16_to_f32(static_cast<uint16_t>(bb.y)));
+      y[3] = f32_to_bf16(sum[3] + bf16_to_f32(static_cast<uint16_t>(bb.y >> 16)));
+      if constexpr (kGated) {
+        // rows n, n+2 are gate (even), n+1, n+3 up (odd)
+        const uint16_t a0 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[0]), bf16_to_f32(y[1]), a.alpha, a.limit));
+        const uint16_t a1 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[2]), bf16_to_f32(y[3]), a.alpha, a.limit));
+        *reinterpret_cast<uint32_t*>(a.out + slot * (N / 2) + n / 2) = a0 | (static_cast<uint32_t>(a1) << 16);
+        if (a.gate_up)
+          *reinterpret_cast<uint2*>(a.gate_up + slot * N + n) =
+              make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
+      } else {
+        *reinterpret_cast<uint2*>(a.out + slot * N + n) =
+            make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
+      }
+    };
+    if constexpr (P == 1) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        if (NC == 1 || c < ncl)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) emit(i, c, braw[4 * c + i], acc[i][c]);
+    } else {
+      // Partial sums through LDS; fragment f = 4 c + i is finished by wave
+      // f % P, adding the parts in order.  Two buffers: a step's writes never
+      // meet the previous step's reads (a barrier separates them).
+      f32x4* rb0 = red + static_cast<size_t>(buf) * P * kFr * kWave;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rb0[(p * kFr + 4 * c + i) * kWave + lane] = acc[i][c];
+      lds_barrier();
+#pragma unroll
+      for (int j = 0; j < kOwn; ++j) {
+        const int f = j * P + p;
+        if (f < kFr && (f >> 2) < ncl) {
+          f32x4 sum = rb0[f * kWave + lane];
+#pragma unroll
+          for (int pp = 1; pp < P; ++pp) sum = sum + rb0[(pp * kFr + f) * kWave + lane];
+          emit(f & 3, f >> 2, braw[j], sum);
+        }
+      }
+      buf ^= 1;
+    }
+    if (!nxt.valid) break;
+    cur = nxt;
+    cs = ns;
+  }
+}
+
+// Per-expert flag: does the slot-order scale region hold code 0 or 255?
+__global__ void special_scan_kernel(const uint8_t* __restrict__ ws, TiledGeom g, int E, int32_t* __restrict__ flags) {
+  const size_t per = static_cast<size_t>(g.N) * g.nb / 16;  // 16-byte words per expert (N*nb is a multiple of 64)
+  const size_t total = per * E;
+  for (size_t q = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; q < total;
+       q += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t e = q / per, w = q % per;
+    const uint4 v = reinterpret_cast<const uint4*>(ws + e * g.scale_bytes + g.mscale_off)[w];
+    if (has_special_code(v.x, 0xffffffffu) || has_special_code(v.y, 0xffffffffu) ||
+        has_special_code(v.z, 0xffffffffu) || has_special_code(v.w, 0xffffffffu))
+      atomicOr(&flags[e], 1);
+  }
+}
+
+template <bool kGated, int P, int D, int NC, bool kSpec, int BPP>
+hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_t s) {
+  static const int per_cu = [] {  // resident work-groups per CU (a property of the kernel)
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mc_stream_kernel<kGated, P, D, NC, kSpec, BPP>, P * kWave,
+                                                     0) != hipSuccess ||
+        n < 1)
+      n = 1;
+    return n;
+  }();
+  const long resident = static_cast<long>(per_cu) * (num_cus > 0 ? num_cus : 256);
+  long grid = max_items < resident ? max_items : resident;
+  grid = (grid + 7) & ~7L;  // a multiple of 8 for the XCD-grouped block order
+  McParams q = p;
+  q.bpp = p.g.nb / P;
+  hipLaunchKernelGGL((mc_stream_kernel<kGated, P, D, NC, kSpec, BPP>), dim3(static_cast<unsigned>(grid)),
+                     dim3(P * kWave), 0, s, q);
+  return hipGetLastError();
+}
+
+// The compiled launch shapes: (waves per work-group = K-parts, ring depth in
+// blocks, 16-token chunks per step).  GPT-OSS (K = 2880, 90 blocks per row)
+// runs straight-line steps of 90 / P blocks; other K take the generic block
+// loop (P = 1, D dividing K / 32).
+constexpr int kNbGptOss = 90;
+#define GX_MC_SHAPES(X) \
+  X(6, 15, 1)           \
+  X(6, 5, 1)            \
+  X(3, 10, 1)           \
+  X(3, 5, 1)            \
+  X(2, 9, 1)            \
+  X(2, 15, 1)           \
+  X(1, 9, 1)            \
+  X(2, 9, 2)
+#define GX_MC_GENERIC(X) \
+  X(1, 4, 1)             \
+  X(1, 3, 1)             \
+  X(1, 2, 1)             \
+  X(1, 1, 1)
+
+bool shape_compiled(int nb, int P, int D, int NC) {
+#define GX_MC_IS(p_, d_, nc_) \
+  if (nb == kNbGptOss && P == p_ && D == d_ && NC == nc_) return true;
+  GX_MC_SHAPES(GX_MC_IS)
+#undef GX_MC_IS
+#define GX_MC_IS(p_, d_, nc_) \
+  if (P == p_ && D == d_ && NC == nc_ && nb % D == 0) return true;
+  GX_MC_GENERIC(GX_MC_IS)
+#undef GX_MC_IS
+  return false;
+}
+
+template <bool kGated>
+hipError_t launch_mc_shape(const McParams& p, int P, int D, int NC, int max_items, int num_cus, hipStream_t s) {
+  if (p.g.nb == kNbGptOss) {
+#define GX_MC_GO(p_, d_, nc_) \
+  if (P == p_ && D == d_ && NC == nc_)  \
+    return launch_mc_t<kGated, p_, d_, nc_, false, kNbGptOss / p_>(p, max_items, num_cus, s);
+    GX_MC_SHAPES(GX_MC_GO)
+#undef GX_MC_GO
+  }
+#define GX_MC_GO(p_, d_, nc_) \
+  if (P == p_ && D == d_ && NC == nc_) return launch_mc_t<kGated, p_, d_, nc_, false, 0>(p, max_items, num_cus, s);
+  GX_MC_GENERIC(GX_MC_GO)
+#undef GX_MC_GO
+  return hipErrorInvalidValue;
+}
+
+// Default shape for nb blocks and S routed slots: small batches split K over
+// more waves (more work-groups in flight for few items), large batches fewer.
+void pick_shape(int nb, int S, int& P, int& D, int& NC) {
+  NC = 1;
+  if (nb == kNbGptOss) {
+    if (S <= 16) { P = 6; D = 15; }
+    else if (S <= 64) { P = 3; D = 10; }
+    else { P = 2; D = 9; }
+    return;
+  }
+  P = 1;
+  D = nb % 4 == 0 ? 4 : nb % 3 == 0 ? 3 : nb % 2 == 0 ? 2 : 1;
+}
+
+hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
+  if (a.T <= 0 || a.max_active <= 0) return hipSuccess;
+  const TiledGeom g = gated ? tiled_geom(2 * a.I, a.H) : tiled_geom(a.H, a.I);
+  McParams p{};
+  p.x = gated ? a.x : a.act;
+  p.wn = gated ? a.w1n : a.w2n;
+  p.ws = gated ? a.w1s : a.w2s;
+  p.bias = gated ? a.b1 : a.b2;
+  p.tasks = a.plan.tasks;
+  p.n_active = a.plan.n_active;
+  p.perm_token = a.plan.perm_token;
+  p.special = gated ? a.special1 : a.special2;
+  p.out = gated ? a.act : a.y;
+  p.gate_up = gated ? a.gate_up : nullptr;
+  p.alpha = a.alpha;
+  p.limit = a.limit;
+  p.slots = a.T * a.k;
+  p.g = g;
+  if (p.slots > kLdsSlots) return hipErrorInvalidValue;  // decode_mc_supported() is false
+  const size_t wn_bytes = g.nib_bytes * a.E, ws_bytes = g.scale_bytes * a.E;
+  const size_t x_bytes = static_cast<size_t>(gated ? a.T : a.T * a.k) * g.K * 2;
+  constexpr size_t kMaxBuf = 0xffff0000u;  // offsets + lane terms stay below 2^32
+  if (wn_bytes > kMaxBuf || ws_bytes > kMaxBuf || x_bytes > kMaxBuf) return hipErrorInvalidValue;
+  p.wn_bytes = static_cast<uint32_t>(wn_bytes);
+  p.ws_bytes = static_cast<uint32_t>(ws_bytes);
+  p.x_bytes = static_cast<uint32_t>(x_bytes);
+  int P, D, NC;
+  pick_shape(g.nb, a.T * a.k, P, D, NC);
+  if (a.mc_shape[0] > 0 && shape_compiled(g.nb, a.mc_shape[0], a.mc_shape[1], a.mc_shape[2])) {
+    P = a.mc_shape[0];
+    D = a.mc_shape[1];
+    NC = a.mc_shape[2];
+  }
+  const int max_items = a.max_active * (g.N / kTileRows);
+  if (gated ? a.special_any1 : a.special_any2)  // weights with e8m0 code 0 or 255: the checking variant
+    return gated ? launch_mc_t<true, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s)
+                 : launch_mc_t<false, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s);
+  return gated ? launch_mc_shape<true>(p, P, D, NC, max_items, a.num_cus, s)
+               : launch_mc_shape<false>(p, P, D, NC, max_items, a.num_cus, s);
+}
+
+}  // namespace
+
+hipError_t launch_w1_mc(const ExpertArgs& a, hipStream_t s) { return launch_mc(a, true, s); }
+hipError_t launch_w2_mc(const ExpertArgs& a, hipStream_t s) { return launch_mc(a, false, s); }
+
+bool decode_shape_valid(int nb, int P, int D, int NC) { return shape_compiled(nb, P, D, NC); }
+
+bool decode_mc_supported(int T, int k, int E, int H, int I) {
+  const TiledGeom g1 = tiled_geom(2 * I, H), g2 = tiled_geom(H, I);
+  constexpr size_t kMaxBuf = 0xffff0000u;
+  return T * k <= kLdsSlots && g1.nib_bytes * E <= kMaxBuf && g1.scale_bytes * E <= kMaxBuf &&
+         g2.nib_bytes * E <= kMaxBuf && g2.scale_bytes * E <= kMaxBuf &&
+         static_cast<size_t>(T) * k * I * 2 <= kMaxBuf && static_cast<size_t>(T) * H * 2 <= kMaxBuf;
+}
+
+hipError_t launch_special_scan(const uint8_t* ws, int N, int K, int E, int32_t* flags, hipStream_t s) {
+  const TiledGeom g = tiled_geom(N, K);
+  hipError_t err = hipMemsetAsync(flags, 0, sizeof(int32_t) * E, s);
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(special_scan_kernel, dim3(1024), dim3(256), 0, s, ws, g, E, flags);
+  return hipGetLastError();
+}
+
+}  // namespace gxmoe

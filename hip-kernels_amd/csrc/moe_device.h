@@ -115,6 +115,60 @@ __device__ __forceinline__ bool has_special_code(uint32_t v, uint32_t mask) {
   return (((x - 0x01010101u) & ~x & 0x80808080u) | ((y - 0x01010101u) & ~y & 0x80808080u)) != 0u;
 }
 
+typedef uint32_t gx_u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 gx_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 gx_bf16x2 __attribute__((ext_vector_type(2)));
+
+// Row r's 16 bytes of one tiled MXFP4 block (layout in moe_kernels.h), given
+// p = &block[tiled_dword(r, 0)]: dword g is slot 16 g + r % 16, 64 dwords
+// after dword g - 1.  Nontemporal: streamed weights are read once.
+__device__ __forceinline__ gx_u32x4 load_row_block_nt(const uint32_t* p) {
+  gx_u32x4 v;
+  v[0] = __builtin_nontemporal_load(p);
+  v[1] = __builtin_nontemporal_load(p + 64);
+  v[2] = __builtin_nontemporal_load(p + 128);
+  v[3] = __builtin_nontemporal_load(p + 192);
+  return v;
+}
+
+__device__ __forceinline__ gx_u32x4 load_row_block(const uint32_t* p) {
+  gx_u32x4 v;
+  v[0] = p[0];
+  v[1] = p[64];
+  v[2] = p[128];
+  v[3] = p[192];
+  return v;
+}
+
+// Eight e2m1 values (one dword, low nibble first) times the e8m0 scale as
+// bf16, for a scale from a code in 1..254: the gfx950 scaled conversion is
+// exact (e2m1 x 2^(code-127) has at most two significant bits).
+__device__ __forceinline__ gx_bf16x8 decode8_bf16(uint32_t d, float scale) {
+  const gx_bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0);
+  const gx_bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1);
+  const gx_bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2);
+  const gx_bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3);
+  const gx_u32x4 w{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1), __builtin_bit_cast(uint32_t, p2),
+                   __builtin_bit_cast(uint32_t, p3)};
+  return __builtin_bit_cast(gx_bf16x8, w);
+}
+
+// decode8_bf16 for any code (a zero-extended byte).  Codes 0 and 255 follow
+// the reference's register decode (scale code << 23: +0 and +inf, so +-0,
+// +-inf and NaN for 0 x inf), built from the exact e2m1 values.
+__device__ __forceinline__ gx_bf16x8 decode8_bf16_special(uint32_t d, uint32_t code) {
+  const float scale = __uint_as_float(code << 23);
+  float w[8];
+  fp4x2_to_f32<0>(d, 1.0f, w[0], w[1]);
+  fp4x2_to_f32<1>(d, 1.0f, w[2], w[3]);
+  fp4x2_to_f32<2>(d, 1.0f, w[4], w[5]);
+  fp4x2_to_f32<3>(d, 1.0f, w[6], w[7]);
+  gx_bf16x8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = __builtin_bit_cast(__bf16, f32_to_bf16(w[j] * scale));
+  return r;
+}
+
 // 64-lane xor butterfly sum: after it every lane holds the same value, the
 // tree v[l] + v[l^m] for m = 32, 16, 8, 4, 2, 1.
 __device__ __forceinline__ float wave_butterfly_sum(float v) {

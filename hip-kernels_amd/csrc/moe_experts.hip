@@ -14,11 +14,11 @@
 // (active expert, tile group) items of the routing plan's task records, so
 // the weights stream without a gap between items (see expert_stream_kernel).
 //
-// Memory layout (tiled MXFP4, built once by pack_nib/pack_scale): for each
-// expert, each 64-row tile holds nb = K/32 blocks of [64 lanes][16 bytes]
-// (one 32-element MXFP4 block of row tile*64+lane per lane), so one wave's
-// 16-byte loads of block b are one contiguous 1 KiB.  Scales of each
-// (tile, part, lane) are one contiguous group of `spad` bytes (bpp used).
+// Memory layout (tiled MXFP4, built once by pack_nib/pack_scale; TiledGeom
+// in moe_kernels.h): for each expert, each 64-row tile holds nb = K/32 blocks
+// of one KiB; lane l's row block is the four dwords tiled_dword(l, 0..3) of
+// it, so one wave's loads of block b cover one contiguous KiB.  Scales of
+// each (tile, part, lane) are one contiguous group of `spad` bytes (bpp used).
 //
 // Arithmetic (the canonical expert dot): lane = row, wave = K-part; each
 // lane runs one ascending fmaf chain over its part; the P part sums are added
@@ -42,7 +42,8 @@ TiledGeom tiled_geom(int N, int K) {
   g.bpp = g.nb / g.parts;
   g.spad = (g.bpp + 3) & ~3;
   g.nib_bytes = static_cast<size_t>(N) * K / 2;
-  g.scale_bytes = static_cast<size_t>(N / kTileRows) * g.parts * kTileRows * g.spad;
+  g.mscale_off = static_cast<size_t>(N / kTileRows) * g.parts * kTileRows * g.spad;
+  g.scale_bytes = g.mscale_off + static_cast<size_t>(N) * g.nb;
   return g;
 }
 
@@ -202,15 +203,16 @@ void expert_stream_kernel(StreamParams a) {
   if constexpr (kGated && kTok > 1)
     if (static_cast<int>(threadIdx.x) < a.slots) tv = a.perm_token[threadIdx.x];
 
-  // Per-step addresses.  An invalid step points every load at fixed valid
-  // data (expert 0, tile 0, input row 0) with a zero block stride.
-  auto wsrc = [&](const Step& s, int r, int& stride) -> const u32x4* {
-    stride = s.valid ? kTileRows : 0;
+  // Per-step addresses (dwords; a block is 256 of them).  An invalid step
+  // points every load at fixed valid data (expert 0, tile 0, input row 0)
+  // with a zero block stride.
+  auto wsrc = [&](const Step& s, int r, int& stride) -> const uint32_t* {
+    stride = s.valid ? 256 : 0;
     const int t = s.valid ? min(s.tp * R + r, ntiles - 1) : 0;
     const int pp = s.valid ? p : 0;
     const size_t eoff = s.valid ? static_cast<size_t>(s.e) * g.nib_bytes : 0;
-    return reinterpret_cast<const u32x4*>(a.wn + eoff + static_cast<size_t>(t) * tile_bytes) +
-           static_cast<size_t>(pp) * bpp * kTileRows + lane;
+    return reinterpret_cast<const uint32_t*>(a.wn + eoff + static_cast<size_t>(t) * tile_bytes) +
+           static_cast<size_t>(pp) * bpp * 256 + tiled_dword(lane, 0);
   };
   auto ssrc = [&](const Step& s, int r) -> const uint32_t* {
     const int t = s.valid ? min(s.tp * R + r, ntiles - 1) : 0;
@@ -287,10 +289,10 @@ void expert_stream_kernel(StreamParams a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       int stride;
-      const u32x4* src = wsrc(cur, r, stride);
+      const uint32_t* src = wsrc(cur, r, stride);
 #pragma unroll
       for (int i = 0; i < kD; ++i)
-        if (BPP || i < bpp) ring[r][i] = __builtin_nontemporal_load(src + static_cast<size_t>(i) * stride);
+        if (BPP || i < bpp) ring[r][i] = load_row_block_nt(src + static_cast<size_t>(i) * stride);
     }
   }
   if (static_cast<int>(threadIdx.x) < kMaxExperts)
@@ -349,8 +351,8 @@ void expert_stream_kernel(StreamParams a) {
     const int mc = __builtin_amdgcn_readfirstlane(min(TC, cur.M - cur.c * TC));
     const float(*sx)[PK] = sm.x[p];
     int cstride[R], nstride[R];
-    const u32x4* csrc[R];
-    const u32x4* nsrc[R];
+    const uint32_t* csrc[R];
+    const uint32_t* nsrc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       csrc[r] = wsrc(cur, r, cstride[r]);
@@ -427,10 +429,10 @@ void expert_stream_kernel(StreamParams a) {
       for (int r = 0; r < R; ++r) {
         if (ni < kLoop) {
           if (BPP || ni < bpp)
-            ring[r][i % kD] = __builtin_nontemporal_load(csrc[r] + static_cast<size_t>(ni) * cstride[r]);
+            ring[r][i % kD] = load_row_block_nt(csrc[r] + static_cast<size_t>(ni) * cstride[r]);
         } else {
           if (BPP || ni - kLoop < bpp)
-            ring[r][i % kD] = __builtin_nontemporal_load(nsrc[r] + static_cast<size_t>(ni - kLoop) * nstride[r]);
+            ring[r][i % kD] = load_row_block_nt(nsrc[r] + static_cast<size_t>(ni - kLoop) * nstride[r]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -522,13 +524,21 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* __restric
   *reinterpret_cast<uint4*>(out + static_cast<size_t>(t) * H + c * 8) = o;
 }
 
-__global__ void pack_nib_kernel(const uint4* __restrict__ src, int N, int nb, uint4* __restrict__ dst) {
+// Row-major [N][K/2] nibbles -> tiled: one thread per (row, block), its 16
+// bytes to the four dwords tiled_dword(row % 64, g).
+__global__ void pack_nib_kernel(const uint4* __restrict__ src, int N, int nb, uint32_t* __restrict__ dst) {
   const size_t total = static_cast<size_t>(N) * nb;
   for (size_t q = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; q < total;
        q += static_cast<size_t>(gridDim.x) * blockDim.x) {
     const size_t row = q / nb, b = q % nb;
-    const size_t tile = row / kTileRows, lane = row % kTileRows;
-    dst[(tile * nb + b) * kTileRows + lane] = src[q];
+    const size_t tile = row / kTileRows;
+    const int r = static_cast<int>(row % kTileRows);
+    uint32_t* blk = dst + (tile * nb + b) * 256;
+    const uint4 v = src[q];
+    blk[tiled_dword(r, 0)] = v.x;
+    blk[tiled_dword(r, 1)] = v.y;
+    blk[tiled_dword(r, 2)] = v.z;
+    blk[tiled_dword(r, 3)] = v.w;
   }
 }
 
@@ -541,6 +551,20 @@ __global__ void pack_scale_kernel(const uint8_t* __restrict__ src, int N, TiledG
     const size_t row = tile * kTileRows + lane;
     for (int i = 0; i < g.spad; ++i)
       dst[q * g.spad + i] = (i < g.bpp) ? src[row * g.nb + p * g.bpp + i] : 0;
+  }
+}
+
+// Scales in the slot order of the nibbles: per (tile, block) 64 bytes, byte
+// 4 j + i = row 64 t + 16 i + j.  One thread per output byte.
+__global__ void pack_mscale_kernel(const uint8_t* __restrict__ src, int N, int nb, uint8_t* __restrict__ dst) {
+  const size_t total = static_cast<size_t>(N) * nb;
+  for (size_t q = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; q < total;
+       q += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t tb = q >> 6;
+    const int o = static_cast<int>(q & 63);
+    const size_t tile = tb / nb, b = tb % nb;
+    const size_t row = tile * kTileRows + 16 * (o & 3) + (o >> 2);
+    dst[q] = src[row * nb + b];
   }
 }
 
@@ -623,10 +647,13 @@ hipError_t launch_pack_tiled(const uint8_t* packed, const uint8_t* scales, int N
                              uint8_t* tiled_nib, uint8_t* tiled_scales, hipStream_t s) {
   const TiledGeom g = tiled_geom(N, K);
   hipLaunchKernelGGL(pack_nib_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const uint4*>(packed), N, g.nb,
-                     reinterpret_cast<uint4*>(tiled_nib));
+                     reinterpret_cast<uint32_t*>(tiled_nib));
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(pack_scale_kernel, dim3(256), dim3(256), 0, s, scales, N, g, tiled_scales);
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(pack_mscale_kernel, dim3(512), dim3(256), 0, s, scales, N, g.nb, tiled_scales + g.mscale_off);
   return hipGetLastError();
 }
 

@@ -26,6 +26,19 @@ inline int dot_parts(int K) {
 }
 
 // Tiled MXFP4 geometry of one [N, K] matrix.
+//
+// Nibbles: per 64-row tile t and 32-element block b, one KiB at
+// (t * nb + b) * 1024 of [64 slots][4 dwords].  Slot s = 16 g + j holds, in
+// dword i, bytes 4g..4g+3 (elements 8g..8g+7, low nibble first) of row
+// 64 t + 16 i + j's block b.  A wave's 16-byte load of slot `lane` is then
+// the A operand of four 16x16x32 matrix-core products (sub-tiles i = 0..3)
+// for one block, and row r's 16 bytes are the dwords (16 g + r % 16, r / 16).
+//
+// Scales, two regions per matrix:
+//   [0, mscale_off): per (tile, K-part, row) one group of spad e8m0 bytes
+//     (the part's blocks, zero-padded), the order the exact kernels read;
+//   [mscale_off, scale_bytes): per (tile, block) 64 bytes, byte 4 j + i =
+//     the scale of row 64 t + 16 i + j, the order of the nibble slots.
 struct TiledGeom {
   int N, K;
   int nb;      // K / 32 blocks per row
@@ -33,9 +46,14 @@ struct TiledGeom {
   int bpp;     // blocks per part
   int spad;    // scale bytes per (tile, part, lane), multiple of 4
   size_t nib_bytes;    // N * K / 2
-  size_t scale_bytes;  // (N/64) * parts * 64 * spad
+  size_t mscale_off;   // (N/64) * parts * 64 * spad
+  size_t scale_bytes;  // mscale_off + N * nb
 };
 TiledGeom tiled_geom(int N, int K);
+
+// Dword index (within one 64-row tile's block KiB) of dword g of row r's
+// 16-byte block: slot 16 g + r % 16, dword r / 16.
+__host__ __device__ constexpr int tiled_dword(int r, int g) { return (16 * g + (r & 15)) * 4 + (r >> 4); }
 
 // Routing plan produced on the device.
 struct PlanBufs {
@@ -99,12 +117,31 @@ struct ExpertArgs {
   const uint16_t* residual;   // [T][H] or null
   uint16_t* out;              // [T][H]
   int max_active;             // grid bound on active experts: min(E, T*k)
+  // matrix-core decode (launch_w1_mc / launch_w2_mc)
+  const int32_t* special1;    // [E] W1 scales hold code 0 or 255 (launch_special_scan), or null
+  const int32_t* special2;    // [E] same for W2
+  int special_any1, special_any2;  // any flag set (read back at layer init)
+  int num_cus;                // compute units of the device (persistent grid size)
+  int mc_shape[3];            // {P, D, NC} launch shape override, {0,0,0} = automatic
 };
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
 // The two launches of launch_experts, for callers that time them separately.
 hipError_t launch_w1(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_w2(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_combine_slots(const ExpertArgs& a, hipStream_t s);
+// The decode expert products on the matrix cores (moe_decode.hip): same
+// outputs as launch_w1 / launch_w2 up to fp32 summation order.
+hipError_t launch_w1_mc(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_w2_mc(const ExpertArgs& a, hipStream_t s);
+// Can the matrix-core decode kernels run T tokens of this layer shape?
+// (At most 1024 routed slots, so the slot -> token map fits LDS, and every
+// weight and activation buffer below 4 GiB for 32-bit buffer offsets.)
+bool decode_mc_supported(int T, int k, int E, int H, int I);
+// Is {P, D, NC} a compiled matrix-core decode shape that fits nb blocks?
+bool decode_shape_valid(int nb, int P, int D, int NC);
+// flags[e] = 1 if expert e's slot-order scales (tiled_geom(N, K)) hold an
+// e8m0 code 0 or 255, else 0.
+hipError_t launch_special_scan(const uint8_t* ws, int N, int K, int E, int32_t* flags, hipStream_t s);
 
 // Grouped MXFP4 product on the matrix cores (prefill): for each expert e and
 // permuted position p in [offsets[e], offsets[e+1]),

@@ -27,7 +27,7 @@
 // accumulator layout gives each lane four consecutive weight rows of one
 // token, so the interleaved gate/up pairs meet in one lane.  The K order
 // inside an MFMA is a permutation shared by both operands: lane half h takes
-// elements 16h..16h+15 of each 32-element block (8 contiguous bytes of the
+// elements 16h..16h+15 of each 32-element block (dwords 2h, 2h+1 of the
 // tiled row block), elements 16h+8s..16h+8s+7 in k16 step s.
 //
 // Numerics: products are exact, sums are fp32 in the matrix core's order, so
@@ -42,8 +42,7 @@
 namespace gxmoe {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef gx_bf16x8 bf16x8_t;
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -113,32 +112,6 @@ __device__ __forceinline__ void find_mtile(const int32_t* __restrict__ offsets, 
   cnt = offsets[e + 1] - off;
 }
 
-// Eight e2m1 values (one dword, low nibble first) times the e8m0 scale
-// `code` as bf16.  Codes 1..254: the scaled conversion is exact.  Codes 0
-// and 255 follow the reference's register decode (scale code << 23: +0 and
-// +inf, so +-0, +-inf and NaN for 0 x inf), built from the exact values.
-__device__ __forceinline__ bf16x8_t decode8_bf16(uint32_t d, float scale) {
-  const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0);
-  const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1);
-  const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2);
-  const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3);
-  return bf16x8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-}
-
-// `code` is a zero-extended byte.
-__device__ __forceinline__ bf16x8_t decode8_bf16_special(uint32_t d, uint32_t code) {
-  const float scale = __uint_as_float(code << 23);
-  float w[8];
-  fp4x2_to_f32<0>(d, 1.0f, w[0], w[1]);
-  fp4x2_to_f32<1>(d, 1.0f, w[2], w[3]);
-  fp4x2_to_f32<2>(d, 1.0f, w[4], w[5]);
-  fp4x2_to_f32<3>(d, 1.0f, w[6], w[7]);
-  bf16x8_t r;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = __builtin_bit_cast(__bf16, f32_to_bf16(w[j] * scale));
-  return r;
-}
-
 template <bool kGated>
 __global__ __launch_bounds__(kGW * kWave) void grouped_mfma_kernel(GroupedParams a) {
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kStageBytes];
@@ -168,11 +141,14 @@ __global__ __launch_bounds__(kGW * kWave) void grouped_mfma_kernel(GroupedParams
   const uint16_t* xsrc = a.x + static_cast<size_t>(prow) * K + pq * 8;
   uint8_t* xdst0 = &xs[0][0] + 1024 * w + 16 * lane;
 
-  // Weights: frag f = rows 32f + lane%32 of the wave's tile, bytes 8*(lane/32)
-  // of each 16-byte row block.  Scales: one byte per (row, block).
+  // Weights: frag f = rows 32f + lane%32 of the wave's tile, dwords 2h and
+  // 2h + 1 (h = lane/32) of each 16-byte row block: tiled_dword(row, 2h) and
+  // the dword 64 after it; row 32 + r sits 2 dwords after row r.  Scales:
+  // one byte per (row, block).
   const int tl = active ? tile : 0;
-  const uint8_t* wsrc = a.wn + static_cast<size_t>(e) * g.nib_bytes + static_cast<size_t>(tl) * nb * 1024 +
-                        (lane & 31) * 16 + (lane >> 5) * 8;
+  const uint32_t* wsrc = reinterpret_cast<const uint32_t*>(a.wn + static_cast<size_t>(e) * g.nib_bytes +
+                                                           static_cast<size_t>(tl) * nb * 1024) +
+                         tiled_dword(lane & 31, 2 * (lane >> 5));
   const uint8_t* ssrc = a.ws + static_cast<size_t>(e) * g.scale_bytes +
                         (static_cast<size_t>(tl) * g.parts * kTileRows + (lane & 31)) * g.spad;
   const size_t spart = static_cast<size_t>(kTileRows) * g.spad;  // scale bytes per part
@@ -191,9 +167,9 @@ __global__ __launch_bounds__(kGW * kWave) void grouped_mfma_kernel(GroupedParams
     xv = *reinterpret_cast<const u32x4_t*>(xsrc + static_cast<size_t>(bb) * 32);
     // Every wave issues the same loads (an inactive one reads tile 0), so the
     // wait counts are the same on every path.
-    const uint8_t* wp = wsrc + static_cast<size_t>(bb) * 1024;
-    wv[0] = *reinterpret_cast<const u32x2_t*>(wp);  // cached: every m-tile of the expert reads them
-    wv[1] = *reinterpret_cast<const u32x2_t*>(wp + 512);
+    const uint32_t* wp = wsrc + static_cast<size_t>(bb) * 256;
+    wv[0] = u32x2_t{wp[0], wp[64]};  // cached: every m-tile of the expert reads them
+    wv[1] = u32x2_t{wp[2], wp[66]};
     // The aligned dword holding the scale byte (extracted at its use: a
     // loop-carried byte load is re-masked where the loop wraps, which waits
     // for the loads in flight).

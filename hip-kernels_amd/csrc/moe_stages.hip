@@ -33,15 +33,15 @@ __global__ __launch_bounds__(kTileRows * kMaxParts) void dense_gemv_kernel(
   const int mc = min(kRows, M - m0);
   const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int K = g.K;
-  const u32x4* src = reinterpret_cast<const u32x4*>(wn + static_cast<size_t>(tile) * g.nb * 1024) +
-                     static_cast<size_t>(p) * g.bpp * kTileRows + lane;
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(wn + static_cast<size_t>(tile) * g.nb * 1024) +
+                        static_cast<size_t>(p) * g.bpp * 256 + tiled_dword(lane, 0);
   const uint8_t* sc = ws + (static_cast<size_t>(tile) * g.parts + p) * kTileRows * g.spad +
                       static_cast<size_t>(lane) * g.spad;
   float acc[kRows];
 #pragma unroll
   for (int m = 0; m < kRows; ++m) acc[m] = 0.0f;
   for (int i = 0; i < g.bpp; ++i) {
-    const u32x4 blk = src[static_cast<size_t>(i) * kTileRows];
+    const u32x4 blk = load_row_block(src + static_cast<size_t>(i) * 256);
     const uint32_t code = sc[i];
     const int kb = (p * g.bpp + i) * 32;
 #pragma unroll
@@ -125,7 +125,8 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ wn, const uint8_t* __
        q += static_cast<size_t>(gridDim.x) * blockDim.x) {
     const size_t row = q / g.nb, b = q % g.nb;
     const size_t tile = row / kTileRows, lane = row % kTileRows;
-    const u32x4 blk = reinterpret_cast<const u32x4*>(wn)[(tile * g.nb + b) * kTileRows + lane];
+    const u32x4 blk = load_row_block(reinterpret_cast<const uint32_t*>(wn) + (tile * g.nb + b) * 256 +
+                                     tiled_dword(static_cast<int>(lane), 0));
     const size_t p = b / g.bpp, i = b % g.bpp;
     const uint32_t code = ws[((tile * g.parts + p) * kTileRows + lane) * g.spad + i];
     uint16_t* o = out + row * g.K + b * 32;

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GPTOSS_MOE_ABI_VERSION 2
+#define GPTOSS_MOE_ABI_VERSION 3
 
 enum {
   GPTOSS_OK = 0,
@@ -55,10 +55,15 @@ typedef struct gptoss_moe_config {
   int max_tokens;         /* largest T a forward call may pass (scratch sizing) */
   /* Forwards of at least this many tokens run the expert products as grouped
    * GEMMs on the matrix cores (fp32 accumulation in the matrix core's order:
-   * within one bf16 rounding step of the canonical result, not bit-identical);
-   * smaller ones (decode) stream the weights through the exact VALU kernels.
+   * within one bf16 rounding step of the canonical result, not bit-identical).
    * 0 = never.  Default 128. */
   int prefill_min_tokens;
+  /* Smaller forwards (decode) stream the expert weights once per step.
+   * 0 (default): on the matrix cores, fp32 accumulation in the matrix core's
+   * order (like prefill).  1: through the exact VALU kernels, whose results
+   * are bit-identical to the canonical order (one ascending fma chain per
+   * K-part, parts added in order), at a lower streaming rate. */
+  int decode_exact;
 } gptoss_moe_config;
 
 /* Fill `cfg` with the GPT-OSS constants for `num_experts` experts. */
@@ -68,8 +73,10 @@ int gptoss_moe_config_default(gptoss_moe_config* cfg, int num_experts, int max_t
  * Reference layout of one expert matrix [N rows, K inputs]
  * (weight_loader.cu:782-842, fused_mxfp4_gemv.cu:13-15): packed [N][K/2]
  * bytes, low nibble = even k; scales [N][K/32] e8m0 bytes.
- * The kernels read a tiled layout: per 64-row tile, K/32 blocks of
- * [64 rows][16 bytes]; scales grouped per (tile, K-part, row). */
+ * The kernels read a tiled layout: per 64-row tile, K/32 blocks of one KiB
+ * holding the 64 rows' 16-byte blocks as dwords ordered for the matrix
+ * cores (slot 16g + r%16, dword r/16 = bytes 4g..4g+3 of row r); scales
+ * twice, per (tile, K-part, row) and per (tile, block) in slot order. */
 int gptoss_mxfp4_tiled_size(int N, int K, size_t* nibble_bytes, size_t* scale_bytes);
 int gptoss_mxfp4_pack_tiled(const uint8_t* packed, const uint8_t* scales, int N, int K,
                             uint8_t* tiled_nibbles, uint8_t* tiled_scales, void* stream);

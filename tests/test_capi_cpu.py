@@ -32,11 +32,12 @@ def test_exports_every_declared_symbol(g):
 
 
 def test_abi_version_and_defaults(g):
-    assert g.lib.gptoss_abi_version() == 2
+    assert g.lib.gptoss_abi_version() == 3
     cfg = g.default_config(128, 64)
     assert (cfg.hidden_size, cfg.num_experts, cfg.top_k, cfg.intermediate_size) == (2880, 128, 4, 2880)
     assert abs(cfg.swiglu_alpha - 1.702) < 1e-6 and cfg.swiglu_limit == 7.0
-    assert cfg.prefill_min_tokens == 128  # decode batches (<= 64) keep the exact kernels
+    assert cfg.prefill_min_tokens == 128  # decode batches (<= 64) stream the weights
+    assert cfg.decode_exact == 0          # decode on the matrix cores unless asked for the exact kernels
     assert g.lib.gptoss_moe_config_default(None, 128, 1) == g.GPTOSS_ERR_INVALID
     assert b"NULL" in g.lib.gptoss_last_error()
 
@@ -44,9 +45,10 @@ def test_abi_version_and_defaults(g):
 def test_tiled_size_and_shape_errors(g):
     nb, sb = g.tiled_size(5760, 2880)
     assert nb == 5760 * 1440                     # nibbles are only permuted
-    assert sb == 90 * 6 * 64 * 16                # 15 scales per (tile, part, row), padded to 16
+    # 15 scales per (tile, part, row) padded to 16, then one per (row, block) in slot order
+    assert sb == 90 * 6 * 64 * 16 + 5760 * 90
     nb, sb = g.tiled_size(2880, 2880)
-    assert nb == 2880 * 1440 and sb == 45 * 6 * 64 * 16
+    assert nb == 2880 * 1440 and sb == 45 * 6 * 64 * 16 + 2880 * 90
     with pytest.raises(ValueError):
         g.tiled_size(64, 33)                     # K not a multiple of the MXFP4 block
     with pytest.raises(g.GptossError) as e:

@@ -1,0 +1,250 @@
+"""GPU parity of the matrix-core decode path (the layer's default for
+T < prefill_min_tokens): mc_stream_kernel gate_up (+ bias + SwiGLU) and down
+(+ bias), against the CPU oracle and against the exact decode kernels on the
+same weights.
+
+Tolerance, as for the prefill path (test_gpu_prefill.py): the matrix core
+adds the exact products (bf16 activations times exactly decoded MXFP4
+weights) in its own fp32 order and the K-parts are added in part order, so
+each value differs from the canonical fp32 sum by reordering alone, carried
+through one bf16 rounding.  Each stage is checked against the canonical
+computation of that stage on the GPU's own inputs:
+  * gate_up and expert outputs (single rounding): within one bf16 step plus
+    2^-9, differing on a small fraction of values, mean-rel <= 1e-3;
+  * SwiGLU activations: bit-identical to the oracle's SwiGLU of the GPU's own
+    gate_up values;
+  * layer output: bit-identical to the combine of the GPU's own expert
+    outputs, and end to end within mean-rel 1e-3 of the exact path / oracle,
+    with the fraction of outputs past 2e-2 (whole bf16 steps at |out| > 4)
+    bounded.
+Routing (indices, weights, plan) is the same launch as the exact path and is
+compared bit for bit.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import moe_data
+from test_gpu_parity import DeviceLayer, _trace_arrays, dev, host, say
+from test_gpu_prefill import check_layer_out, check_single_rounding
+
+pytestmark = pytest.mark.gpu
+
+E120, K120, H120, I120 = 128, 4, 2880, 2880
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+    return torch
+
+
+def _y_given(gpu, torch, act_dev, tiled, bias_t, offs, H, I):
+    """Expert outputs from the given activations with the exact dense kernel
+    (bit-identical to the oracle's canonical order)."""
+    n2, s2 = gpu.tiled_size(H, I)
+    y = np.zeros((act_dev.shape[0], H), np.uint16)
+    for e in range(len(offs) - 1):
+        a, b = int(offs[e]), int(offs[e + 1])
+        if b > a:
+            y[a:b] = host(gpu.mxfp4_gemv(act_dev[a:b], tiled[2][e * n2:(e + 1) * n2], tiled[3][e * s2:(e + 1) * s2],
+                                         bias_t[e] if bias_t is not None else None, H, I))
+    return y
+
+
+@pytest.mark.parametrize("T", [1, 5, 8, 9, 40])
+@pytest.mark.parametrize("bias", ["random", "none"])
+def test_mc_layer_small_stagewise(gpu, orc, torch_mod, T, bias):
+    """E=8, k=2, H=I=128 (4 blocks per row: the generic block loop), every
+    stage against the oracle on the GPU's own inputs."""
+    torch = torch_mod
+    E, k, H, I = 8, 2, 128, 128
+    w = moe_data.make_layer(20 + T, E, H, I, bias=bias)
+    x, res = moe_data.make_tokens(20 + T, T, H)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=64, exact=False)
+    L.layer.set_trace_gate_up(True)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    torch.cuda.synchronize()
+    ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    got = _trace_arrays(gpu, L.layer, T, k, E, H, I, torch, True)
+    assert np.array_equal(got["idx"], tr["idx"])
+    assert np.array_equal(got["w"].view(np.uint32), tr["w"].view(np.uint32))
+    assert np.array_equal(got["gather_map"], tr["gather_map"])
+    check_single_rounding(got["gate_up"], tr["gate_up"], f"mc small T={T} gate_up")
+    assert np.array_equal(got["act"], orc.swiglu_rows(got["gate_up"], I))
+    offs = np.concatenate([[0], np.cumsum(np.bincount(tr["idx"].ravel(), minlength=E))])
+    ylocal = np.zeros_like(got["y"])
+    for e in range(E):
+        a, b = int(offs[e]), int(offs[e + 1])
+        if b > a:
+            ylocal[a:b] = orc.mxfp4_gemv(got["act"][a:b], w["w2_packed"][e], w["w2_scales"][e],
+                                         w["w2_bias"][e] if w["w2_bias"] is not None else None, H, I)
+    check_single_rounding(got["y"], ylocal, f"mc small T={T} y (same activations)")
+    assert np.array_equal(out, orc.combine(got["y"], tr["gather_map"], tr["w"], res, T, k, H))
+    check_layer_out(out, ref, f"mc small T={T} bias={bias} out vs oracle")
+
+
+@pytest.fixture(scope="module")
+def pair120(gpu, torch_mod):
+    """One tiled copy of GPT-OSS-120B-shaped weights (E=128, H=I=2880) under
+    two layers: the matrix-core decode path and the exact decode path."""
+    torch = torch_mod
+    say("building GPT-OSS-120B-shaped layer pair (matrix-core / exact decode)")
+    w = moe_data.make_layer(4321, E120, H120, I120, bias="random")
+    ex = DeviceLayer(gpu, torch, w, E120, K120, H120, I120, max_tokens=64, via_tables=False, exact=True)
+    mc = DeviceLayer(gpu, torch, w, E120, K120, H120, I120, max_tokens=64, exact=False, tiled=ex.tiled, t=ex.t)
+    torch.cuda.synchronize()
+    return w, ex, mc
+
+
+def _stagewise_vs_exact(gpu, orc, torch, ex, mc, x, res, T, what, idx=None, wt=None):
+    k, H, I = K120, H120, I120
+    S = T * k
+    dx, dr = dev(x, torch), dev(res, torch)
+    mc.layer.set_trace_gate_up(True)
+    ex.layer.set_trace_gate_up(True)
+    if idx is None:
+        out_mc = host(mc.layer.forward_prenormed(dx, dr))
+    else:
+        out_mc = host(mc.layer.forward_routed(dx, dev(idx, torch), dev(wt, torch), residual=dr))
+    tr = mc.layer.trace()
+    rd = lambda p, n, dt: gpu.copy_device_to_tensor(p, n * np.dtype(dt).itemsize).cpu().numpy().view(dt)  # noqa
+    gu_mc = rd(tr.gate_up, S * 2 * I, np.uint16).reshape(S, 2 * I)
+    act_dev = gpu.copy_device_to_tensor(tr.act, S * I * 2).view(torch.bfloat16).reshape(S, I)
+    act_mc = host(act_dev)
+    y_mc = rd(tr.expert_out, S * H, np.uint16).reshape(S, H)
+    gm = rd(tr.gather_map, S, np.int32)
+    wts = rd(tr.expert_weights, S, np.float32).reshape(T, k) if idx is None else wt
+    offs = rd(tr.expert_offsets, E120 + 1, np.int32)
+    if idx is None:
+        out_ex = host(ex.layer.forward_prenormed(dx, dr))
+    else:
+        out_ex = host(ex.layer.forward_routed(dx, dev(idx, torch), dev(wt, torch), residual=dr))
+    tr_ex = ex.layer.trace()
+    gu_ex = rd(tr_ex.gate_up, S * 2 * I, np.uint16).reshape(S, 2 * I)
+    assert np.array_equal(rd(tr_ex.gather_map, S, np.int32), gm)
+    check_single_rounding(gu_mc, gu_ex, f"{what} gate_up")
+    assert np.array_equal(act_mc, orc.swiglu_rows(gu_mc, I))
+    y_given = _y_given(gpu, torch, act_dev, ex.tiled, ex.t["w2_bias"], offs, H, I)
+    check_single_rounding(y_mc, y_given, f"{what} y (same activations)")
+    assert np.array_equal(out_mc, orc.combine(y_mc, gm, wts, res, T, k, H))
+    check_layer_out(out_mc, out_ex, f"{what} out vs exact")
+    return out_mc, out_ex
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 64])
+def test_mc_gptoss120b_decode(gpu, orc, torch_mod, pair120, T):
+    """BASELINE config 2 (decode at batch 1/8/32/64): stage by stage against
+    the exact kernels, end to end against the exact path and the oracle."""
+    torch = torch_mod
+    w, ex, mc = pair120
+    x, res = moe_data.make_tokens(700 + T, T, H120)
+    say("120B matrix-core decode T", T)
+    out_mc, out_ex = _stagewise_vs_exact(gpu, orc, torch, ex, mc, x, res, T, f"120B mc T={T}")
+    ref = orc.moe_forward(w, x[:1], res[:1], E120, K120, H120, I120)
+    assert np.array_equal(out_ex[:1], ref)
+    check_layer_out(out_mc[:1], ref, f"120B mc T={T} token 0 vs oracle")
+    out2 = host(mc.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    assert np.array_equal(out_mc, out2)  # run-to-run deterministic
+
+
+def test_mc_many_tokens_per_expert(gpu, orc, torch_mod, pair120):
+    """Injected routing that sends all 64 tokens to experts 0..3 (64 slots per
+    expert: several 16-token steps per weight tile) and 40 tokens to a skewed
+    mix (a work-group's next step often the same tile's next chunk)."""
+    torch = torch_mod
+    w, ex, mc = pair120
+    T = 64
+    x, res = moe_data.make_tokens(811, T, H120)
+    idx = np.tile(np.array([[0, 1, 2, 3]], np.int32), (T, 1))
+    rng = np.random.default_rng(5)
+    wt = rng.dirichlet(np.ones(K120), T).astype(np.float32)
+    _stagewise_vs_exact(gpu, orc, torch, ex, mc, x, res, T, "mc 64 slots/expert", idx=idx, wt=wt)
+    idx2, wt2 = moe_data.zipf_routing(812, T, E120, K120, s=2.0)
+    _stagewise_vs_exact(gpu, orc, torch, ex, mc, x, res, T, "mc zipf(2.0) T=64", idx=idx2, wt=wt2)
+
+
+# every compiled launch shape for the GPT-OSS K (90 blocks per row): waves
+# per work-group P, ring depth D, 16-token chunks NC
+MC_SHAPES = ["6,15,1", "6,5,1", "3,10,1", "3,5,1", "2,9,1", "2,15,1", "1,9,1", "2,9,2"]
+
+
+@pytest.mark.parametrize("shape", MC_SHAPES)
+def test_mc_launch_shapes(gpu, orc, torch_mod, pair120, shape, monkeypatch):
+    """Each compiled launch shape (selected by GPTOSS_MOE_DECODE_SHAPE at
+    layer init) at T = 64 and T = 3, against the exact path."""
+    torch = torch_mod
+    w, ex, _ = pair120
+    monkeypatch.setenv("GPTOSS_MOE_DECODE_SHAPE", shape)
+    mc = DeviceLayer(gpu, torch, w, E120, K120, H120, I120, max_tokens=64, exact=False, tiled=ex.tiled, t=ex.t)
+    try:
+        for T in (64, 3):
+            x, res = moe_data.make_tokens(900 + T, T, H120)
+            say("mc shape", shape, "T", T)
+            _stagewise_vs_exact(gpu, orc, torch, ex, mc, x, res, T, f"mc shape {shape} T={T}")
+    finally:
+        mc.layer.destroy()
+
+
+def test_mc_special_scales(gpu, orc, torch_mod):
+    """Experts whose scales hold e8m0 codes 0 (+0) and 255 (+inf): the
+    checking variant runs; NaN / inf positions match the exact path and the
+    finite values agree to the tolerance above."""
+    torch = torch_mod
+    E, k, H, I, T = 8, 2, 256, 128, 6
+    w = moe_data.make_layer(61, E, H, I, bias="random")
+    rng = np.random.default_rng(61)
+    for e in (1, 5):
+        s1 = w["w1_scales"][e]
+        s1[rng.integers(0, s1.shape[0], 3), rng.integers(0, s1.shape[1], 3)] = 0
+        s1[rng.integers(0, s1.shape[0], 1), rng.integers(0, s1.shape[1], 1)] = 255
+        s2 = w["w2_scales"][e]
+        s2[rng.integers(0, s2.shape[0], 3), rng.integers(0, s2.shape[1], 3)] = 0
+    x, res = moe_data.make_tokens(61, T, H)
+    idx = np.array([[1, 5], [5, 0], [2, 1], [3, 4], [6, 7], [1, 2]], np.int32)
+    wt = np.full((T, k), 0.5, np.float32)
+    ex = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=8, via_tables=False, exact=True)
+    mc = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=8, exact=False, tiled=ex.tiled, t=ex.t)
+    ex.layer.set_trace_gate_up(True)
+    mc.layer.set_trace_gate_up(True)
+    dx, dr, di, dw = dev(x, torch), dev(res, torch), dev(idx, torch), dev(wt, torch)
+    out_mc = host(mc.layer.forward_routed(dx, di, dw, residual=dr))
+    g_mc = _trace_arrays(gpu, mc.layer, T, k, E, H, I, torch, True)
+    out_ex = host(ex.layer.forward_routed(dx, di, dw, residual=dr))
+    g_ex = _trace_arrays(gpu, ex.layer, T, k, E, H, I, torch, True)
+    c = moe_data.mfma_stats(g_mc["gate_up"], g_ex["gate_up"])
+    say("mc special gate_up", c)
+    assert c["nan_ok"] and c["inf_ok"] and c["max_excess"] <= 2.0 ** -9
+    c = moe_data.mfma_stats(out_mc, out_ex)
+    say("mc special out", c)
+    assert c["nan_ok"] and c["inf_ok"]
+
+
+def test_mc_graph_replay(gpu, orc, torch_mod):
+    """Matrix-core decode captured in a HIP graph: every replay matches the
+    eager forward bit for bit (the path is deterministic)."""
+    torch = torch_mod
+    E, k, H, I, T = 16, 4, 128, 128, 8
+    w = moe_data.make_layer(51, E, H, I)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T, exact=False)
+    xs = [moe_data.make_tokens(60 + i, T, H) for i in range(4)]
+    eager = [host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch))) for x, res in xs]
+    sx, sr = dev(xs[0][0], torch), dev(xs[0][1], torch)
+    so = torch.empty_like(sx)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        L.layer.forward_prenormed(sx, sr, out=so)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        L.layer.forward_prenormed(sx, sr, out=so)
+    for rep in range(3):
+        for i, (x, res) in enumerate(xs):
+            sx.copy_(dev(x, torch))
+            sr.copy_(dev(res, torch))
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(host(so), eager[i]), (rep, i)
+    check_layer_out(eager[1], orc.moe_forward(w, xs[1][0], xs[1][1], E, k, H, I), "mc graph eager vs oracle")

@@ -1,11 +1,13 @@
 """GPU parity tests: the HIP library (through its C ABI) against the CPU oracle.
 
 Tolerance: outputs within max-abs 2e-2 and mean-rel
-1e-3 of the reference on bf16 outputs, expert indices bit-exact.  The kernels
-follow the oracle's summation order, so every comparison below first asserts
-the strict result -- bit-identical bf16 / fp32 / int32 -- and the north-star
-tolerance is therefore met with margin zero.  Inputs are seeded synthetic
-data with the BASELINE distributions (tests/moe_data.py).
+1e-3 of the reference on bf16 outputs, expert indices bit-exact.  The layers
+here run the exact decode kernels (decode_exact = 1), which follow the
+oracle's summation order, so every comparison below first asserts the strict
+result -- bit-identical bf16 / fp32 / int32 -- and the north-star tolerance
+is therefore met with margin zero.  The matrix-core decode path (the default)
+is checked in test_gpu_decode_mc.py.  Inputs are seeded synthetic data with
+the BASELINE distributions (tests/moe_data.py).
 """
 import os
 import sys
@@ -214,14 +216,22 @@ def test_combine(gpu, orc, torch_mod):
 # the fused layer
 # ---------------------------------------------------------------------------
 class DeviceLayer:
-    def __init__(self, gpu, torch, w, E, k, H, I, max_tokens, norm_w=None, via_tables=True):
+    """A layer on device copies of the oracle's weights.  exact: the exact
+    decode kernels (bit-identical to the oracle) instead of the matrix-core
+    ones; tiled: share another layer's tiled weights."""
+    def __init__(self, gpu, torch, w, E, k, H, I, max_tokens, norm_w=None, via_tables=True, exact=True,
+                 tiled=None, t=None):
         self.torch = torch
-        self.t = {n: dev(w[n], torch) for n in w if w[n] is not None}
-        cfg = gpu.default_config(E, max_tokens)
+        self.t = t if t is not None else {n: dev(w[n], torch) for n in w if w[n] is not None}
+        cfg = gpu.default_config(E, max_tokens, decode_exact=exact)
         cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, k
         self.norm = dev(norm_w, torch) if norm_w is not None else None
         self.layer = gpu.MoELayer()
-        if via_tables:
+        if tiled is not None:
+            self.tiled = tiled
+            self.layer.init(cfg, 0, self.t["router_w"], self.t.get("router_b"), self.t.get("w1_bias"),
+                            self.t.get("w2_bias"), moe_norm_weight=self.norm, tiled=tiled)
+        elif via_tables:
             mlp1 = ([self.t["w1_packed"][e] for e in range(E)], [self.t["w1_scales"][e] for e in range(E)])
             mlp2 = ([self.t["w2_packed"][e] for e in range(E)], [self.t["w2_scales"][e] for e in range(E)])
             self.layer.init(cfg, 0, self.t["router_w"], self.t.get("router_b"), self.t.get("w1_bias"),
@@ -410,6 +420,8 @@ def test_cpp_operator_shim_matches_c_abi(gpu, torch_mod, gptoss120):
     torch = torch_mod
     w, L = gptoss120
     E, H = 128, 2880
+    # the operator shim runs the default configuration (matrix-core decode)
+    Lmc = DeviceLayer(gpu, torch, w, E, 4, H, H, max_tokens=8, exact=False, t=L.t, via_tables=True)
     lib = ctypes.CDLL(os.path.join(os.path.dirname(gpu.LIB_PATH), "libgptoss_moe_compat.so"))
     create = getattr(lib, _SHIM["create"])
     create.restype = ctypes.c_void_p
@@ -445,7 +457,8 @@ def test_cpp_operator_shim_matches_c_abi(gpu, torch_mod, gptoss120):
             out = torch.empty_like(dx)
             fwd(layer, dx.data_ptr(), dr.data_ptr(), out.data_ptr(), T, torch.cuda.current_stream().cuda_stream)
             torch.cuda.synchronize()
-            want = host(L.layer.forward_prenormed(dx, dr))
+            want = host(Lmc.layer.forward_prenormed(dx, dr))
             assert np.array_equal(host(out), want), T
     finally:
         destroy(layer)
+        Lmc.layer.destroy()

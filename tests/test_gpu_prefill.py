@@ -227,7 +227,7 @@ def zipf120(gpu, torch_mod):
     say("building GPT-OSS-120B-shaped layer for T=4096 prefill")
     w = moe_data.make_layer(4242, E, H, I, bias="zero")
     pre = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T, via_tables=False)
-    cfg = gpu.default_config(E, T, prefill_min_tokens=0)
+    cfg = gpu.default_config(E, T, prefill_min_tokens=0, decode_exact=True)
     exact = gpu.MoELayer().init(cfg, 0, pre.t["router_w"], pre.t.get("router_b"), pre.t.get("w1_bias"),
                                 pre.t.get("w2_bias"), tiled=pre.tiled)
     torch.cuda.synchronize()
