@@ -32,6 +32,8 @@ sys.path.insert(0, os.path.join(ROOT, "hip-kernels_amd"))
 
 E, K_TOP, H, I = 128, 4, 2880, 2880
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0   # dense bf16 matrix-core peak
+MXFP4_PEAK_TFLOPS = 10100.0  # dense MXFP4 (fp4 x fp4) matrix-core peak
 # algorithmic bytes per touched expert: W1 nibbles + scales + bias, W2 nibbles + scales + bias
 W1_EXPERT_BYTES = 2 * I * H // 2 + 2 * I * H // 32 + 2 * I * 2
 W2_EXPERT_BYTES = H * I // 2 + H * I // 32 + H * 2
@@ -64,13 +66,14 @@ def make_copy(g, torch, seed: int):
     return dict(tiled=(w1n, w1s, w2n, w2s), router_w=rw, router_b=rb, b1=b1, b2=b2)
 
 
-def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, graph_timing: bool = True):
+def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, graph_timing: bool = True,
+                exact: bool = False):
     """Time `steps` graph-replayed layer forwards at batch T; returns a dict.
     Without graph_timing the headline interval is the eager pass (profiler
     runs that count per-dispatch hardware counters)."""
     layers = []
     for c, wc in enumerate(copies):
-        cfg = g.default_config(E, T)
+        cfg = g.default_config(E, T, decode_exact=exact)
         L = g.MoELayer().init(cfg, 0, wc["router_w"], wc["router_b"], wc["b1"], wc["b2"], tiled=wc["tiled"])
         layers.append(L)
     gen = torch.Generator(device="cuda")
@@ -123,10 +126,10 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, gr
         wall = time.perf_counter() - wall0
     total_ms = t0.elapsed_time(t1)
 
-    # per-launch durations: the same K steps eagerly, with HIP events recorded
-    # by the library on the launch stream around each launch.  A bounded sleep
-    # kernel holds the stream while the host enqueues all K steps, so no
-    # interval contains a wait for the host.
+    # per-launch durations: the same K steps eagerly, each launch timed by HIP
+    # events stamped by its own dispatch (the library's profiling mode).  A
+    # bounded sleep kernel holds the stream while the host enqueues all K
+    # steps, so the launches run back to back as in the replay.
     per_layer = [sum(1 for li, _ in plan if li == j) for j in range(len(layers))]
     for j, L in enumerate(layers):
         L.set_profiling(per_layer[j])
@@ -138,13 +141,14 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, gr
         for li, xi in plan:
             layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
     torch.cuda.synchronize()
-    r_ms = w1_ms = w2_ms = 0.0
+    r_ms = w1_ms = w2_ms = c_ms = 0.0
     n_rec = 0
     for L in layers:
-        r, a, b, n = L.profile_read()
+        r, a, b, c, n = L.profile_read()
         r_ms += r
         w1_ms += a
         w2_ms += b
+        c_ms += c
         n_rec += n
     for L in layers:
         L.destroy()
@@ -158,7 +162,9 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, gr
     res["hbm_frac"] = res["hbm_gbs"] / HBM_PEAK_GBS
     if n_rec == steps:
         res["kernel_us"] = dict(route=1e3 * r_ms / steps, w1=1e3 * w1_ms / steps, w2=1e3 * w2_ms / steps,
-                                source="HIP events on the launch stream, eager pass of the same steps")
+                                combine=1e3 * c_ms / steps,
+                                source="HIP events stamped by each dispatch (hipExtLaunchKernelGGL) on the launch "
+                                       "stream, eager pass of the same steps")
         res["w1_algorithmic_bytes"] = w1_bytes
         res["w1_gbs"] = w1_bytes / (w1_ms / steps / 1e3) / 1e9
     return res
@@ -190,6 +196,138 @@ def copy_calibration(torch, mib: int = 256, reps: int = 4):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_per_launch": mib << 20, "launches": reps}), flush=True)
+
+
+def zipf_routing(seed: int, T: int, k: int, s: float = 1.1):
+    """BASELINE prefill routing: expert popularity p(e) ~ (pi(e)+1)^-s for a
+    seeded permutation pi of the E experts, k distinct experts per token
+    (Gumbel top-k without replacement), weights = softmax of k sorted N(0,1)
+    draws, descending."""
+    import numpy as np
+    rng = np.random.default_rng([seed, 3])
+    pi = rng.permutation(E)
+    keys = -s * np.log(pi + 1.0)[None, :] + rng.gumbel(size=(T, E))
+    top = np.argpartition(-keys, k - 1, axis=1)[:, :k]
+    order = np.argsort(-np.take_along_axis(keys, top, axis=1), axis=1, kind="stable")
+    idx = np.take_along_axis(top, order, axis=1).astype(np.int32)
+    z = -np.sort(-rng.normal(size=(T, k)), axis=1)
+    w = np.exp(z - z[:, :1])
+    return idx, (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def timed_events(torch, fn, reps: int):
+    """Mean ms of fn() over reps on the current stream (HIP events)."""
+    fn()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / reps
+
+
+def bench_prefill(g, torch, wc, T: int = 4096, reps: int = 5):
+    """one GPT-OSS-120B layer forward at T tokens with
+    Zipf(1.1) routing injected (forward_routed: plan, grouped gate_up + SwiGLU
+    and grouped down on the matrix cores, combine)."""
+    idx, wt = zipf_routing(4096, T, K_TOP)
+    cfg = g.default_config(E, T)
+    L = g.MoELayer().init(cfg, 0, wc["router_w"], wc["router_b"], wc["b1"], wc["b2"], tiled=wc["tiled"])
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4096)
+    x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+    r = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+    di = torch.from_numpy(idx).cuda()
+    dw = torch.from_numpy(wt).cuda()
+    out = torch.empty_like(x)
+    ms = timed_events(torch, lambda: L.forward_routed(x, di, dw, residual=r, out=out), reps)
+    L.set_profiling(reps)
+    for _ in range(reps):
+        L.forward_routed(x, di, dw, residual=r, out=out)
+    plan_ms, w1_ms, w2_ms, c_ms, n = L.profile_read()
+    L.destroy()
+    flops_w1 = 2.0 * T * K_TOP * (2 * I) * H
+    flops_w2 = 2.0 * T * K_TOP * H * I
+    w1 = w1_ms / n
+    res = dict(tokens=T, routing="zipf(1.1), top-4 distinct", ms_per_layer=ms, tokens_per_s=T / (ms / 1e3),
+               tflops_layer=(flops_w1 + flops_w2) / (ms / 1e3) / 1e12,
+               kernel_ms=dict(plan=plan_ms / n, gate_up=w1, down=w2_ms / n, combine=c_ms / n),
+               gate_up_tflops=flops_w1 / (w1 / 1e3) / 1e12)
+    res["gate_up_frac_bf16_peak"] = res["gate_up_tflops"] / BF16_PEAK_TFLOPS
+    res["gate_up_frac_mxfp4_peak"] = res["gate_up_tflops"] / MXFP4_PEAK_TFLOPS
+    res["layer_frac_bf16_peak"] = res["tflops_layer"] / BF16_PEAK_TFLOPS
+    return res
+
+
+def bench_router(g, torch, T: int = 4096, reps: int = 20):
+    """router GEMV + top-k softmax alone, fp32 logits
+    [4096 x 128] from bf16 x [4096 x 2880] and router W [128 x 2880] + bias."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1)
+    x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+    W = (torch.randn((E, H), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    b = (torch.randn((E,), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    scratch = g.route_scratch(T, E, K_TOP)
+    logits = torch.empty((T, E), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, K_TOP), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, K_TOP), dtype=torch.float32, device="cuda")
+    ms = timed_events(torch, lambda: g.route(x, W, b, K_TOP, logits_fp32=True, out=(logits, idx, w),
+                                             scratch=scratch), reps)
+    nbytes = T * H * 2 + E * H * 2 + E * 2 + T * E * 4 + 2 * T * K_TOP * 4
+    return dict(tokens=T, logits="fp32", us=ms * 1e3, tokens_per_s=T / (ms / 1e3), algorithmic_bytes=nbytes,
+                gbs=nbytes / (ms / 1e3) / 1e9)
+
+
+def bench_stack(g, torch, layers: int = 36, T: int = 32, steps: int = 256):
+    """36 distinct GPT-OSS-120B MoE layers resident (random
+    MXFP4 weights, ~61 GB), a decode step at batch 32 = the 36 layer forwards
+    chained through the residual stream, captured once in a hipGraph and
+    replayed `steps` times."""
+    cps = [make_copy(g, torch, 5000 + l) for l in range(layers)]
+    Ls = [g.MoELayer().init(g.default_config(E, T), 0, c["router_w"], c["router_b"], c["b1"], c["b2"],
+                            tiled=c["tiled"]) for c in cps]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(32)
+    h0 = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+    hs = [h0] + [torch.empty_like(h0) for _ in range(layers)]
+
+    def step():
+        for l, L in enumerate(Ls):
+            # prenormed input = the residual stream itself (no attention or norm in this stack)
+            L.forward_prenormed(hs[l], hs[l], out=hs[l + 1])
+
+    step()
+    torch.cuda.synchronize()
+    U = []
+    for L in Ls:
+        U.append(int(g.copy_device_to_tensor(L.trace().n_active, 4, torch.int32).item()))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        step()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        t0.record(s)
+        for _ in range(steps):
+            graph.replay()
+        t1.record(s)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    del graph
+    for L in Ls:
+        L.destroy()
+    nbytes = sum(layer_bytes(u, T) for u in U)
+    return dict(layers=layers, batch=T, steps=steps, ms_per_step=ms, tokens_per_s=T / (ms / 1e3),
+                experts_touched_mean=sum(U) / len(U), algorithmic_bytes_per_step=nbytes,
+                hbm_gbs=nbytes / (ms / 1e3) / 1e9, hbm_frac=nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+                weights_gb=layers * E * (W1_EXPERT_BYTES + W2_EXPERT_BYTES) / 1e9)
 
 
 def cpu_baseline(seconds: float, threads: int):
@@ -230,6 +368,9 @@ def main():
                     help="time the eager launches instead of a hipGraph replay (profiler counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (scales FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="decode sweep only (skip the exact-path, prefill, router and 36-layer stack legs)")
+    ap.add_argument("--stack-layers", type=int, default=36)
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -256,14 +397,32 @@ def main():
     head = sweep[headline_b]
     rf = None
     if "w1_gbs" in head:
-        traffic = profiled_traffic("expert_stream_gate_up_b64_traffic.md") if headline_b == 64 else None
+        traffic = profiled_traffic("mc_gate_up_b64_traffic.md") if headline_b == 64 else None
         rf = dict(bound="hbm", achieved=head["w1_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                   frac=head["w1_gbs"] / HBM_PEAK_GBS, traffic=traffic,
-                  kernel="expert_stream_kernel<gated> (MXFP4 gate_up + bias + SwiGLU)",
-                  traffic_source="profiles/expert_stream_gate_up_b64_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                  kernel="mc_stream_kernel<gated> (matrix-core MXFP4 gate_up + bias + SwiGLU)",
+                  traffic_source="profiles/mc_gate_up_b64_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                  "copy-calibrated)" if traffic else None,
                   algorithmic_bytes_per_launch=head["w1_algorithmic_bytes"],
                   avg_launch_us=head["kernel_us"]["w1"])
+    extra = {}
+    if not args.no_extra:
+        # the exact (bit-identical to the oracle) decode kernels at the headline batch
+        log("decode_exact at the headline batch")
+        ex_copies = [dict(c) for c in copies]
+        extra["decode_exact"] = bench_batch(g, torch, ex_copies, headline_b, args.steps, args.warmup, seed=headline_b,
+                                            graph_timing=not args.no_graph, exact=True)
+        log("prefill T=4096 (zipf routing)")
+        extra["prefill"] = bench_prefill(g, torch, copies[0])
+        log(json.dumps(extra["prefill"]))
+        log("router + top-k T=4096 fp32 logits")
+        extra["router"] = bench_router(g, torch)
+        log(json.dumps(extra["router"]))
+        del copies
+        torch.cuda.empty_cache()
+        log(f"{args.stack_layers}-layer stack at batch 32")
+        extra["stack"] = bench_stack(g, torch, layers=args.stack_layers)
+        log(json.dumps(extra["stack"]))
     cpu = None
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -291,6 +450,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": {str(k): v for k, v in sweep.items()},
     }
+    line.update(extra)
     print(json.dumps(line), flush=True)
 
 

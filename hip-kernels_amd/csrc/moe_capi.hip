@@ -336,11 +336,20 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   return ok();
 }
 
+// Timing of one profiled forward (gptoss_moe_layer_set_profiling): launch i
+// (0 route or plan, 1 gate_up, 2 down, 3 combine) between events 2i and
+// 2i + 1, stamped by the dispatch itself (hipExtLaunchKernelGGL).
+struct ProfForward {
+  hipEvent_t* ev = nullptr;
+  KernelTimer timer(int i) const { return ev ? KernelTimer{ev[2 * i], ev[2 * i + 1]} : KernelTimer{}; }
+};
+constexpr int kProfEvents = 8;
+
 // Expert products and combine after the plan (decode: weight-streaming
 // kernels, on the matrix cores or exact; prefill: grouped matrix-core GEMMs).
 // w: routing weights [T][k].
 static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, const float* w,
-                         uint16_t* out, int T, hipStream_t s, hipEvent_t* ev) {
+                         uint16_t* out, int T, hipStream_t s, const ProfForward& pf) {
   const gptoss_moe_config& c = L->cfg;
   ExpertArgs ea{};
   ea.x = normed;
@@ -390,8 +399,8 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
     g.gated = 1;
     g.alpha = c.swiglu_alpha;
     g.limit = c.swiglu_limit;
+    g.timer = pf.timer(1);
     HIP_TRY(launch_grouped_mxfp4(g, s), "grouped gate_up launch");
-    if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
     g.x = L->act;
     g.row_index = nullptr;
     g.wn = L->w2n;
@@ -402,24 +411,31 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
     g.out = L->y;
     g.gate_up = nullptr;
     g.gated = 0;
+    g.timer = pf.timer(2);
     HIP_TRY(launch_grouped_mxfp4(g, s), "grouped down launch");
-  } else if (c.decode_exact || !decode_mc_supported(T, c.top_k, c.num_experts, c.hidden_size, c.intermediate_size)) {
-    HIP_TRY(launch_w1(ea, s), "w1 launch");
-    if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
-    HIP_TRY(launch_w2(ea, s), "w2 launch");
   } else {
-    HIP_TRY(launch_w1_mc(ea, s), "w1 launch");
-    if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
-    HIP_TRY(launch_w2_mc(ea, s), "w2 launch");
+    const bool exact =
+        c.decode_exact || !decode_mc_supported(T, c.top_k, c.num_experts, c.hidden_size, c.intermediate_size);
+    ea.timer = pf.timer(1);
+    HIP_TRY(exact ? launch_w1(ea, s) : launch_w1_mc(ea, s), "w1 launch");
+    ea.timer = pf.timer(2);
+    HIP_TRY(exact ? launch_w2(ea, s) : launch_w2_mc(ea, s), "w2 launch");
   }
+  ea.timer = pf.timer(3);
   HIP_TRY(launch_combine_slots(ea, s), "combine launch");
-  if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");
   return ok();
 }
 
-static hipEvent_t* next_prof_events(gptoss_moe_layer* L) {
-  if (L->prof_count < L->prof_capacity) return &L->prof_events[4 * static_cast<size_t>(L->prof_count++)];
-  return nullptr;
+// Forwards being captured into a graph are not timed (events inside a graph
+// cannot be timed on this runtime) and leave the profiling slots unused.
+static ProfForward next_prof(gptoss_moe_layer* L, hipStream_t s) {
+  ProfForward pf;
+  if (L->prof_count < L->prof_capacity) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+    if (!capturing) pf.ev = &L->prof_events[kProfEvents * static_cast<size_t>(L->prof_count++)];
+  }
+  return pf;
 }
 
 static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, uint16_t* out,
@@ -440,11 +456,10 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ra.w = L->w;
   ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks};
   route_scratch_carve(L->route_scratch, L->cfg.max_tokens, c.num_experts, c.top_k, ra);
-  hipEvent_t* ev = next_prof_events(L);
-  if (ev) HIP_TRY(hipEventRecord(ev[0], s), "hipEventRecord");
+  const ProfForward pf = next_prof(L, s);
+  ra.timer = pf.timer(0);
   HIP_TRY(launch_route(ra, s), "route launch");
-  if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
-  return layer_experts(L, normed, residual, L->w, out, T, s, ev);
+  return layer_experts(L, normed, residual, L->w, out, T, s, pf);
 }
 
 static int check_forward_args(gptoss_moe_layer* L, const void* in, const void* out, int T) {
@@ -490,13 +505,12 @@ int gptoss_moe_layer_forward_routed(gptoss_moe_layer* L, const uint16_t* normed,
   if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const gptoss_moe_config& c = L->cfg;
-  hipEvent_t* ev = next_prof_events(L);
-  if (ev) HIP_TRY(hipEventRecord(ev[0], s), "hipEventRecord");
+  const ProfForward pf = next_prof(L, s);
   HIP_TRY(launch_plan(idx, T, c.top_k, c.num_experts,
-                      PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks}, s),
+                      PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks}, s,
+                      pf.timer(0)),
           "plan launch");
-  if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
-  return layer_experts(L, normed, residual, w, out, T, s, ev);
+  return layer_experts(L, normed, residual, w, out, T, s, pf);
 }
 
 const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* L) {
@@ -539,31 +553,31 @@ int gptoss_moe_layer_set_profiling(gptoss_moe_layer* L, int max_forwards) {
   if (max_forwards < 0) return fail(GPTOSS_ERR_INVALID, "max_forwards=%d < 0", max_forwards);
   ScopedDevice sd(L->device);
   for (hipEvent_t e : L->prof_events) (void)hipEventDestroy(e);
-  L->prof_events.assign(4 * static_cast<size_t>(max_forwards), nullptr);
+  L->prof_events.assign(kProfEvents * static_cast<size_t>(max_forwards), nullptr);
   for (auto& e : L->prof_events) HIP_TRY(hipEventCreate(&e), "hipEventCreate");
   L->prof_capacity = max_forwards;
   L->prof_count = 0;
   return ok();
 }
 
-int gptoss_moe_layer_profile_read(gptoss_moe_layer* L, float* route_ms, float* w1_ms, float* w2_ms, int* n_forwards) {
+int gptoss_moe_layer_profile_read(gptoss_moe_layer* L, float* route_ms, float* w1_ms, float* w2_ms, float* combine_ms,
+                                  int* n_forwards) {
   if (L == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
   ScopedDevice sd(L->device);
-  double r = 0, a = 0, b = 0;
+  double sum[4] = {0, 0, 0, 0};
   for (int i = 0; i < L->prof_count; ++i) {
-    hipEvent_t* ev = &L->prof_events[4 * static_cast<size_t>(i)];
-    float t;
-    HIP_TRY(hipEventSynchronize(ev[3]), "hipEventSynchronize");
-    HIP_TRY(hipEventElapsedTime(&t, ev[0], ev[1]), "hipEventElapsedTime");
-    r += t;
-    HIP_TRY(hipEventElapsedTime(&t, ev[1], ev[2]), "hipEventElapsedTime");
-    a += t;
-    HIP_TRY(hipEventElapsedTime(&t, ev[2], ev[3]), "hipEventElapsedTime");
-    b += t;
+    hipEvent_t* ev = &L->prof_events[kProfEvents * static_cast<size_t>(i)];
+    HIP_TRY(hipEventSynchronize(ev[kProfEvents - 1]), "hipEventSynchronize");
+    for (int j = 0; j < 4; ++j) {
+      float t;
+      HIP_TRY(hipEventElapsedTime(&t, ev[2 * j], ev[2 * j + 1]), "hipEventElapsedTime");
+      sum[j] += t;
+    }
   }
-  if (route_ms) *route_ms = static_cast<float>(r);
-  if (w1_ms) *w1_ms = static_cast<float>(a);
-  if (w2_ms) *w2_ms = static_cast<float>(b);
+  if (route_ms) *route_ms = static_cast<float>(sum[0]);
+  if (w1_ms) *w1_ms = static_cast<float>(sum[1]);
+  if (w2_ms) *w2_ms = static_cast<float>(sum[2]);
+  if (combine_ms) *combine_ms = static_cast<float>(sum[3]);
   if (n_forwards) *n_forwards = L->prof_count;
   return ok();
 }

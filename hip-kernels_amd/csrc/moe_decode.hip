@@ -372,7 +372,7 @@ __global__ void special_scan_kernel(const uint8_t* __restrict__ ws, TiledGeom g,
 }
 
 template <bool kGated, int P, int D, int NC, bool kSpec, int BPP>
-hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_t s) {
+hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_t s, const KernelTimer& timer) {
   static const int per_cu = [] {  // resident work-groups per CU (a property of the kernel)
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mc_stream_kernel<kGated, P, D, NC, kSpec, BPP>, P * kWave,
@@ -386,8 +386,8 @@ hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_
   grid = (grid + 7) & ~7L;  // a multiple of 8 for the XCD-grouped block order
   McParams q = p;
   q.bpp = p.g.nb / P;
-  hipLaunchKernelGGL((mc_stream_kernel<kGated, P, D, NC, kSpec, BPP>), dim3(static_cast<unsigned>(grid)),
-                     dim3(P * kWave), 0, s, q);
+  gx_launch(mc_stream_kernel<kGated, P, D, NC, kSpec, BPP>, dim3(static_cast<unsigned>(grid)), dim3(P * kWave), 0, s,
+            timer, q);
   return hipGetLastError();
 }
 
@@ -424,29 +424,33 @@ bool shape_compiled(int nb, int P, int D, int NC) {
 }
 
 template <bool kGated>
-hipError_t launch_mc_shape(const McParams& p, int P, int D, int NC, int max_items, int num_cus, hipStream_t s) {
+hipError_t launch_mc_shape(const McParams& p, int P, int D, int NC, int max_items, int num_cus, hipStream_t s,
+                           const KernelTimer& timer) {
   if (p.g.nb == kNbGptOss) {
 #define GX_MC_GO(p_, d_, nc_) \
   if (P == p_ && D == d_ && NC == nc_)  \
-    return launch_mc_t<kGated, p_, d_, nc_, false, kNbGptOss / p_>(p, max_items, num_cus, s);
+    return launch_mc_t<kGated, p_, d_, nc_, false, kNbGptOss / p_>(p, max_items, num_cus, s, timer);
     GX_MC_SHAPES(GX_MC_GO)
 #undef GX_MC_GO
   }
 #define GX_MC_GO(p_, d_, nc_) \
-  if (P == p_ && D == d_ && NC == nc_) return launch_mc_t<kGated, p_, d_, nc_, false, 0>(p, max_items, num_cus, s);
+  if (P == p_ && D == d_ && NC == nc_)  \
+    return launch_mc_t<kGated, p_, d_, nc_, false, 0>(p, max_items, num_cus, s, timer);
   GX_MC_GENERIC(GX_MC_GO)
 #undef GX_MC_GO
   return hipErrorInvalidValue;
 }
 
-// Default shape for nb blocks and S routed slots: small batches split K over
-// more waves (more work-groups in flight for few items), large batches fewer.
+// Default shape for nb blocks and S routed slots (measured on MI355X at the
+// GPT-OSS-120B shape; the shapes differ by a few percent): one token takes
+// three K-parts with a short ring, a few tokens two parts, larger batches
+// six parts with each wave's whole part (15 blocks) in flight.
 void pick_shape(int nb, int S, int& P, int& D, int& NC) {
   NC = 1;
   if (nb == kNbGptOss) {
-    if (S <= 16) { P = 6; D = 15; }
-    else if (S <= 64) { P = 3; D = 10; }
-    else { P = 2; D = 9; }
+    if (S <= 4) { P = 3; D = 5; }
+    else if (S <= 16) { P = 2; D = 9; }
+    else { P = 6; D = 15; }
     return;
   }
   P = 1;
@@ -488,10 +492,10 @@ hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
   }
   const int max_items = a.max_active * (g.N / kTileRows);
   if (gated ? a.special_any1 : a.special_any2)  // weights with e8m0 code 0 or 255: the checking variant
-    return gated ? launch_mc_t<true, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s)
-                 : launch_mc_t<false, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s);
-  return gated ? launch_mc_shape<true>(p, P, D, NC, max_items, a.num_cus, s)
-               : launch_mc_shape<false>(p, P, D, NC, max_items, a.num_cus, s);
+    return gated ? launch_mc_t<true, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s, a.timer)
+                 : launch_mc_t<false, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s, a.timer);
+  return gated ? launch_mc_shape<true>(p, P, D, NC, max_items, a.num_cus, s, a.timer)
+               : launch_mc_shape<false>(p, P, D, NC, max_items, a.num_cus, s, a.timer);
 }
 
 }  // namespace

@@ -597,7 +597,8 @@ static void launch_stream_t(const ExpertArgs& a, const TiledGeom& g, bool gated,
   const int items = a.max_active * ntp;
   const int resident = 256 * 2;
   const int grid = items < resident ? items : resident;
-  hipLaunchKernelGGL((expert_stream_kernel<BPP, R, TC, D, kGated, kTok>), dim3(grid), dim3(kTileRows * g.parts), 0, s, p);
+  gx_launch(expert_stream_kernel<BPP, R, TC, D, kGated, kTok>, dim3(grid), dim3(kTileRows * g.parts), 0, s, a.timer,
+            p);
 }
 
 template <int BPP, bool kGated>
@@ -631,8 +632,8 @@ hipError_t launch_w2(const ExpertArgs& a, hipStream_t s) {
 hipError_t launch_combine_slots(const ExpertArgs& a, hipStream_t s) {
   if (a.T <= 0) return hipSuccess;
   const int n = a.T * (a.H / 8);
-  hipLaunchKernelGGL(combine8_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a.y, a.plan.gather_map, a.w, a.residual,
-                     a.out, a.T, a.H, a.k);
+  gx_launch(combine8_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a.timer, static_cast<const uint16_t*>(a.y),
+            static_cast<const int32_t*>(a.plan.gather_map), a.w, a.residual, a.out, a.T, a.H, a.k);
   return hipGetLastError();
 }
 

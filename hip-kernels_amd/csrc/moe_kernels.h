@@ -5,7 +5,25 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <hip/hip_ext.h>
+
 namespace gxmoe {
+
+// Optional per-launch timing: with start set, the kernel is launched through
+// hipExtLaunchKernelGGL, which stamps start/stop with the dispatch's own
+// begin and end (no marker packets between launches).
+struct KernelTimer {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
+template <typename F, typename... Args>
+inline void gx_launch(F kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t s, const KernelTimer& t,
+                      Args... args) {
+  if (t.start)
+    hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(shmem), s, t.start, t.stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+}
 
 constexpr int kMaxExperts = 256;  // LDS tables of the routing plan
 constexpr int kMaxTopK = 8;       // topk_softmax.cu:34
@@ -85,6 +103,7 @@ struct RouteArgs {
   uint32_t* done_counter;  // [1] zero at rest
   float* xchg_logits;      // [T][E] fp32 exchange (the logits as rounded)
   int32_t* xchg_idx;       // [T][k] exchange of the selections (T > 8)
+  KernelTimer timer;
 };
 
 // Bytes of route scratch: counters, then the exchange buffers (256-aligned).
@@ -97,7 +116,8 @@ hipError_t launch_topk(const void* logits, int logits_fp32, int T, int E, int k,
                        int32_t* idx, float* w, int32_t* tokens_per_expert, hipStream_t s);
 
 // Standalone plan (histogram, scan, stable gather map) from expert indices.
-hipError_t launch_plan(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s);
+hipError_t launch_plan(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s,
+                       const KernelTimer& timer = KernelTimer{});
 
 struct ExpertArgs {
   const uint16_t* x;          // [T][H] bf16 expert input (the normed activations)
@@ -123,6 +143,7 @@ struct ExpertArgs {
   int special_any1, special_any2;  // any flag set (read back at layer init)
   int num_cus;                // compute units of the device (persistent grid size)
   int mc_shape[3];            // {P, D, NC} launch shape override, {0,0,0} = automatic
+  KernelTimer timer;          // of the next launch_w1* / launch_w2* / launch_combine_slots
 };
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
 // The two launches of launch_experts, for callers that time them separately.
@@ -162,6 +183,7 @@ struct GroupedArgs {
   uint16_t* gate_up;
   int gated;
   float alpha, limit;
+  KernelTimer timer;
 };
 bool grouped_supported(int N, int K, int E);
 hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s);

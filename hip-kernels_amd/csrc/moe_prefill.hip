@@ -341,9 +341,9 @@ hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s) {
   p.total = static_cast<int>(total);
   const int grid = (p.total + 7) & ~7;
   if (a.gated)
-    hipLaunchKernelGGL(grouped_mfma_kernel<true>, dim3(grid), dim3(kGW * kWave), 0, s, p);
+    gx_launch(grouped_mfma_kernel<true>, dim3(grid), dim3(kGW * kWave), 0, s, a.timer, p);
   else
-    hipLaunchKernelGGL(grouped_mfma_kernel<false>, dim3(grid), dim3(kGW * kWave), 0, s, p);
+    gx_launch(grouped_mfma_kernel<false>, dim3(grid), dim3(kGW * kWave), 0, s, a.timer, p);
   return hipGetLastError();
 }
 

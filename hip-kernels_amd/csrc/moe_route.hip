@@ -514,13 +514,13 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
   // chunks of 8 inputs per thread: 2 covers H <= 4096 (GPT-OSS: 2880)
   const int nj = ((a.H >> 3) + kRouteThreads - 1) / kRouteThreads;
   if (a.logits_fp32) {
-    if (nj <= 1) hipLaunchKernelGGL((route_kernel<true, 1>), grid, dim3(kRouteThreads), 0, s, a);
-    else if (nj == 2) hipLaunchKernelGGL((route_kernel<true, 2>), grid, dim3(kRouteThreads), 0, s, a);
-    else hipLaunchKernelGGL((route_kernel<true, 0>), grid, dim3(kRouteThreads), 0, s, a);
+    if (nj <= 1) gx_launch(route_kernel<true, 1>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
+    else if (nj == 2) gx_launch(route_kernel<true, 2>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
+    else gx_launch(route_kernel<true, 0>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
   } else {
-    if (nj <= 1) hipLaunchKernelGGL((route_kernel<false, 1>), grid, dim3(kRouteThreads), 0, s, a);
-    else if (nj == 2) hipLaunchKernelGGL((route_kernel<false, 2>), grid, dim3(kRouteThreads), 0, s, a);
-    else hipLaunchKernelGGL((route_kernel<false, 0>), grid, dim3(kRouteThreads), 0, s, a);
+    if (nj <= 1) gx_launch(route_kernel<false, 1>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
+    else if (nj == 2) gx_launch(route_kernel<false, 2>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
+    else gx_launch(route_kernel<false, 0>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
   }
   return hipGetLastError();
 }
@@ -536,9 +536,10 @@ hipError_t launch_topk(const void* logits, int logits_fp32, int T, int E, int k,
   return hipGetLastError();
 }
 
-hipError_t launch_plan(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s) {
+hipError_t launch_plan(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s,
+                       const KernelTimer& timer) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kRouteThreads), 0, s, idx, T, k, E, plan);
+  gx_launch(plan_kernel, dim3(1), dim3(kRouteThreads), 0, s, timer, idx, T, k, E, plan);
   return hipGetLastError();
 }
 

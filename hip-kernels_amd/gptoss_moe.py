@@ -93,7 +93,7 @@ _sig("gptoss_moe_layer_trace", [_P, ctypes.POINTER(MoeTrace)])
 _sig("gptoss_moe_layer_set_trace_gate_up", [_P, _I])
 _sig("gptoss_moe_layer_set_profiling", [_P, _I])
 _sig("gptoss_moe_layer_profile_read", [_P, ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_F),
-                                        ctypes.POINTER(_I)])
+                                        ctypes.POINTER(_F), ctypes.POINTER(_I)])
 _sig("gptoss_moe_route_scratch_bytes", [_I, _I, _I], _SZ)
 _sig("gptoss_moe_route", [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P])
 _sig("gptoss_topk_softmax_forward", [_P, _I, _P, _P, _P, _I, _I, _I, _P])
@@ -256,11 +256,12 @@ class MoELayer:
         check(_lib.gptoss_moe_layer_set_profiling(self._h, max_forwards))
 
     def profile_read(self):
-        """(route_ms, w1_ms, w2_ms, n_forwards) summed over the recorded forwards."""
-        r, a, b, n = _F(), _F(), _F(), _I()
+        """(route_ms, w1_ms, w2_ms, combine_ms, n_forwards) summed over the
+        recorded forwards (route_ms is the plan launch for forward_routed)."""
+        r, a, b, c, n = _F(), _F(), _F(), _F(), _I()
         check(_lib.gptoss_moe_layer_profile_read(self._h, ctypes.byref(r), ctypes.byref(a), ctypes.byref(b),
-                                                 ctypes.byref(n)))
-        return r.value, a.value, b.value, n.value
+                                                 ctypes.byref(c), ctypes.byref(n)))
+        return r.value, a.value, b.value, c.value, n.value
 
     def trace(self) -> Trace:
         t = MoeTrace()
@@ -304,14 +305,25 @@ def copy_device_to_tensor(ptr: int, nbytes: int, dtype=torch.uint8, device="cuda
 # ---------------------------------------------------------------------------
 # stage entry points
 # ---------------------------------------------------------------------------
-def route(x, router_w, router_b, top_k: int, logits_fp32: bool = False, stream=None):
+def route_scratch(T: int, E: int, top_k: int, device="cuda") -> torch.Tensor:
+    """Zero-filled scratch for route() (the call leaves its counters zero)."""
+    return torch.zeros(_lib.gptoss_moe_route_scratch_bytes(T, E, top_k), dtype=torch.uint8, device=device)
+
+
+def route(x, router_w, router_b, top_k: int, logits_fp32: bool = False, stream=None, out=None, scratch=None):
+    """Router GEMV + top-k softmax (gptoss_moe_route): (logits, idx, weights).
+    out: preallocated (logits, idx, weights); scratch: from route_scratch()."""
     T, H = x.shape
     E = router_w.shape[0]
     dev = x.device
-    logits = torch.empty((T, E), dtype=torch.float32 if logits_fp32 else torch.bfloat16, device=dev)
-    idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
-    w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
-    scratch = torch.zeros(_lib.gptoss_moe_route_scratch_bytes(T, E, top_k), dtype=torch.uint8, device=dev)
+    if out is None:
+        logits = torch.empty((T, E), dtype=torch.float32 if logits_fp32 else torch.bfloat16, device=dev)
+        idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+        w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    else:
+        logits, idx, w = out
+    if scratch is None:
+        scratch = route_scratch(T, E, top_k, dev)
     check(_lib.gptoss_moe_route(_ptr(x), _ptr(router_w), _ptr(router_b), T, E, H, top_k, 1 if logits_fp32 else 0,
                                 _ptr(logits), _ptr(idx), _ptr(w), _ptr(scratch), _stream(stream)))
     return logits, idx, w

@@ -153,15 +153,17 @@ int gptoss_moe_layer_set_trace_gate_up(gptoss_moe_layer* layer, int enable);
 
 /* Per-launch timing, the role of the reference's PROF regions
  * (include/profiler.h:20-30, src/engine/profiler.cu:106-360): with
- * max_forwards > 0 the next max_forwards forwards record HIP events on their
- * stream around the route, W1 and W2 launches.  profile_read waits for them
- * and returns the summed milliseconds per launch and the count of recorded
- * forwards.  Forwards captured in a hipGraph record the same events again on
- * every replay, so profile_read after a replay reads that replay.  Calling
- * set_profiling again re-arms; max_forwards = 0 turns recording off. */
+ * max_forwards > 0 the next max_forwards forwards time their route (or plan,
+ * for forward_routed), gate_up (W1), down (W2) and combine launches with HIP
+ * events stamped by each dispatch itself (hipExtLaunchKernelGGL: the
+ * kernel's execution alone).  Forwards captured into a hipGraph are not
+ * timed and use no slot.  profile_read waits for the events and returns the
+ * summed milliseconds per launch and the count of recorded forwards (any
+ * output pointer may be NULL).  Calling set_profiling again re-arms;
+ * max_forwards = 0 turns recording off. */
 int gptoss_moe_layer_set_profiling(gptoss_moe_layer* layer, int max_forwards);
 int gptoss_moe_layer_profile_read(gptoss_moe_layer* layer, float* route_ms, float* w1_ms,
-                                  float* w2_ms, int* n_forwards);
+                                  float* w2_ms, float* combine_ms, int* n_forwards);
 
 /* ---- Stage entry points (the reference's kernel launchers) --------------- */
 

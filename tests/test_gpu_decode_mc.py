@@ -248,3 +248,49 @@ def test_mc_graph_replay(gpu, orc, torch_mod):
             torch.cuda.synchronize()
             assert np.array_equal(host(so), eager[i]), (rep, i)
     check_layer_out(eager[1], orc.moe_forward(w, xs[1][0], xs[1][1], E, k, H, I), "mc graph eager vs oracle")
+
+
+def test_layer_profiling_events(gpu, torch_mod):
+    """gptoss_moe_layer_set_profiling / profile_read: four timed launches per
+    forward (route, gate_up, down, combine), positive and summing to at most
+    the forwards' wall interval; a forward captured into a graph is not timed
+    and leaves its slot to the next eager forward."""
+    torch = torch_mod
+    E, k, H, I, T = 16, 4, 128, 128, 8
+    w = moe_data.make_layer(71, E, H, I)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T, exact=False)
+    x, res = moe_data.make_tokens(71, T, H)
+    dx, dr = dev(x, torch), dev(res, torch)
+    out = torch.empty_like(dx)
+    L.layer.forward_prenormed(dx, dr, out=out)
+    torch.cuda.synchronize()
+    L.layer.set_profiling(3)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(3):
+        L.layer.forward_prenormed(dx, dr, out=out)
+    t1.record()
+    torch.cuda.synchronize()
+    r, a, b, c, n = L.layer.profile_read()
+    say("profiling eager ms", r, a, b, c, n, "wall", t0.elapsed_time(t1))
+    assert n == 3 and min(r, a, b, c) > 0.0
+    assert r + a + b + c <= t0.elapsed_time(t1) * 1.05
+    # graph capture: not timed; the replays match the eager result
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    L.layer.set_profiling(1)
+    with torch.cuda.graph(g, stream=s):
+        L.layer.forward_prenormed(dx, dr, out=out)
+    want = host(out)
+    for _ in range(2):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), want)
+    assert L.layer.profile_read()[4] == 0
+    L.layer.forward_prenormed(dx, dr, out=out)
+    r, a, b, c, n = L.layer.profile_read()
+    assert n == 1 and min(r, a, b, c) > 0.0
+    L.layer.set_profiling(0)
