@@ -451,11 +451,9 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ra.k = c.top_k;
   ra.logits_fp32 = c.logits_fp32;
   ra.logits = L->logits;
-  ra.xf = nullptr;
   ra.idx = L->idx;
   ra.w = L->w;
   ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks};
-  route_scratch_carve(L->route_scratch, L->cfg.max_tokens, c.num_experts, c.top_k, ra);
   const ProfForward pf = next_prof(L, s);
   ra.timer = pf.timer(0);
   HIP_TRY(launch_route(ra, s), "route launch");
@@ -606,11 +604,9 @@ int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t
   ra.k = k;
   ra.logits_fp32 = logits_fp32 ? 1 : 0;
   ra.logits = logits;
-  ra.xf = nullptr;
   ra.idx = idx;
   ra.w = w;
   ra.plan = PlanBufs{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-  route_scratch_carve(scratch, T, E, k, ra);
   HIP_TRY(launch_route(ra, static_cast<hipStream_t>(stream)), "route launch");
   return ok();
 }

@@ -16,10 +16,12 @@ struct KernelTimer {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 
+// Either event may be null (a sequence of launches timed from the first
+// one's start to the last one's stop).
 template <typename F, typename... Args>
 inline void gx_launch(F kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t s, const KernelTimer& t,
                       Args... args) {
-  if (t.start)
+  if (t.start || t.stop)
     hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(shmem), s, t.start, t.stop, 0, args...);
   else
     hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
@@ -95,20 +97,14 @@ struct RouteArgs {
   int T, E, H, k;
   int logits_fp32;         // 1: fp32 logits, 0: bf16 logits
   void* logits;            // [T][E]
-  float* xf;               // [T][H] fp32 copy of x, or null
   int32_t* idx;            // [T][k]
   float* w;                // [T][k]
   PlanBufs plan;           // plan outputs (all may be null to skip the plan)
-  uint32_t* group_counter; // [ceil(T/8)] zero at rest
-  uint32_t* done_counter;  // [1] zero at rest
-  float* xchg_logits;      // [T][E] fp32 exchange (the logits as rounded)
-  int32_t* xchg_idx;       // [T][k] exchange of the selections (T > 8)
-  KernelTimer timer;
+  KernelTimer timer;       // from the first launch's start to the last one's stop
 };
 
-// Bytes of route scratch: counters, then the exchange buffers (256-aligned).
+// Bytes of route scratch (reserved: the launches need none).
 size_t route_scratch_bytes(int T, int E, int k);
-void route_scratch_carve(void* scratch, int T, int E, int k, RouteArgs& a);
 hipError_t launch_route(const RouteArgs& a, hipStream_t s);
 
 // Standalone top-k softmax over given logits (bf16 or fp32).

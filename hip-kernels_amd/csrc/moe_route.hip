@@ -1,20 +1,23 @@
 // moe_route.hip -- router GEMV + top-k softmax + device routing plan (gfx950).
 //
-// One launch replaces the reference's router GEMV/GEMM (gemv_bf16.cu:40-130,
+// Replaces the reference's router GEMV/GEMM (gemv_bf16.cu:40-130,
 // cuda_utils.h:226-308), topk_softmax_forward (topk_softmax.cu:380-432),
 // moe_permute_classify (moe_permute.cu:129-179) and the host gather map
 // (moe_permute.cu:184-236, moe_layer.cu:1217-1234), with no host round trip:
 //
-//   grid (ceil(E/4), ceil(T/8)), 256 threads.  Work-group (g, tg) computes
-//   the logits of experts 4g..4g+3 for tokens 8tg..8tg+7 with the
-//   gemv_bf16_kernel summation tree.  The last work-group to finish a token
-//   group (atomic ticket) selects the top-k of its tokens; the last token
-//   group to finish builds the plan (histogram, exclusive scan, stable
-//   counting-sort gather map, permuted token list, active expert list); with
-//   a single token group (T <= 8) the selecting work-group builds it from
-//   LDS directly.  Values crossing work-groups go through write-through
-//   exchange buffers (no L2 flush).  Tickets are reset by their last holder,
-//   so the launch is replayable (hipGraph) without a memset.
+//   logits_kernel      each wave computes whole logits (TT tokens x EPW
+//                      experts) with the gemv_bf16_kernel summation tree;
+//   topk_plan_kernel   (T <= kTopkPlanMaxT) one work-group of 16 waves selects
+//                      every token's top-k and builds the plan from LDS;
+//   topk_kernel +      (larger T) top-k spread over the device, then the plan
+//   plan_kernel        from the selections.
+//
+// Kernel boundaries order the stages: no values cross work-groups inside a
+// launch, so there are no tickets, exchange buffers or cache maintenance.
+//
+// Lane reductions use the gfx950 cross-lane moves (v_permlane32_swap and
+// v_permlane16_swap for lanes 32 and 16 apart, DPP row_shl within 16-lane
+// rows) instead of LDS permutes: a reduction to lane 0 is 6 VALU steps.
 #include <float.h>
 
 #include "moe_device.h"
@@ -25,49 +28,13 @@ namespace gxmoe {
 namespace {
 
 constexpr int kRouteThreads = 256;
+constexpr int kPlanThreads = 1024;
+constexpr int kTopkPlanMaxT = 256;  // tokens of the single-work-group top-k + plan
 
 __device__ __forceinline__ float sanitize_logit(float v) {
   // topk_softmax.cu:47-52: NaN and +-Inf become -FLT_MAX.
   return ((__float_as_uint(v) & 0x7f800000u) == 0x7f800000u) ? -FLT_MAX : v;
 }
-
-// Cross-work-group exchange without cache maintenance: agent-scope relaxed
-// stores and loads write through / read past the per-XCD L2, so a writer
-// that waits for its stores (vmcnt 0) before taking a ticket, and a reader
-// that loads only after holding the last ticket, see each other's data.
-__device__ __forceinline__ void st_xchg(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_xchg(int32_t* p, int32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_xchg(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int32_t ld_xchg(const int32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
-__device__ __forceinline__ uint32_t take_ticket(uint32_t* counter) {
-  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void reset_ticket(uint32_t* counter) {
-  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Logit loaders for the top-k: a user buffer (bf16 or fp32) or the fp32
-// exchange row (already rounded as the logits are).
-struct LogitsUser {
-  const void* row;
-  bool f32;
-  __device__ float operator()(int e) const {
-    return f32 ? reinterpret_cast<const float*>(row)[e] : bf16_to_f32(reinterpret_cast<const uint16_t*>(row)[e]);
-  }
-};
-struct LogitsXchg {
-  const float* row;
-  __device__ float operator()(int e) const { return ld_xchg(row + e); }
-};
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   const uint32_t d[4] = {v.x, v.y, v.z, v.w};
@@ -78,62 +45,123 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   }
 }
 
-// Lane l's four logits (experts l, l+64, l+128, l+192); -FLT_MAX past E.
-template <typename Loader>
-__device__ __forceinline__ void load_token_logits(const Loader& load, int E, int lane, float (&v)[4]) {
+// Lane l + 16 / l + 32 values into lane l (for l below 16 / 32), and DPP
+// row_shl:m (lane l reads lane l + m of its 16-lane row).
+__device__ __forceinline__ uint32_t from_plus32(uint32_t x) {
+  return __builtin_amdgcn_permlane32_swap(x, x, false, false)[1];
+}
+__device__ __forceinline__ uint32_t from_plus16(uint32_t x) {
+  return __builtin_amdgcn_permlane16_swap(x, x, false, false)[1];
+}
+template <int M>
+__device__ __forceinline__ uint32_t from_plus_row(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x100 | M, 0xf, 0xf, true));
+}
+
+// The sum of the 64 lanes' values in the order of the xor butterfly of
+// gemv_bf16.cu:95-100 (lanes 32 apart added first, then 16, 8, 4, 2, 1):
+// lane 0 adds exactly the same pairs in the same order.  Valid in lane 0.
+__device__ __forceinline__ float tree_sum_lane0(float v) {
+  v = v + __uint_as_float(from_plus32(__float_as_uint(v)));
+  v = v + __uint_as_float(from_plus16(__float_as_uint(v)));
+  v = v + __uint_as_float(from_plus_row<8>(__float_as_uint(v)));
+  v = v + __uint_as_float(from_plus_row<4>(__float_as_uint(v)));
+  v = v + __uint_as_float(from_plus_row<2>(__float_as_uint(v)));
+  v = v + __uint_as_float(from_plus_row<1>(__float_as_uint(v)));
+  return v;
+}
+
+// Wave-uniform max / min of a per-lane u32.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, from_plus32(x));
+  x = max(x, from_plus16(x));
+  x = max(x, from_plus_row<8>(x));
+  x = max(x, from_plus_row<4>(x));
+  x = max(x, from_plus_row<2>(x));
+  x = max(x, from_plus_row<1>(x));
+  return __builtin_amdgcn_readfirstlane(x);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  x = min(x, from_plus32(x));
+  x = min(x, from_plus16(x));
+  x = min(x, from_plus_row<8>(x));
+  x = min(x, from_plus_row<4>(x));
+  x = min(x, from_plus_row<2>(x));
+  x = min(x, from_plus_row<1>(x));
+  return __builtin_amdgcn_readfirstlane(x);
+}
+
+// Selection key of a logit: larger key = earlier in the reference's order
+// (value descending; -0 and +0 equal).  After sanitizing, -FLT_MAX is never
+// selected (the reference compares strictly against -FLT_MAX,
+// topk_softmax.cu:133-159) and gets key 0.
+__device__ __forceinline__ uint32_t select_key(float v) {
+  if (v == -FLT_MAX) return 0u;
+  if (v == 0.0f) v = 0.0f;
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Logits of one token as the lanes of a wave hold them: expert lane + 64 j
+// (NV = ceil(E / 64) values per lane).
+template <bool F32, int NV>
+__device__ __forceinline__ void load_token_logits(const void* logits, int t, int E, int lane, float (&v)[NV]) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int e = lane + 64 * j;
-    v[j] = (e < E) ? load(e) : -FLT_MAX;
+  for (int j = 0; j < NV; ++j) {
+    const int e = lane + kWave * j;
+    const size_t o = static_cast<size_t>(t) * E + e;
+    v[j] = e >= E ? -FLT_MAX
+           : F32  ? reinterpret_cast<const float*>(logits)[o]
+                  : bf16_to_f32(reinterpret_cast<const uint16_t*>(logits)[o]);
   }
 }
 
-// Top-k of one token by one wave from its lanes' logits v (as loaded by
-// load_token_logits; sanitised here).  Each round takes the largest visible
-// logit (> -FLT_MAX) by (value desc, index asc); a round with nothing visible
-// yields (-FLT_MAX, -1), the reference's padding (topk_softmax.cu:133-159).
-// Lane 0 then applies the softmax over the k selected values in the order of
-// the reference variant (v1 sequential sum for T <= 8, v2 xor-butterfly sum
-// otherwise).
-__device__ __forceinline__ void topk_select(float (&v)[4], int k, int variant, int32_t* out_idx, float* out_w,
-                                            int32_t* tokens_per_expert, int32_t* lds_idx, int lane) {
+// Sum of the k selected exponentials in the reference's order: v1
+// (topk_softmax.cu:199-204) adds them in slot order; v2 (topk_softmax.cu:
+// 358-362) ends every lane of its butterfly with the tree t[s] + t[s ^ m],
+// m = k/2 .. 1, whose value in slot 0 this returns.
+template <int K>
+__device__ __forceinline__ float slot_sum(const float* ex, int variant) {
+  if (variant == 1) {
+    float sum = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = sanitize_logit(v[j]);
-  float sel_v[kMaxTopK];
-  int sel_i[kMaxTopK];
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) {
-    sel_v[s] = -FLT_MAX;
-    sel_i[s] = -1;
-    if (s < k) {
-      float bv = -FLT_MAX;
-      int bi = -1;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) {
-        float ov = __shfl_xor(bv, m, kWave);
-        int oi = __shfl_xor(bi, m, kWave);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-      }
-      sel_v[s] = bv;
-      sel_i[s] = bi;
-      if (bi >= 0 && (bi & 63) == lane) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if ((bi >> 6) == j) v[j] = -FLT_MAX;
-      }
-    }
+    for (int s = 0; s < K; ++s) sum = sum + ex[s];
+    return sum;
   }
-  if (lane != 0) return;
-  if (sel_i[0] == -1) {  // topk_softmax.cu:339-346: no finite logit at all
+  float t[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) t[s] = ex[s];
+#pragma unroll
+  for (int m = K >> 1; m > 0; m >>= 1) {
+    float u[K];
+#pragma unroll
+    for (int s = 0; s < K; ++s) u[s] = t[s] + t[s ^ m];
+#pragma unroll
+    for (int s = 0; s < K; ++s) t[s] = u[s];
+  }
+  return t[0];
+}
+
+__device__ __forceinline__ float slot_sum_k(const float* ex, int k, int variant) {
+  switch (k) {
+    case 1: return slot_sum<1>(ex, variant);
+    case 2: return slot_sum<2>(ex, variant);
+    case 4: return slot_sum<4>(ex, variant);
+    default: return slot_sum<8>(ex, variant);
+  }
+}
+
+// Softmax over the selected slots and the slot outputs (topk_softmax.cu:
+// 160-215, 339-375): sel_i[0] == -1 means no finite logit at all (experts
+// 0..k-1, weight 1/k); padded slots (index -1) get weight 0.
+__device__ __forceinline__ void write_slots(const float* sel_v, const int* sel_i, int k, int variant, int32_t* out_idx,
+                                            float* out_w, int32_t* tokens_per_expert) {
+  if (sel_i[0] == -1) {
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s)
       if (s < k) {
         out_idx[s] = s;
         out_w[s] = 1.0f / static_cast<float>(k);
-        if (lds_idx) lds_idx[s] = s;
       }
     if (tokens_per_expert)
       for (int s = 0; s < k; ++s) atomicAdd(&tokens_per_expert[s], 1);
@@ -146,120 +174,157 @@ __device__ __forceinline__ void topk_select(float (&v)[4], int k, int variant, i
     if (s < k && sel_v[s] > mx) mx = sel_v[s];
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s) ex[s] = (s < k) ? gx_expf(sel_v[s] - mx) : 0.0f;
-  float sum;
-  if (variant == 1) {  // topk_softmax.cu:199-204
-    sum = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) sum = sum + ex[s];
-  } else {  // topk_softmax.cu:358-362, the tree every lane of the butterfly ends with
-    float t[kMaxTopK];
-#pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s) t[s] = ex[s];
-    for (int m = k >> 1; m > 0; m >>= 1) {
-      float u[kMaxTopK];
-#pragma unroll
-      for (int s = 0; s < kMaxTopK; ++s) u[s] = t[s] + t[s ^ m];
-#pragma unroll
-      for (int s = 0; s < kMaxTopK; ++s) t[s] = u[s];
-    }
-    sum = t[0];
-  }
-  float inv = 1.0f / sum;
+  const float inv = 1.0f / slot_sum_k(ex, k, variant);
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s) {
     if (s < k) {
       out_idx[s] = sel_i[s];
       out_w[s] = (sel_i[s] < 0) ? 0.0f : ex[s] * inv;
-      if (lds_idx) lds_idx[s] = sel_i[s];
       if (tokens_per_expert && sel_i[s] >= 0) atomicAdd(&tokens_per_expert[sel_i[s]], 1);
     }
   }
 }
 
-template <typename Loader>
-__device__ __forceinline__ void topk_one_token(const Loader& load, int E, int k, int variant,
-                                               int32_t* out_idx, float* out_w,
-                                               int32_t* tokens_per_expert, int32_t* lds_idx, int lane) {
-  float v[4];
-  load_token_logits(load, E, lane, v);
-  topk_select(v, k, variant, out_idx, out_w, tokens_per_expert, lds_idx, lane);
+// Top-k of one token and the softmax over the selected k (topk_softmax.cu:
+// 77-375), from the lanes' logits v.  Round s takes the largest visible key
+// (value desc) and, among equal keys, the smallest expert index; a round with
+// nothing visible yields (-FLT_MAX, -1), the reference's padding.  Lane 0
+// writes the slot outputs (v1 sequential sum for variant 1, v2 butterfly tree
+// otherwise).  Control flow is wave-uniform.
+template <int NV>
+__device__ __forceinline__ void topk_token(float (&v)[NV], int k, int variant, int32_t* out_idx, float* out_w,
+                                           int32_t* tokens_per_expert, int lane) {
+  uint32_t key[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    v[j] = sanitize_logit(v[j]);
+    key[j] = select_key(v[j]);
+  }
+  float sel_v[kMaxTopK];
+  int sel_i[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    sel_v[s] = -FLT_MAX;
+    sel_i[s] = -1;
+    if (s < k) {
+      uint32_t best = key[0];
+#pragma unroll
+      for (int j = 1; j < NV; ++j) best = max(best, key[j]);
+      const uint32_t K = wave_max_u32(best);
+      if (K != 0u) {
+        uint32_t cand = 0xffffffffu;
+#pragma unroll
+        for (int j = NV - 1; j >= 0; --j)
+          if (key[j] == K) cand = static_cast<uint32_t>(lane + kWave * j);
+        const int I = static_cast<int>(wave_min_u32(cand));
+        const int jj = I >> 6, ll = I & 63;
+        float val = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          if (j == jj) {
+            val = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v[j])), ll)));
+            if (lane == ll) key[j] = 0u;
+          }
+        }
+        sel_v[s] = val;
+        sel_i[s] = I;
+      }
+    }
+  }
+  if (lane != 0) return;
+  write_slots(sel_v, sel_i, k, variant, out_idx, out_w, tokens_per_expert);
 }
 
-// Block-wide (256 threads) dispatch plan over the T*k slots of `idx`:
-// counts, exclusive offsets, a gather map that is stable in slot order (the
-// counting sort of moe_permute.cu:184-236), the permuted token list and the
-// ascending list of experts with at least one slot.  Slots with an index
-// outside [0, E) get gather_map = -1 and are not dispatched.
-template <typename IdxFn>
+// Dispatch plan over the T*k slots of `idx` with NT threads: counts,
+// exclusive offsets, a gather map that is stable in slot order (the counting
+// sort of moe_permute.cu:184-236), the permuted token list, the ascending
+// list of experts with at least one slot and the task records.  Slots with an
+// index outside [0, E) get gather_map = -1 and are not dispatched.
+template <int NT, typename IdxFn>
 __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
+  constexpr int NW = NT / kWave;
+  static_assert(NT >= kMaxExperts, "one thread per expert in the scan");
   __shared__ int s_off[kMaxExperts + 1];
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_run[kMaxExperts];
-  __shared__ int s_wc[4][kMaxExperts];
+  __shared__ int s_wc[NW][kMaxExperts];
   __shared__ int s_aidx[kMaxExperts];
-  __shared__ unsigned long long s_mask[4];
-  __shared__ int s_wsum[4];
+  __shared__ unsigned long long s_mask[kMaxExperts / kWave];
+  __shared__ int s_wsum[kMaxExperts / kWave];
   const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
   const int S = T * k;
 
-  // slot tid's expert is read once and reused by the rank pass below
-  const int e_first = (tid < S) ? idx(tid) : -1;
-  auto slot_expert = [&](int s) { return s == tid ? e_first : idx(s); };
-  s_cnt[tid] = 0;
-  s_run[tid] = 0;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) s_wc[w][tid] = 0;
+  if (tid < kMaxExperts) {
+    s_cnt[tid] = 0;
+    s_run[tid] = 0;
+  }
+  for (int i = tid; i < NW * kMaxExperts; i += NT) (&s_wc[0][0])[i] = 0;
   __syncthreads();
-  for (int s = tid; s < S; s += kRouteThreads) {
-    int e = slot_expert(s);
+  for (int s = tid; s < S; s += NT) {
+    const int e = idx(s);
     if (e >= 0 && e < E) atomicAdd(&s_cnt[e], 1);
   }
   __syncthreads();
 
-  // exclusive scan of the counts (E <= 256: one value per thread)
-  const int c = (tid < E) ? s_cnt[tid] : 0;
-  int incl = c;
+  // exclusive scan of the counts (E <= 256: one value per thread of waves 0..3)
+  int c = 0, incl = 0;
+  bool act = false;
+  unsigned long long am = 0ull;
+  if (tid < kMaxExperts) {  // wave-uniform
+    c = (tid < E) ? s_cnt[tid] : 0;
+    incl = c;
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
-  if (lane == 63) s_wsum[warp] = incl;
-  const bool act = (tid < E) && (c > 0);
-  const unsigned long long am = __ballot(act);
-  if (lane == 0) s_mask[warp] = am;
-  __syncthreads();
-  int base = 0, abase = 0;
-  for (int w = 0; w < warp; ++w) { base += s_wsum[w]; abase += __popcll(s_mask[w]); }
-  const int excl = base + incl - c;
-  if (tid < E) {
-    s_off[tid] = excl;
-    p.counts[tid] = c;
-    p.offsets[tid] = excl;
-  }
-  if (tid == E - 1) { s_off[E] = excl + c; p.offsets[E] = excl + c; }
-  const int aidx = abase + __popcll(am & ((1ull << lane) - 1ull));
-  const int nact = __popcll(s_mask[0]) + __popcll(s_mask[1]) + __popcll(s_mask[2]) + __popcll(s_mask[3]);
-  if (act) {
-    p.active[aidx] = tid;
-    s_aidx[tid] = aidx;
-    if (p.tasks) {
-      int32_t* t = p.tasks + static_cast<size_t>(aidx) * kTaskInts;
-      t[0] = tid;
-      t[1] = excl;
-      t[2] = c;
-      t[3] = 0;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += o;
     }
+    if (lane == 63) s_wsum[warp] = incl;
+    act = (tid < E) && (c > 0);
+    am = __ballot(act);
+    if (lane == 0) s_mask[warp] = am;
   }
-  if (p.tasks && tid < E && tid >= nact) p.tasks[static_cast<size_t>(tid) * kTaskInts] = -1;
+  __syncthreads();
+  int nact = 0;
+#pragma unroll
+  for (int w = 0; w < kMaxExperts / kWave; ++w) nact += __popcll(s_mask[w]);
+  if (tid < kMaxExperts) {
+    int base = 0, abase = 0;
+    for (int w = 0; w < warp; ++w) {
+      base += s_wsum[w];
+      abase += __popcll(s_mask[w]);
+    }
+    const int excl = base + incl - c;
+    if (tid < E) {
+      s_off[tid] = excl;
+      p.counts[tid] = c;
+      p.offsets[tid] = excl;
+    }
+    if (tid == E - 1) {
+      s_off[E] = excl + c;
+      p.offsets[E] = excl + c;
+    }
+    const int aidx = abase + __popcll(am & ((1ull << lane) - 1ull));
+    if (act) {
+      p.active[aidx] = tid;
+      s_aidx[tid] = aidx;
+      if (p.tasks) {
+        int32_t* t = p.tasks + static_cast<size_t>(aidx) * kTaskInts;
+        t[0] = tid;
+        t[1] = excl;
+        t[2] = c;
+        t[3] = 0;
+      }
+    }
+    if (p.tasks && tid < E && tid >= nact) p.tasks[static_cast<size_t>(tid) * kTaskInts] = -1;
+  }
   if (tid == 0) *p.n_active = nact;
   __syncthreads();
 
-  // stable positions, 256 slots per round
-  for (int r0 = 0; r0 < S; r0 += kRouteThreads) {
+  // stable positions, NT slots per round: rank among equal experts of the
+  // wave by ballots, then the counts of earlier waves and rounds
+  for (int r0 = 0; r0 < S; r0 += NT) {
     const int s = r0 + tid;
-    const int e = (s < S) ? slot_expert(s) : -1;
+    const int e = (s < S) ? idx(s) : -1;
     const bool valid = (e >= 0 && e < E);
     unsigned long long peers = __ballot(valid);
 #pragma unroll
@@ -283,263 +348,372 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
     }
     __syncthreads();
     if (tid < E) {
-      s_run[tid] += s_wc[0][tid] + s_wc[1][tid] + s_wc[2][tid] + s_wc[3][tid];
+      int add = 0;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) s_wc[w][tid] = 0;
+      for (int w = 0; w < NW; ++w) {
+        add += s_wc[w][tid];
+        s_wc[w][tid] = 0;
+      }
+      s_run[tid] += add;
     }
     __syncthreads();
   }
 }
 
-// The H%8 tail of the router chains (gemv_bf16.cu:118-125), after the chunks.
-__device__ __forceinline__ void router_tail(const uint16_t* xr, const RouteArgs& a, int e0, int KV, int tid,
-                                            float (&acc)[kRouteExpertsPerGroup]) {
-  const int H = a.H, E = a.E;
-  for (int kk = KV * 8 + tid; kk < H; kk += kRouteThreads) {
-    const float xs = bf16_to_f32(xr[kk]);
-#pragma unroll
-    for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee)
-      if (e0 + ee < E) acc[ee] = __builtin_fmaf(xs, bf16_to_f32(a.W[static_cast<size_t>(e0 + ee) * H + kk]), acc[ee]);
-  }
-}
-
-// Logits of one token with the gemv_bf16_kernel tree (gemv_bf16.cu:57-129):
-// thread tid chains fmaf over 8-element chunks tid, tid+256, ... (NJ of
-// them at most), then the H%8 tail.  xs_chunk(j) / ws_chunk(ee, j) give chunk
-// tid + 256 j.
-template <int NJ, typename XFn, typename WFn>
-__device__ __forceinline__ void router_chains(XFn xs_chunk, WFn ws_chunk, const uint16_t* xr, const RouteArgs& a,
-                                              int e0, int KV, int tid, float (&acc)[kRouteExpertsPerGroup]) {
-  const int E = a.E;
-#pragma unroll
-  for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) acc[ee] = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    if (tid + kRouteThreads * j < KV) {
-      float xs[8];
-      unpack_bf16x8(xs_chunk(j), xs);
-#pragma unroll
-      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) {
-        if (e0 + ee < E) {
-          float ws[8];
-          unpack_bf16x8(ws_chunk(ee, j), ws);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[ee] = __builtin_fmaf(xs[i], ws[i], acc[ee]);
-        }
-      }
-    }
-  }
-  router_tail(xr, a, e0, KV, tid, acc);
-}
-
-// NJ > 0: every thread holds at most NJ chunks (H <= 2048 * NJ); all of the
-// work-group's router and token loads are issued before the first FMA.
-// NJ == 0: any H, one chunk in flight at a time.
-template <bool F32, int NJ>
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
-  const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
-  const int e0 = blockIdx.x * kRouteExpertsPerGroup;
-  const int t0 = blockIdx.y * kRouteTokensPerGroup;
-  const int tn = min(kRouteTokensPerGroup, a.T - t0);
-  const int H = a.H, E = a.E;
+// Logits of TT tokens x EPW experts per wave (work-group: 4 waves, 4 EPW
+// consecutive experts) with the gemv_bf16_kernel tree (gemv_bf16.cu:57-129):
+// logical thread tau = lane + 64 j (j = 0..3) chains fmaf over the 8-element
+// chunks tau, tau + 256, ... in that order; the chains of wave j are summed
+// by the xor-butterfly tree; the four wave sums are added in order from 0;
+// + bias; bf16 (or fp32) rounding.  Lane l holds chain j of every (token,
+// expert) pair of the wave in acc[t][e][j]; its chunk positions are
+// c = l + 64 p, p = j + 4 r.  NCH > 0: every position is loaded before the
+// first FMA (H <= 512 NCH); NCH == 0: any H, one position at a time.
+template <int TT, int EPW, int NCH, bool F32>
+__global__ __launch_bounds__(kRouteThreads) void logits_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ W,
+                                                               const uint16_t* __restrict__ bias, int T, int E, int H,
+                                                               void* __restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int e0 = (blockIdx.x * 4 + wv) * EPW;
+  const int t0 = blockIdx.y * TT;
+  if (e0 >= E) return;  // wave-uniform; the kernel has no barriers
   const int KV = H >> 3;
-  __shared__ float red[kRouteTokensPerGroup][kRouteExpertsPerGroup][4];
-  __shared__ uint32_t s_ticket;
-
-  // Logits: per token, the chains of router_chains; xor butterfly per wave;
-  // the 4 wave sums are added in order from 0.
-  constexpr int kNJ = NJ > 0 ? NJ : 1;
-  uint4 wv[kRouteExpertsPerGroup][kNJ];
-  uint4 xv[kRouteTokensPerGroup][kNJ];
-  if constexpr (NJ > 0) {
+  float acc[TT][EPW][4];
 #pragma unroll
-    for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee)
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int kv = tid + kRouteThreads * j;
-        wv[ee][j] = (kv < KV && e0 + ee < E)
-                        ? *reinterpret_cast<const uint4*>(a.W + static_cast<size_t>(e0 + ee) * H + kv * 8)
-                        : make_uint4(0, 0, 0, 0);
-      }
+    for (int e = 0; e < EPW; ++e)
 #pragma unroll
-    for (int tt = 0; tt < kRouteTokensPerGroup; ++tt)
+      for (int j = 0; j < 4; ++j) acc[t][e][j] = 0.0f;
+  // rows past T / E read row 0 (their results are not stored)
+  const uint16_t* xr[TT];
+  const uint16_t* wr[EPW];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int kv = tid + kRouteThreads * j;
-        xv[tt][j] = (tt < tn && kv < KV)
-                        ? *reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(t0 + tt) * H + kv * 8)
-                        : make_uint4(0, 0, 0, 0);
-      }
-  }
+  for (int t = 0; t < TT; ++t) xr[t] = x + static_cast<size_t>(t0 + t < T ? t0 + t : 0) * H;
 #pragma unroll
-  for (int tt = 0; tt < kRouteTokensPerGroup; ++tt) {
-    if (tt >= tn) break;
-    const uint16_t* xr = a.x + static_cast<size_t>(t0 + tt) * H;
-    float acc[kRouteExpertsPerGroup];
-    if constexpr (NJ > 0) {
-      router_chains<NJ>([&](int j) { return xv[tt][j]; }, [&](int ee, int j) { return wv[ee][j]; }, xr, a, e0, KV,
-                        tid, acc);
-    } else {
-      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) acc[ee] = 0.0f;
-      for (int kv = tid; kv < KV; kv += kRouteThreads) {
-        float xs[8];
-        unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + kv * 8), xs);
+  for (int e = 0; e < EPW; ++e) wr[e] = W + static_cast<size_t>(e0 + e < E ? e0 + e : 0) * H;
+  auto fma_chunk = [&](int j, const uint4 (&xv)[TT], const uint4 (&wv4)[EPW]) __attribute__((always_inline)) {
+    float wf[EPW][8];
 #pragma unroll
-        for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) {
-          if (e0 + ee < E) {
-            float ws[8];
-            unpack_bf16x8(*reinterpret_cast<const uint4*>(a.W + static_cast<size_t>(e0 + ee) * H + kv * 8), ws);
+    for (int e = 0; e < EPW; ++e) unpack_bf16x8(wv4[e], wf[e]);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[ee] = __builtin_fmaf(xs[i], ws[i], acc[ee]);
-          }
+    for (int t = 0; t < TT; ++t) {
+      float xf[8];
+      unpack_bf16x8(xv[t], xf);
+#pragma unroll
+      for (int e = 0; e < EPW; ++e)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[t][e][j] = __builtin_fmaf(xf[i], wf[e][i], acc[t][e][j]);
+    }
+  };
+  if constexpr (NCH > 0) {
+    uint4 xv[NCH][TT], wv4[NCH][EPW];
+#pragma unroll
+    for (int q = 0; q < NCH; ++q) {
+      const int c = min(lane + kWave * q, KV - 1);  // positions past KV load a valid chunk, unused
+#pragma unroll
+      for (int t = 0; t < TT; ++t) xv[q][t] = *reinterpret_cast<const uint4*>(xr[t] + c * 8);
+#pragma unroll
+      for (int e = 0; e < EPW; ++e) wv4[q][e] = *reinterpret_cast<const uint4*>(wr[e] + c * 8);
+    }
+#pragma unroll
+    for (int q = 0; q < NCH; ++q)
+      if (lane + kWave * q < KV) fma_chunk(q & 3, xv[q], wv4[q]);
+  } else {
+    for (int r = 0; kRouteThreads * r < KV; ++r) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = lane + kWave * j + kRouteThreads * r;
+        if (c < KV) {
+          uint4 xv[TT], wv4[EPW];
+#pragma unroll
+          for (int t = 0; t < TT; ++t) xv[t] = *reinterpret_cast<const uint4*>(xr[t] + c * 8);
+#pragma unroll
+          for (int e = 0; e < EPW; ++e) wv4[e] = *reinterpret_cast<const uint4*>(wr[e] + c * 8);
+          fma_chunk(j, xv, wv4);
         }
       }
-      router_tail(xr, a, e0, KV, tid, acc);
-    }
-#pragma unroll
-    for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) acc[ee] = wave_butterfly_sum(acc[ee]);
-    if (lane == 0) {
-#pragma unroll
-      for (int ee = 0; ee < kRouteExpertsPerGroup; ++ee) red[tt][ee][warp] = acc[ee];
     }
   }
-  __syncthreads();
-  if (tid < tn * kRouteExpertsPerGroup) {
-    const int tt = tid / kRouteExpertsPerGroup, ee = tid % kRouteExpertsPerGroup, e = e0 + ee;
-    if (e < E) {
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) {
       float v = 0.0f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) v = v + red[tt][ee][w];
-      if (a.b != nullptr) v = v + bf16_to_f32(a.b[e]);
-      const size_t o = static_cast<size_t>(t0 + tt) * E + e;
-      if constexpr (F32) {
-        reinterpret_cast<float*>(a.logits)[o] = v;
-      } else {
-        const uint16_t h = f32_to_bf16(v);
-        reinterpret_cast<uint16_t*>(a.logits)[o] = h;
-        v = bf16_to_f32(h);
+      for (int j = 0; j < 4; ++j) v = v + tree_sum_lane0(acc[t][e][j]);
+      if (lane == 0 && t0 + t < T && e0 + e < E) {
+        if (bias != nullptr) v = v + bf16_to_f32(bias[e0 + e]);
+        const size_t o = static_cast<size_t>(t0 + t) * E + e0 + e;
+        if constexpr (F32) reinterpret_cast<float*>(logits)[o] = v;
+        else reinterpret_cast<uint16_t*>(logits)[o] = f32_to_bf16(v);
       }
-      st_xchg(a.xchg_logits + o, v);
     }
   }
+}
 
-  // The last expert group of this token group selects the top-k.
-  wait_stores();
-  __syncthreads();
-  if (tid == 0) s_ticket = take_ticket(&a.group_counter[blockIdx.y]);
-  __syncthreads();
-  if (s_ticket != gridDim.x - 1) return;
-  if (tid == 0) reset_ticket(&a.group_counter[blockIdx.y]);
-  const int variant = (a.T <= 8) ? 1 : 2;  // topk_softmax.cu:399
-  const bool one_group = gridDim.y == 1;
-  __shared__ int32_t s_idx[kRouteTokensPerGroup * kMaxTopK];
-  // Wave w selects tokens w and w + 4; both rows' logits are loaded first.
-  static_assert(kRouteTokensPerGroup == 8, "two tokens per wave");
-  float lv[2][4];
+// Top-k softmax of every token, one token per wave.
+template <bool F32, int NV>
+__global__ __launch_bounds__(kRouteThreads) void topk_kernel(const void* logits, int T, int E, int k, int variant,
+                                                            int32_t* idx, float* w, int32_t* tpe) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (kRouteThreads / kWave) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float v[NV];
+  load_token_logits<F32, NV>(logits, t, E, lane, v);
+  topk_token(v, k, variant, idx + static_cast<size_t>(t) * k, w + static_cast<size_t>(t) * k, tpe, lane);
+}
+
+// Top-k of all T <= kTopkPlanMaxT tokens (16 waves, tokens w, w + 16, ...),
+// then the plan from the selections.  Each wave loads all its tokens' logits
+// before it stores anything (gfx9 counts stores in vmcnt, so a load issued
+// after a store waits for the store's completion), keeps the selections and
+// weights in LDS and the work-group writes them out once.
+template <bool F32, int NV>
+__global__ __launch_bounds__(kPlanThreads) void topk_plan_kernel(const void* logits, int T, int E, int k,
+                                                                int variant, int32_t* idx, float* w, PlanBufs p) {
+  constexpr int kWaves = kPlanThreads / kWave;
+  constexpr int kTPW = kTopkPlanMaxT / kWaves;  // tokens per wave
+  __shared__ int32_t s_idx[kTopkPlanMaxT * kMaxTopK];
+  __shared__ float s_w[kTopkPlanMaxT * kMaxTopK];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  float v[kTPW][NV];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int tt = warp + 4 * h;
-    if (tt < tn) load_token_logits(LogitsXchg{a.xchg_logits + static_cast<size_t>(t0 + tt) * E}, E, lane, lv[h]);
+  for (int i = 0; i < kTPW; ++i) {
+    const int t = wv + kWaves * i;
+    load_token_logits<F32, NV>(logits, t < T ? t : 0, E, lane, v[i]);  // rows past T read row 0, unused
   }
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int tt = warp + 4 * h;
-    if (tt < tn) {
-      const int t = t0 + tt;
-      topk_select(lv[h], a.k, variant, a.idx + static_cast<size_t>(t) * a.k, a.w + static_cast<size_t>(t) * a.k,
-                  nullptr, one_group ? s_idx + tt * a.k : nullptr, lane);
-      if (!one_group && lane == 0)
-        for (int s2 = 0; s2 < a.k; ++s2)
-          st_xchg(a.xchg_idx + static_cast<size_t>(t) * a.k + s2, a.idx[static_cast<size_t>(t) * a.k + s2]);
+  for (int i = 0; i < kTPW; ++i) {
+    const int t = wv + kWaves * i;
+    if (t < T) topk_token(v[i], k, variant, s_idx + t * k, s_w + t * k, nullptr, lane);
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < T * k; q += kPlanThreads) {
+    idx[q] = s_idx[q];
+    w[q] = s_w[q];
+  }
+  build_plan<kPlanThreads>([&](int s) { return s_idx[s]; }, T, k, E, p);
+}
+
+// Top-k + plan for T <= 64 tokens with one lane per token (E <= 128, a
+// multiple of 8): wave w sorts the 8 logits of experts 8w..8w+7 of its
+// lane's token (a depth-6 sorting network on 64-bit entries, key << 32 |
+// 0xffff - expert: larger = earlier in the reference's order, 0 = not
+// selectable), keeps the top K, and the lists of the E/8 slices meet in a
+// 4-level tree of bitonic merges through LDS.  Each lane then applies its
+// token's softmax.  Every step is a few dependent instructions on all tokens
+// at once, where one wave per token would chain k wave-wide reductions.
+constexpr int kLaneTopkSlice = 8;
+constexpr int kLaneTopkMaxT = kWave;
+
+__device__ __forceinline__ void ce_desc(uint64_t& a, uint64_t& b) {
+  const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+  a = hi;
+  b = lo;
+}
+
+template <bool F32, int K>
+__global__ __launch_bounds__(kPlanThreads) void topk_plan_lanes_kernel(const void* logits, int T, int E, int variant,
+                                                                      int32_t* idx, float* w, PlanBufs p) {
+  constexpr int kSlices = kPlanThreads / kWave;  // 16: up to 128 experts
+  __shared__ uint64_t s_list[kSlices][kLaneTopkMaxT][K];
+  __shared__ int32_t s_idx[kLaneTopkMaxT * K];
+  __shared__ float s_w[kLaneTopkMaxT * K];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int nsl = (E + kLaneTopkSlice - 1) / kLaneTopkSlice;
+  const int t = lane;
+  if (wv < nsl) {
+    const int e0 = wv * kLaneTopkSlice;
+    float v[kLaneTopkSlice];
+    const size_t o = static_cast<size_t>(t < T ? t : 0) * E + e0;  // lanes past T read token 0, unused
+    if constexpr (F32) {
+      const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(logits) + o);
+      const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(logits) + o + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+      const uint4 a = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(logits) + o);
+      unpack_bf16x8(a, v);
     }
+    uint64_t en[kLaneTopkSlice];
+#pragma unroll
+    for (int i = 0; i < kLaneTopkSlice; ++i) {
+      const uint32_t key = select_key(sanitize_logit(v[i]));
+      en[i] = key ? (static_cast<uint64_t>(key) << 32) | static_cast<uint32_t>(0xffff - (e0 + i)) : 0ull;
+    }
+    // optimal 19-comparator sorting network for 8 inputs (descending)
+    ce_desc(en[0], en[2]); ce_desc(en[1], en[3]); ce_desc(en[4], en[6]); ce_desc(en[5], en[7]);
+    ce_desc(en[0], en[4]); ce_desc(en[1], en[5]); ce_desc(en[2], en[6]); ce_desc(en[3], en[7]);
+    ce_desc(en[0], en[1]); ce_desc(en[2], en[3]); ce_desc(en[4], en[5]); ce_desc(en[6], en[7]);
+    ce_desc(en[2], en[4]); ce_desc(en[3], en[5]);
+    ce_desc(en[1], en[4]); ce_desc(en[3], en[6]);
+    ce_desc(en[1], en[2]); ce_desc(en[3], en[4]); ce_desc(en[5], en[6]);
+#pragma unroll
+    for (int i = 0; i < K; ++i) s_list[wv][t][i] = i < kLaneTopkSlice ? en[i < kLaneTopkSlice ? i : 0] : 0ull;
   }
-  if (a.plan.counts == nullptr) return;
-  if (one_group) {  // T <= 8: this work-group holds every token's selection
+  __syncthreads();
+  // merge tree: at width d, wave w merges slice lists 2dw and 2dw + d
+  for (int d = 1; d < nsl; d <<= 1) {
+    const int a = 2 * d * wv, b = a + d;
+    if (b < nsl) {
+      uint64_t c[K];
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        const uint64_t x = s_list[a][t][i], y = s_list[b][t][K - 1 - i];
+        c[i] = x > y ? x : y;
+      }
+#pragma unroll
+      for (int h = K >> 1; h > 0; h >>= 1)
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+          if ((i & h) == 0) ce_desc(c[i], c[i + h]);
+#pragma unroll
+      for (int i = 0; i < K; ++i) s_list[a][t][i] = c[i];
+    }
     __syncthreads();
-    build_plan([&](int s2) { return s_idx[s2]; }, a.T, a.k, E, a.plan);
-    return;
   }
+  if (wv == 0 && t < T) {
+    float sel_v[kMaxTopK];
+    int sel_i[kMaxTopK];
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxTopK; ++s2) {
+      sel_v[s2] = -FLT_MAX;
+      sel_i[s2] = -1;
+      if (s2 < K) {
+        const uint64_t en = s_list[0][t][s2 < K ? s2 : 0];
+        if (en) {
+          const uint32_t key = static_cast<uint32_t>(en >> 32);
+          sel_v[s2] = __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+          sel_i[s2] = 0xffff - static_cast<int>(en & 0xffffu);
+        }
+      }
+    }
+    write_slots(sel_v, sel_i, K, variant, s_idx + t * K, s_w + t * K, nullptr);
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < T * K; q += kPlanThreads) {
+    idx[q] = s_idx[q];
+    w[q] = s_w[q];
+  }
+  build_plan<kPlanThreads>([&](int s2) { return s_idx[s2]; }, T, K, E, p);
+}
 
-  // The last token group builds the plan over all T*k slots.
-  wait_stores();
-  __syncthreads();
-  if (tid == 0) s_ticket = take_ticket(a.done_counter);
-  __syncthreads();
-  if (s_ticket != gridDim.y - 1) return;
-  if (tid == 0) reset_ticket(a.done_counter);
-  build_plan([&](int s2) { return ld_xchg(a.xchg_idx + s2); }, a.T, a.k, E, a.plan);
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* idx, int T, int k, int E, PlanBufs p) {
+  build_plan<kPlanThreads>([&](int s) { return idx[s]; }, T, k, E, p);
 }
 
 template <bool F32>
-__global__ __launch_bounds__(kRouteThreads) void topk_kernel(const void* logits, int T, int E, int k,
-                                                            int32_t* idx, float* w, int32_t* tpe) {
-  const int lane = threadIdx.x & 63, warp = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + warp;
-  if (t >= T) return;
-  const void* row = F32 ? static_cast<const void*>(reinterpret_cast<const float*>(logits) + static_cast<size_t>(t) * E)
-                        : static_cast<const void*>(reinterpret_cast<const uint16_t*>(logits) + static_cast<size_t>(t) * E);
-  topk_one_token(LogitsUser{row, F32}, E, k, (T <= 8) ? 1 : 2, idx + static_cast<size_t>(t) * k,
-                 w + static_cast<size_t>(t) * k, tpe, nullptr, lane);
-}
-
-__global__ __launch_bounds__(kRouteThreads) void plan_kernel(const int32_t* idx, int T, int k, int E,
-                                                            PlanBufs p) {
-  build_plan([&](int s) { return idx[s]; }, T, k, E, p);
+void launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t) {
+  // tokens per wave x experts per wave: more waves for few tokens (latency),
+  // more reuse of each loaded row for many.  Up to H = 3072 the decode
+  // shapes load every chunk up front.
+  const bool upfront = (a.H >> 3) <= kWave * 6;
+  if (a.T <= 8 && upfront) {
+    gx_launch(logits_kernel<1, 1, 6, F32>, dim3((a.E + 3) / 4, a.T), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b,
+              a.T, a.E, a.H, a.logits);
+  } else if (a.T <= 64 && upfront) {
+    gx_launch(logits_kernel<2, 2, 6, F32>, dim3((a.E + 7) / 8, (a.T + 1) / 2), dim3(kRouteThreads), 0, s, t, a.x, a.W,
+              a.b, a.T, a.E, a.H, a.logits);
+  } else if (a.T <= 8) {
+    gx_launch(logits_kernel<1, 1, 0, F32>, dim3((a.E + 3) / 4, a.T), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b,
+              a.T, a.E, a.H, a.logits);
+  } else {
+    gx_launch(logits_kernel<8, 4, 0, F32>, dim3((a.E + 15) / 16, (a.T + 7) / 8), dim3(kRouteThreads), 0, s, t, a.x,
+              a.W, a.b, a.T, a.E, a.H, a.logits);
+  }
 }
 
 }  // namespace
 
-static size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+size_t route_scratch_bytes(int, int, int) { return 256; }
 
-size_t route_scratch_bytes(int T, int E, int k) {
-  const size_t groups = (static_cast<size_t>(T > 0 ? T : 1) + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup;
-  return align256((groups + 1) * 4) + align256(static_cast<size_t>(T) * E * 4) + align256(static_cast<size_t>(T) * k * 4);
+// Instantiations per NV = ceil(E / 64) values per lane.
+template <bool F32>
+void launch_topk_plan_t(const RouteArgs& a, int variant, hipStream_t s, const KernelTimer& t) {
+  const int nv = (a.E + kWave - 1) / kWave;
+  const void* lg = a.logits;
+#define GX_TPK(NV_) gx_launch(topk_plan_kernel<F32, NV_>, dim3(1), dim3(kPlanThreads), 0, s, t, lg, a.T, a.E, a.k, \
+                              variant, a.idx, a.w, a.plan)
+  if (nv <= 1) GX_TPK(1);
+  else if (nv == 2) GX_TPK(2);
+  else if (nv == 3) GX_TPK(3);
+  else GX_TPK(4);
+#undef GX_TPK
 }
 
-void route_scratch_carve(void* scratch, int T, int E, int k, RouteArgs& a) {
-  const size_t groups = (static_cast<size_t>(T > 0 ? T : 1) + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup;
-  char* p = static_cast<char*>(scratch);
-  a.group_counter = reinterpret_cast<uint32_t*>(p);
-  a.done_counter = a.group_counter + groups;
-  p += align256((groups + 1) * 4);
-  a.xchg_logits = reinterpret_cast<float*>(p);
-  p += align256(static_cast<size_t>(T) * E * 4);
-  a.xchg_idx = reinterpret_cast<int32_t*>(p);
+template <bool F32>
+void launch_topk_t(const void* logits, int T, int E, int k, int variant, int32_t* idx, float* w, int32_t* tpe,
+                   hipStream_t s, const KernelTimer& t) {
+  const int nv = (E + kWave - 1) / kWave;
+  const dim3 grid((T + 3) / 4);
+#define GX_TK(NV_) gx_launch(topk_kernel<F32, NV_>, grid, dim3(kRouteThreads), 0, s, t, logits, T, E, k, variant, idx, \
+                             w, tpe)
+  if (nv <= 1) GX_TK(1);
+  else if (nv == 2) GX_TK(2);
+  else if (nv == 3) GX_TK(3);
+  else GX_TK(4);
+#undef GX_TK
 }
 
 hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
   if (a.T <= 0) return hipSuccess;
-  dim3 grid((a.E + kRouteExpertsPerGroup - 1) / kRouteExpertsPerGroup,
-            (a.T + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup);
-  // chunks of 8 inputs per thread: 2 covers H <= 4096 (GPT-OSS: 2880)
-  const int nj = ((a.H >> 3) + kRouteThreads - 1) / kRouteThreads;
-  if (a.logits_fp32) {
-    if (nj <= 1) gx_launch(route_kernel<true, 1>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
-    else if (nj == 2) gx_launch(route_kernel<true, 2>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
-    else gx_launch(route_kernel<true, 0>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
-  } else {
-    if (nj <= 1) gx_launch(route_kernel<false, 1>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
-    else if (nj == 2) gx_launch(route_kernel<false, 2>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
-    else gx_launch(route_kernel<false, 0>, grid, dim3(kRouteThreads), 0, s, a.timer, a);
+  const int variant = (a.T <= 8) ? 1 : 2;  // topk_softmax.cu:399
+  const bool plan = a.plan.counts != nullptr;
+  const bool fused = plan && a.T <= kTopkPlanMaxT;
+  const KernelTimer first{a.timer.start, nullptr}, last{nullptr, a.timer.stop};
+  if (a.logits_fp32) launch_logits<true>(a, s, first);
+  else launch_logits<false>(a, s, first);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  if (fused && a.T <= kLaneTopkMaxT && a.E <= kLaneTopkSlice * (kPlanThreads / kWave) && a.E % kLaneTopkSlice == 0) {
+    const void* lg = a.logits;
+#define GX_TPL(F_, K_) gx_launch(topk_plan_lanes_kernel<F_, K_>, dim3(1), dim3(kPlanThreads), 0, s, last, lg, a.T, \
+                                 a.E, variant, a.idx, a.w, a.plan)
+    if (a.logits_fp32) {
+      if (a.k == 1) GX_TPL(true, 1);
+      else if (a.k == 2) GX_TPL(true, 2);
+      else if (a.k == 4) GX_TPL(true, 4);
+      else GX_TPL(true, 8);
+    } else {
+      if (a.k == 1) GX_TPL(false, 1);
+      else if (a.k == 2) GX_TPL(false, 2);
+      else if (a.k == 4) GX_TPL(false, 4);
+      else GX_TPL(false, 8);
+    }
+#undef GX_TPL
+    return hipGetLastError();
   }
+  if (fused) {
+    if (a.logits_fp32) launch_topk_plan_t<true>(a, variant, s, last);
+    else launch_topk_plan_t<false>(a, variant, s, last);
+    return hipGetLastError();
+  }
+  const KernelTimer mid = plan ? KernelTimer{} : last;
+  if (a.logits_fp32) launch_topk_t<true>(a.logits, a.T, a.E, a.k, variant, a.idx, a.w, nullptr, s, mid);
+  else launch_topk_t<false>(a.logits, a.T, a.E, a.k, variant, a.idx, a.w, nullptr, s, mid);
+  err = hipGetLastError();
+  if (err != hipSuccess || !plan) return err;
+  gx_launch(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, last, static_cast<const int32_t*>(a.idx), a.T, a.k, a.E,
+            a.plan);
   return hipGetLastError();
 }
 
 hipError_t launch_topk(const void* logits, int logits_fp32, int T, int E, int k,
                        int32_t* idx, float* w, int32_t* tpe, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  dim3 grid((T + 3) / 4);
-  if (logits_fp32)
-    hipLaunchKernelGGL(topk_kernel<true>, grid, dim3(kRouteThreads), 0, s, logits, T, E, k, idx, w, tpe);
-  else
-    hipLaunchKernelGGL(topk_kernel<false>, grid, dim3(kRouteThreads), 0, s, logits, T, E, k, idx, w, tpe);
+  const int variant = (T <= 8) ? 1 : 2;
+  if (logits_fp32) launch_topk_t<true>(logits, T, E, k, variant, idx, w, tpe, s, KernelTimer{});
+  else launch_topk_t<false>(logits, T, E, k, variant, idx, w, tpe, s, KernelTimer{});
   return hipGetLastError();
 }
 
 hipError_t launch_plan(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s,
                        const KernelTimer& timer) {
   if (T <= 0) return hipSuccess;
-  gx_launch(plan_kernel, dim3(1), dim3(kRouteThreads), 0, s, timer, idx, T, k, E, plan);
+  gx_launch(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, timer, idx, T, k, E, plan);
   return hipGetLastError();
 }
 

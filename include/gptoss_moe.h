@@ -167,12 +167,13 @@ int gptoss_moe_layer_profile_read(gptoss_moe_layer* layer, float* route_ms, floa
 
 /* ---- Stage entry points (the reference's kernel launchers) --------------- */
 
-/* Router + top-k softmax in one launch: replaces gemv_bf16_forward (T == 1,
+/* Router + top-k softmax: replaces gemv_bf16_forward (T == 1,
  * gemv_bf16.cu:236-247) / gemm_bf16_lt (T > 1, cuda_utils.h:226-308) plus
  * topk_softmax_forward (topk_softmax.cu:380).  logits: [T][E] bf16 if
- * logits_fp32 == 0 else fp32.  Needs a device scratch of
- * gptoss_moe_route_scratch_bytes(T, E, k) bytes whose first 256-byte-aligned
- * counter block is zero-filled; the call leaves it zero-filled again. */
+ * logits_fp32 == 0 else fp32 (the router output, rounded as the reference's
+ * bf16 logits or kept in fp32).  `scratch` (gptoss_moe_route_scratch_bytes
+ * bytes of device memory) is reserved and not read or written by this
+ * version. */
 size_t gptoss_moe_route_scratch_bytes(int num_tokens, int num_experts, int top_k);
 int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
                      int num_tokens, int num_experts, int hidden, int top_k, int logits_fp32,
