@@ -12,23 +12,37 @@
 //                                gated: bf16 gate/up, clamped SwiGLU, bf16
 //                                activations (the gate_up never reaches HBM)
 //
-// Work decomposition: a work-group computes a tile of kBM permuted rows (one
-// expert's tokens) x 256 weight rows; its four waves own one 64-row tile of
-// the tiled MXFP4 layout each (the layout the decode kernels stream, so one
-// copy of the weights serves both paths).  The (m-tile, n-tile) pairs are
-// counted expert by expert from the plan's offsets on the device, so no host
-// synchronisation is needed; consecutive tiles share their token rows and
-// land on the same XCD (one L2).
+// Work decomposition: a work-group (four waves, two work-groups per CU)
+// computes a tile of kBM = 128 permuted rows (one expert's tokens) x 256
+// weight rows; each wave owns one 64-row tile of the tiled MXFP4 layout (the
+// layout the decode kernels stream, so one copy of the weights serves both
+// paths).  The m-tiles are counted expert by expert from the plan's offsets
+// on the device (no host synchronisation); the tile sequence runs kGroupM
+// m-tiles x all n-tiles at a time (a weight tile is read by the group's
+// m-tiles close together, from L2) and is cut into eight equal contiguous
+// ranges, one per XCD, so every XCD gets the same number of real tiles.
 //
-// Matrix-core mapping (v_mfma_f32_32x32x16_bf16, fp32 accumulation): the A
-// operand is 32 weight rows, decoded from MXFP4 in registers with the gfx950
-// scaled fp4 -> bf16 conversion (exact: e2m1 x 2^(s-127) has at most two
-// significant bits); the B operand is 32 tokens read from an LDS tile.  The
-// accumulator layout gives each lane four consecutive weight rows of one
-// token, so the interleaved gate/up pairs meet in one lane.  The K order
-// inside an MFMA is a permutation shared by both operands: lane half h takes
-// elements 16h..16h+15 of each 32-element block (dwords 2h, 2h+1 of the
-// tiled row block), elements 16h+8s..16h+8s+7 in k16 step s.
+// Data movement: every operand of a 32-element K block (the tile's tokens,
+// each wave's 64 nibble slots and scale dwords) reaches an LDS ring stage
+// through direct global -> LDS loads, so no register waits on memory and
+// every wait is an explicit vmcnt count of whole blocks.  The work-group
+// synchronises every second block; each wave runs a software pipeline in
+// which block kb's products issue while block kb + 1's LDS reads land and
+// its A operands decode, and the refill loads are issued behind the products.
+//
+// Matrix-core mapping (v_mfma_f32_16x16x32_bf16, fp32 accumulation): the A
+// operand of sub-tile i (rows 16i..16i+15 of the wave's tile) is dword i of
+// the lane's 16-byte slot of the tiled block, decoded from MXFP4 in
+// registers with the gfx950 scaled fp4 -> bf16 conversion (exact: e2m1 x
+// 2^(s-127) has at most two significant bits); lane l holds row l % 16,
+// elements 8(l/16)..8(l/16)+7 of the 32-element block, exactly the
+// operand's K order, so one 32-element block is one K step.  The B operand
+// is 16 tokens of the LDS stage.  The accumulator gives each lane four
+// consecutive weight rows of one token, so the interleaved gate/up pairs
+// meet in one lane.  Partial m-tiles (an expert's last rows) load and
+// multiply only the 16-token fragments that hold rows.  Scale codes 0 and
+// 255 (decoded as the reference's register path does) send the wave through
+// an exact unpipelined pass after the main loop.
 //
 // Numerics: products are exact, sums are fp32 in the matrix core's order, so
 // results are not bit-identical to the canonical order of the decode path;
@@ -43,15 +57,27 @@ namespace gxmoe {
 namespace {
 
 typedef gx_bf16x8 bf16x8_t;
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef gx_u32x4 u32x4_t;
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int kGW = 4;                    // waves per work-group (a 64-row weight tile each)
-constexpr int kBM = 64;                   // permuted rows per work-group tile (2 x 32 tokens)
-constexpr int kGD = 4;                    // blocks in flight ahead of the one computed
-constexpr int kStageBytes = kBM * 64;     // one 32-element bf16 block of kBM rows
+constexpr int kGW = 4;                  // waves per work-group (a 64-row weight tile each), two per CU
+constexpr int kBM = 128;                // permuted rows per work-group tile
+constexpr int kFrags = kBM / 16;        // 16-token B fragments
+constexpr int kXBytes = kBM * 64;       // tokens: one 32-element bf16 block of kBM rows
+constexpr int kXPerWave = kXBytes / 1024 / kGW;  // token KiBs each wave fills per block
+constexpr int kWOff = kXBytes;          // nibbles: wave w's 64 slots x 16 bytes at kWOff + 1024 w
+constexpr int kSOff = kWOff + kGW * 1024;  // scales: wave w's 16 dwords (+ 48 unread) at kSOff + 256 w
+constexpr int kStageBytes = kSOff + kGW * 256;
+constexpr int kStages = (80 * 1024) / kStageBytes;  // LDS stages (blocks in flight), a ring; two work-groups per CU
+constexpr int kLoadsPerStep = kXPerWave + 2;  // direct LDS loads per wave and block: token KiBs, nibbles, scales
+#ifndef GX_PREFILL_GROUP_M
+#define GX_PREFILL_GROUP_M 4
+#endif
+constexpr int kGroupM = GX_PREFILL_GROUP_M;  // m-tiles per tile group
 constexpr int kExpertsPerLane = kMaxExperts / kWave;
+static_assert(kXPerWave * kGW * 1024 == kXBytes, "token KiBs split evenly over the waves");
+static_assert(kStages >= 5 && kLoadsPerStep * (kStages - 2) < 64, "vmcnt range");
 
 struct GroupedParams {
   const uint16_t* x;         // [*][K] bf16 rows
@@ -66,14 +92,24 @@ struct GroupedParams {
   uint16_t* gate_up;         // gated and optional: [rows][N] bf16 gate/up values
   float alpha, limit;
   int nwt;                   // work-group n-tiles: ceil(N / (64 kGW))
-  int total;                 // virtual tiles (bound on m-tiles x nwt)
 };
 
-// Expert, first row (within the expert), offset and row count of m-tile
-// `mt`, counting ceil(M_e / kBM) m-tiles per expert in expert order; e = -1
-// past the last.  Every lane returns the same values.
-__device__ __forceinline__ void find_mtile(const int32_t* __restrict__ offsets, int E, int mt, int lane, int& e,
-                                           int& m0, int& off, int& cnt) {
+struct TileCoord {
+  int e;    // expert
+  int m0;   // first row within the expert
+  int off;  // the expert's first permuted position
+  int cnt;  // the expert's rows
+  int nt;   // n-tile
+};
+
+// Work-group vb's tile, or false if it has none.  The m-tiles (ceil(M_e /
+// kBM) per expert, in expert order) and n-tiles form total = m-tiles x nwt
+// tiles, ordered group by group (kGroupM m-tiles x nwt n-tiles, m fastest)
+// and cut into 8 contiguous ranges of ceil(total / 8): work-group vb runs
+// on XCD vb % 8 and takes tile (vb % 8) * range + vb / 8.  Every lane
+// returns the same values.
+__device__ __forceinline__ bool map_tile(const int32_t* __restrict__ offsets, int E, int nwt, int vb, int lane,
+                                         TileCoord& tc) {
   int c[kExpertsPerLane], o[kExpertsPerLane + 1];
   const int e0 = lane * kExpertsPerLane;
 #pragma unroll
@@ -91,224 +127,297 @@ __device__ __forceinline__ void find_mtile(const int32_t* __restrict__ offsets, 
     if (lane >= d) incl += t;
   }
   const int excl = incl - local;
+  const int mtiles = __builtin_amdgcn_readlane(incl, kWave - 1);
+  const int total = mtiles * nwt;
+  const int range = (total + 7) >> 3;
+  const int i = vb >> 3;
+  if (i >= range) return false;
+  const int v = (vb & 7) * range + i;
+  if (v >= total) return false;
+  const int gsz = kGroupM * nwt;
+  const int grp = v / gsz;
+  const int r = v - grp * gsz;
+  const int gm = min(kGroupM, mtiles - grp * kGroupM);  // m-tiles in this group
+  const int mt = grp * kGroupM + r % gm;
+  tc.nt = r / gm;
   const bool mine = mt >= excl && mt < incl;
   const unsigned long long bal = __ballot(mine);
-  if (bal == 0ull) {
-    e = -1;
-    return;
-  }
-  const int src = __ffsll(static_cast<long long>(bal)) - 1;
-  int ee = -1, base = excl;
+  const int src = __ffsll(static_cast<long long>(bal)) - 1;  // bal != 0: mt < mtiles
+  int ee = -1, base = excl, run = excl;
 #pragma unroll
-  for (int i = 0; i < kExpertsPerLane; ++i) {
-    if (ee < 0) {
-      if (mt < base + c[i]) ee = e0 + i;
-      else base += c[i];
+  for (int k = 0; k < kExpertsPerLane; ++k) {
+    if (ee < 0 && mt < run + c[k]) {
+      ee = e0 + k;
+      base = run;
     }
+    run += c[k];
   }
-  e = __shfl(ee, src, kWave);
-  m0 = (mt - __shfl(base, src, kWave)) * kBM;
-  off = offsets[e];
-  cnt = offsets[e + 1] - off;
+  // wave-uniform values in scalar registers (buffer descriptors, branches)
+  tc.e = __builtin_amdgcn_readfirstlane(__shfl(ee, src, kWave));
+  tc.m0 = __builtin_amdgcn_readfirstlane((mt - __shfl(base, src, kWave)) * kBM);
+  tc.nt = __builtin_amdgcn_readfirstlane(tc.nt);
+  tc.off = __builtin_amdgcn_readfirstlane(offsets[tc.e]);
+  tc.cnt = __builtin_amdgcn_readfirstlane(offsets[tc.e + 1]) - tc.off;
+  return true;
 }
 
-template <bool kGated>
-__global__ __launch_bounds__(kGW * kWave) void grouped_mfma_kernel(GroupedParams a) {
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kStageBytes];
-  const int G = gridDim.x;  // a multiple of 8: block b runs on XCD b % 8
-  const int vb = static_cast<int>(blockIdx.x);
-  const int v = (vb & 7) * (G >> 3) + (vb >> 3);
-  if (v >= a.total) return;
-  const int nt = v % a.nwt, mt = v / a.nwt;
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  int e, m0, off, cnt;
-  find_mtile(a.offsets, a.E, mt, lane, e, m0, off, cnt);
-  if (e < 0) return;  // the whole work-group: no barrier has been passed
-  const int mc = min(kBM, cnt - m0);
+// s_waitcnt vmcnt(N), other counters untouched.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// s_waitcnt vmcnt(NB * per) for a wave issuing `per` loads per block
+// (wave-uniform, kLoadsPerStep - kXPerWave .. kLoadsPerStep).
+template <int NB>
+__device__ __forceinline__ void wait_blocks(int per) {
+  static_assert(kXPerWave == 2, "three load counts per block");
+  if (per == kLoadsPerStep) wait_vm<NB * kLoadsPerStep>();
+  else if (per == kLoadsPerStep - 1) wait_vm<NB * (kLoadsPerStep - 1)>();
+  else wait_vm<NB * (kLoadsPerStep - 2)>();
+}
+
+template <bool kGated, bool kFull>
+__device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileCoord& tc, uint8_t* xs, int lane,
+                                             int w) {
   const TiledGeom& g = a.g;
   const int K = g.K, N = g.N, nb = g.nb;
-  const int tile = nt * kGW + w;
+  const int mc = min(kBM, tc.cnt - tc.m0);
+  const int nfr = kFull ? kFrags : (mc + 15) >> 4;  // 16-token fragments holding rows
+  const int tile = tc.nt * kGW + w;
   const bool active = tile < N / kTileRows;  // wave-uniform: rows past N (last n-tile) only stage tokens
 
-  // Token staging: lane -> row pm = 16w + lane/4 of the tile, LDS quarter
-  // lane%4 holding global quarter (lane%4) ^ swz(pm), swz(m) = (m/2)%4, so
-  // that 8 consecutive rows read at one quarter hit distinct banks.
-  const int pm = 16 * w + (lane >> 2);
-  const int pq = (lane & 3) ^ ((pm >> 1) & 3);
-  const int pmr = pm < mc ? pm : 0;  // rows past the expert's end stage a valid row (their outputs are not stored)
-  const int prow = a.row_index ? a.row_index[off + m0 + pmr] : off + m0 + pmr;
-  const uint16_t* xsrc = a.x + static_cast<size_t>(prow) * K + pq * 8;
-  uint8_t* xdst0 = &xs[0][0] + 1024 * w + 16 * lane;
+  // Everything a block needs reaches LDS by direct loads (no registers wait
+  // on memory): per stage, the tokens (wave w fills KiBs kXPerWave w + c;
+  // lane l writes bytes 16l..16l+15 of a KiB), wave w's nibble slots and its
+  // scale dwords.  Token LDS unit u = 4j + (q ^ swz(j)) holds quarter q of
+  // token j, swz(j) = (j/2) % 4, so the 16 tokens of a B fragment read at
+  // one quarter hit distinct banks 8 at a time.
+  const uint16_t* xsrc[kXPerWave];
+#pragma unroll
+  for (int c = 0; c < kXPerWave; ++c) {
+    const int j = 16 * (kXPerWave * w + c) + (lane >> 2);
+    const int q = (lane & 3) ^ ((j >> 1) & 3);
+    const int jr = j < mc ? j : 0;  // rows past the expert's end stage a valid row (their outputs are not stored)
+    const int prow = a.row_index ? a.row_index[tc.off + tc.m0 + jr] : tc.off + tc.m0 + jr;
+    xsrc[c] = a.x + static_cast<size_t>(prow) * K + q * 8;
+  }
+  // Token KiBs of this wave holding rows (the others are not loaded).
+  const int nxw = kFull ? kXPerWave : max(0, min(kXPerWave, nfr - kXPerWave * w));
+  // B fragment t: token 16t + l % 16, quarter l / 16.
+  const int bj = lane & 15;
+  const int boff = bj * 64 + 16 * ((lane >> 4) ^ ((bj >> 1) & 3));
 
-  // Weights: frag f = rows 32f + lane%32 of the wave's tile, dwords 2h and
-  // 2h + 1 (h = lane/32) of each 16-byte row block: tiled_dword(row, 2h) and
-  // the dword 64 after it; row 32 + r sits 2 dwords after row r.  Scales:
-  // one byte per (row, block).
-  const int tl = active ? tile : 0;
-  const uint32_t* wsrc = reinterpret_cast<const uint32_t*>(a.wn + static_cast<size_t>(e) * g.nib_bytes +
-                                                           static_cast<size_t>(tl) * nb * 1024) +
-                         tiled_dword(lane & 31, 2 * (lane >> 5));
-  const uint8_t* ssrc = a.ws + static_cast<size_t>(e) * g.scale_bytes +
-                        (static_cast<size_t>(tl) * g.parts * kTileRows + (lane & 31)) * g.spad;
-  const size_t spart = static_cast<size_t>(kTileRows) * g.spad;  // scale bytes per part
-  const size_t sfrag = static_cast<size_t>(32) * g.spad;
+  // Nibbles: the lane's 16-byte slot of each block of the wave's tile;
+  // scales: dword l % 16 of the (tile, block) scale group (rows 16i + l % 16,
+  // byte i).  Inactive waves read past the buffer end (zeros, no memory
+  // access) so every wave issues the same loads.
+  const size_t eoff_n = static_cast<size_t>(tc.e) * g.nib_bytes;
+  const size_t eoff_s = static_cast<size_t>(tc.e) * g.scale_bytes + g.mscale_off;
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.wn + eoff_n), 0, static_cast<int>(g.nib_bytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.ws + eoff_s), 0, static_cast<int>(static_cast<size_t>(N) * nb), 0x00020000);
+  const int wvoff = active ? tile * nb * 1024 + 16 * lane : static_cast<int>(g.nib_bytes);
+  const int svoff = active ? tile * nb * 64 + 4 * (lane & 15) : N * nb;
 
-  u32x4_t xr[kGD];
-  u32x2_t wr[kGD][2];
-  uint32_t sr[kGD][2];
-  int ssh[kGD];  // bit offset of the scale byte in sr
-  // Prefetch cursor (block index of the next loads, clamped to the last block).
-  int lb = 0, lp = 0, lq = 0;
-  auto issue = [&](u32x4_t& xv, u32x2_t (&wv)[2], uint32_t (&sv)[2], int& sh) __attribute__((always_inline)) {
-    const int bb = lb < nb ? lb : nb - 1;
-    const int bp = lb < nb ? lp : (nb - 1) / g.bpp;
-    const int bq = lb < nb ? lq : (nb - 1) % g.bpp;
-    xv = *reinterpret_cast<const u32x4_t*>(xsrc + static_cast<size_t>(bb) * 32);
-    // Every wave issues the same loads (an inactive one reads tile 0), so the
-    // wait counts are the same on every path.
-    const uint32_t* wp = wsrc + static_cast<size_t>(bb) * 256;
-    wv[0] = u32x2_t{wp[0], wp[64]};  // cached: every m-tile of the expert reads them
-    wv[1] = u32x2_t{wp[2], wp[66]};
-    // The aligned dword holding the scale byte (extracted at its use: a
-    // loop-carried byte load is re-masked where the loop wraps, which waits
-    // for the loads in flight).
-    const uint8_t* sp = ssrc + bp * spart + (bq & ~3);
-    sv[0] = *reinterpret_cast<const uint32_t*>(sp);
-    sv[1] = *reinterpret_cast<const uint32_t*>(sp + sfrag);
-    sh = 8 * (bq & 3);
-    ++lb;
-    if (++lq == g.bpp) {
-      lq = 0;
-      ++lp;
-    }
+  // Block kb's loads into stage st (clamped to the last block past the end:
+  // the stage is not read again).
+  auto issue = [&](int kb, int st) __attribute__((always_inline)) {
+    const int bb = kb < nb ? kb : nb - 1;
+    uint8_t* sp = xs + st * kStageBytes;
+#pragma unroll
+    for (int c = 0; c < kXPerWave; ++c)
+      if (c < nxw)
+        __builtin_amdgcn_global_load_lds(xsrc[c] + static_cast<size_t>(bb) * 32,
+                                         (lds_void_t*)(sp + 1024 * (kXPerWave * w + c)), 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void_t*)(sp + kWOff + 1024 * w), 16, wvoff, bb * 1024, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_void_t*)(sp + kSOff + 256 * w), 4, svoff, bb * 64, 0, 0);
   };
+  // Software pipeline over blocks: step kb runs block kb's products from
+  // registers while the LDS reads of block kb + 1 land and its A operands
+  // are decoded.  The work-group synchronises every second step: at even kb
+  // it waits for blocks kb + 1, kb + 2 and refills the stages of kb - 1 and
+  // kb with blocks kb + kStages - 1, kb + kStages.  The ring then holds
+  // blocks kb - 1 .. kb + kStages - 2 before the refill.
+#pragma unroll
+  for (int b = 0; b < kStages - 1; ++b) issue(b, b);
 
-  issue(xr[0], wr[0], sr[0], ssh[0]);
-  issue(xr[1], wr[1], sr[1], ssh[1]);
-  issue(xr[2], wr[2], sr[2], ssh[2]);
-  issue(xr[3], wr[3], sr[3], ssh[3]);
-  *reinterpret_cast<u32x4_t*>(xdst0) = xr[0];
-  __syncthreads();
+  f32x4_t acc[4][kFrags];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < kFrags; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  f32x16_t acc[2][2];
+  // Operands of one block: raw nibbles and scales, decoded A, B fragments.
+  auto read_stage = [&](int st, u32x4_t& wv, uint32_t& sv, bf16x8_t (&bv)[kFrags]) __attribute__((always_inline)) {
+    const uint8_t* sp = xs + st * kStageBytes;
+    wv = *reinterpret_cast<const u32x4_t*>(sp + kWOff + 1024 * w + 16 * lane);
+    sv = *reinterpret_cast<const uint32_t*>(sp + kSOff + 256 * w + 4 * (lane & 15));
 #pragma unroll
-  for (int f = 0; f < 2; ++f)
+    for (int t = 0; t < kFrags; ++t)
+      if (kFull || t < nfr) bv[t] = *reinterpret_cast<const bf16x8_t*>(sp + boff + 1024 * t);
+  };
+  // Decoded as codes 1..254 (exact); a block holding code 0 or 255 marks
+  // the wave, which then recomputes its tile on the exact path below.
+  bool spec = false;
+  auto decode = [&](const u32x4_t& wv, uint32_t sv, bf16x8_t (&av)[4]) __attribute__((always_inline)) {
+    spec |= has_special_code(sv, 0xffffffffu);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[f][t][r] = 0.0f;
+    for (int i = 0; i < 4; ++i) av[i] = decode8_bf16(wv[i], __uint_as_float(((sv >> (8 * i)) & 0xffu) << 23));
+  };
+  bf16x8_t av[2][4], bv[2][kFrags];
 
-  // B operand: token j = 32t + lane%32, quarter 2h + s of the 32-element block.
-  const int h = lane >> 5;
-  int boff[2][2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int j = 32 * t + (lane & 31);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) boff[t][s] = j * 64 + 16 * ((2 * h + s) ^ ((j >> 1) & 3));
+  // Block 0: its loads were followed by those of blocks 1 .. kStages - 2.
+  const int per = nxw + 2;  // this wave's loads per block
+  wait_blocks<kStages - 2>(per);
+  __builtin_amdgcn_s_barrier();
+  if (active) {
+    u32x4_t wv;
+    uint32_t sv;
+    read_stage(0, wv, sv, bv[0]);
+    decode(wv, sv, av[0]);
   }
 
-  // One block of the main loop; the ring slot u is a compile-time constant
-  // so the ring stays in registers.
-  auto step = [&](auto U, int kb) __attribute__((always_inline)) {
-    constexpr int u = decltype(U)::value;
-    const uint8_t* stage = &xs[kb & 1][0];
-    bf16x8_t av[2][2];
-    if (active) {
-      const uint32_t c0 = __builtin_amdgcn_ubfe(sr[u][0], ssh[u], 8), c1 = __builtin_amdgcn_ubfe(sr[u][1], ssh[u], 8);
-      const bool special = ((c0 - 1u) >= 254u) || ((c1 - 1u) >= 254u);
-      if (__builtin_expect(__ballot(special) != 0ull, 0)) {
-        av[0][0] = decode8_bf16_special(wr[u][0].x, c0);
-        av[0][1] = decode8_bf16_special(wr[u][0].y, c0);
-        av[1][0] = decode8_bf16_special(wr[u][1].x, c1);
-        av[1][1] = decode8_bf16_special(wr[u][1].y, c1);
-      } else {
-        // c0, c1 are zero-extended bytes: code << 23 is the e8m0 scale
-        const float s0 = __uint_as_float(c0 << 23), s1 = __uint_as_float(c1 << 23);
-        av[0][0] = decode8_bf16(wr[u][0].x, s0);
-        av[0][1] = decode8_bf16(wr[u][0].y, s0);
-        av[1][0] = decode8_bf16(wr[u][1].x, s1);
-        av[1][1] = decode8_bf16(wr[u][1].y, s1);
-      }
+  int st = 0;  // stage of block kb
+  auto step = [&](auto P, int kb) __attribute__((always_inline)) {
+    constexpr int p = decltype(P)::value;  // register set of block kb = kb % 2
+    const int st1 = st == kStages - 1 ? 0 : st + 1;
+    if constexpr (p == 0) {
+      // Blocks kb + 1, kb + 2 were followed by kb + 3 .. kb + kStages - 2.
+      // This wave's reads of stages kb - 1 and kb are complete, so after the
+      // barrier no wave reads them any more and kb + 1, kb + 2 are visible.
+      wait_blocks<kStages - 4>(per);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
     }
-    // The ring slot is free: fetch block kb + kGD into it.
-    issue(xr[u], wr[u], sr[u], ssh[u]);
+    __builtin_amdgcn_sched_barrier(0);
     if (active) {
+      // Block kb + 1's reads go out in two halves, each ahead of the
+      // products of the half of block kb whose fragments it replaces.
+      const uint8_t* sp = xs + st1 * kStageBytes;
+      const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(sp + kWOff + 1024 * w + 16 * lane);
+      const uint32_t sv = *reinterpret_cast<const uint32_t*>(sp + kSOff + 256 * w + 4 * (lane & 15));
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        bf16x8_t bv[2];
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) bv[t] = *reinterpret_cast<const bf16x8_t*>(stage + boff[t][s]);
+        for (int t = h * kFrags / 2; t < (h + 1) * kFrags / 2; ++t)
+          if (kFull || t < nfr) bv[p ^ 1][t] = *reinterpret_cast<const bf16x8_t*>(sp + boff + 1024 * t);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int f = 0; f < 2; ++f)
+        for (int t = h * kFrags / 2; t < (h + 1) * kFrags / 2; ++t)
+          if (kFull || t < nfr) {
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
-            acc[f][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[f][s], bv[t], acc[f][t], 0, 0, 0);
+            for (int i = 0; i < 4; ++i)
+              acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[p][i], bv[p][t], acc[i][t], 0, 0, 0);
+          }
+        __builtin_amdgcn_sched_barrier(0);
       }
+      decode(wv, sv, av[p ^ 1]);
     }
-    // Stage block kb + 1 (fetched kGD - 1 steps ago) into the other buffer.
-    *reinterpret_cast<u32x4_t*>(&xs[(kb + 1) & 1][0] + 1024 * w + 16 * lane) = xr[(u + 1) % kGD];
-    __syncthreads();
+    // The refill, issued behind the products so a stalled address queue
+    // overlaps the matrix cores.
+    if constexpr (p == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue(kb + kStages - 1, st == 0 ? kStages - 1 : st - 1);
+      issue(kb + kStages, st);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    st = st1;
   };
-  static_assert(kGD == 4, "the main loop is unrolled by hand for a ring of 4");
   int kb0 = 0;
-  for (; kb0 + kGD <= nb; kb0 += kGD) {
+  for (; kb0 + 2 <= nb; kb0 += 2) {
     step(std::integral_constant<int, 0>{}, kb0);
     step(std::integral_constant<int, 1>{}, kb0 + 1);
-    step(std::integral_constant<int, 2>{}, kb0 + 2);
-    step(std::integral_constant<int, 3>{}, kb0 + 3);
   }
-  if (kb0 < nb) {
-    step(std::integral_constant<int, 0>{}, kb0);
-    if (kb0 + 1 < nb) {
-      step(std::integral_constant<int, 1>{}, kb0 + 1);
-      if (kb0 + 2 < nb) step(std::integral_constant<int, 2>{}, kb0 + 2);
-    }
-  }
+  if (kb0 < nb) step(std::integral_constant<int, 0>{}, kb0);
+  wait_vm<0>();  // the clamped loads past the last block land before the work-group ends
   if (!active) return;
 
-  // Epilogue.  acc[f][t][4q + r] is row 32f + 8q + 4h + r of the tile for
-  // token 32t + lane%32.
-  const int nrow0 = tile * kTileRows + 4 * h;
-  const uint16_t* brow = a.bias ? a.bias + static_cast<size_t>(e) * N : nullptr;
+  // Scale codes 0 and 255 (none in a regular checkpoint): redo the wave's
+  // tile block by block with the reference's decode of those codes, tokens
+  // read from global memory (no LDS, no barriers: the other waves are not
+  // involved).
+  if (__builtin_expect(__ballot(spec) != 0ull, 0)) {
+    const uint16_t* trow[kFrags];
 #pragma unroll
-  for (int f = 0; f < 2; ++f) {
+    for (int t = 0; t < kFrags; ++t) {
+      const int j = min(16 * t + bj, mc - 1);
+      const int prow = a.row_index ? a.row_index[tc.off + tc.m0 + j] : tc.off + tc.m0 + j;
+      trow[t] = a.x + static_cast<size_t>(prow) * K + 8 * (lane >> 4);
+    }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = nrow0 + 32 * f + 8 * q;  // four consecutive rows n..n+3
-      float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (brow) {
-        const uint2 bb = *reinterpret_cast<const uint2*>(brow + n);
-        bias[0] = bf16_to_f32(static_cast<uint16_t>(bb.x));
-        bias[1] = bf16_to_f32(static_cast<uint16_t>(bb.x >> 16));
-        bias[2] = bf16_to_f32(static_cast<uint16_t>(bb.y));
-        bias[3] = bf16_to_f32(static_cast<uint16_t>(bb.y >> 16));
-      }
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int j = 32 * t + (lane & 31);
-        if (j < mc) {
-          const size_t p = static_cast<size_t>(off + m0 + j);
-          uint16_t y[4];
+      for (int t = 0; t < kFrags; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb = 0; kb < nb; ++kb) {
+      const u32x4_t wv = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff, kb * 1024, 0));
+      const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b32(srs, svoff, kb * 64, 0);
+      bf16x8_t av1[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) y[r] = f32_to_bf16(acc[f][t][4 * q + r] + bias[r]);
-          if constexpr (kGated) {
-            // rows n, n+2 are gate (even), n+1, n+3 up (odd)
-            const uint16_t a0 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[0]), bf16_to_f32(y[1]), a.alpha, a.limit));
-            const uint16_t a1 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[2]), bf16_to_f32(y[3]), a.alpha, a.limit));
-            *reinterpret_cast<uint32_t*>(a.out + p * (N / 2) + n / 2) = a0 | (static_cast<uint32_t>(a1) << 16);
-            if (a.gate_up)
-              *reinterpret_cast<uint2*>(a.gate_up + p * N + n) =
-                  make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
-          } else {
-            *reinterpret_cast<uint2*>(a.out + p * N + n) =
+      for (int i = 0; i < 4; ++i) av1[i] = decode8_bf16_special(wv[i], (sv >> (8 * i)) & 0xffu);
+#pragma unroll
+      for (int t = 0; t < kFrags; ++t)
+        if (kFull || t < nfr) {
+          const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(trow[t] + kb * 32);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av1[i], b1, acc[i][t], 0, 0, 0);
+        }
+    }
+  }
+
+  // Epilogue.  acc[i][t][r] is row 16i + 4(l/16) + r of the tile for token
+  // 16t + l % 16.
+  const int nrow0 = tile * kTileRows + 4 * (lane >> 4);
+  const uint16_t* brow = a.bias ? a.bias + static_cast<size_t>(tc.e) * N : nullptr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = nrow0 + 16 * i;  // four consecutive rows n..n+3
+    float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (brow) {
+      const uint2 bb = *reinterpret_cast<const uint2*>(brow + n);
+      bias[0] = bf16_to_f32(static_cast<uint16_t>(bb.x));
+      bias[1] = bf16_to_f32(static_cast<uint16_t>(bb.x >> 16));
+      bias[2] = bf16_to_f32(static_cast<uint16_t>(bb.y));
+      bias[3] = bf16_to_f32(static_cast<uint16_t>(bb.y >> 16));
+    }
+#pragma unroll
+    for (int t = 0; t < kFrags; ++t) {
+      const int j = 16 * t + bj;
+      if (j < mc) {
+        const size_t p = static_cast<size_t>(tc.off + tc.m0 + j);
+        uint16_t y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = f32_to_bf16(acc[i][t][r] + bias[r]);
+        if constexpr (kGated) {
+          // rows n, n+2 are gate (even), n+1, n+3 up (odd)
+          const uint16_t a0 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[0]), bf16_to_f32(y[1]), a.alpha, a.limit));
+          const uint16_t a1 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[2]), bf16_to_f32(y[3]), a.alpha, a.limit));
+          *reinterpret_cast<uint32_t*>(a.out + p * (N / 2) + n / 2) = a0 | (static_cast<uint32_t>(a1) << 16);
+          if (a.gate_up)
+            *reinterpret_cast<uint2*>(a.gate_up + p * N + n) =
                 make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
-          }
+        } else {
+          *reinterpret_cast<uint2*>(a.out + p * N + n) =
+              make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
         }
       }
     }
   }
+}
+
+template <bool kGated>
+__global__ __launch_bounds__(kGW * kWave, 2) void grouped_mfma_kernel(GroupedParams a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[kStages * kStageBytes];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  TileCoord tc;
+  if (!map_tile(a.offsets, a.E, a.nwt, static_cast<int>(blockIdx.x), lane, tc)) return;  // the whole work-group
+  if (tc.cnt - tc.m0 >= kBM)
+    grouped_tile<kGated, true>(a, tc, xs, lane, w);
+  else
+    grouped_tile<kGated, false>(a, tc, xs, lane, w);
 }
 
 }  // namespace
@@ -334,12 +443,14 @@ hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s) {
   p.alpha = a.alpha;
   p.limit = a.limit;
   p.nwt = (a.N / kTileRows + kGW - 1) / kGW;
-  // sum_e ceil(M_e / kBM) <= rows / kBM + (experts with rows)
+  // sum_e ceil(M_e / kBM) <= rows / kBM + (experts with rows); the kernel
+  // counts the real tiles and spreads them evenly over the XCDs
   const long mt_bound = (a.rows + kBM - 1) / kBM + (a.E < a.rows ? a.E : a.rows);
   const long total = mt_bound * p.nwt;
-  if (total > (1L << 30)) return hipErrorInvalidValue;
-  p.total = static_cast<int>(total);
-  const int grid = (p.total + 7) & ~7;
+  if (total > (1L << 30) || static_cast<size_t>(a.N) * (a.K / 32) > (1u << 30) ||
+      p.g.nib_bytes >= (static_cast<size_t>(1) << 31))
+    return hipErrorInvalidValue;  // tile and buffer offsets are 32-bit
+  const int grid = static_cast<int>((total + 7) & ~7L);
   if (a.gated)
     gx_launch(grouped_mfma_kernel<true>, dim3(grid), dim3(kGW * kWave), 0, s, a.timer, p);
   else
