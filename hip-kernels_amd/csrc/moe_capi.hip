@@ -115,6 +115,7 @@ struct gptoss_moe_layer {
   void* route_scratch = nullptr;
   int32_t* special1 = nullptr;  // [E] W1 / W2 scales hold e8m0 code 0 or 255
   int32_t* special2 = nullptr;
+  int32_t* gqueue = nullptr;    // tile queue of the persistent grouped kernel (zeroed; left zeroed)
   int special_any1 = 0, special_any2 = 0;
   int num_cus = 0;
   int mc_shape[3] = {0, 0, 0};  // matrix-core decode launch shape override
@@ -298,11 +299,13 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   ALLOC(route_scratch, void*, route_bytes)
   ALLOC(special1, int32_t*, E * 4)
   ALLOC(special2, int32_t*, E * 4)
+  ALLOC(gqueue, int32_t*, grouped_queue_ints() * 4)
   if (L->norm_w != nullptr) {
     ALLOC(normed, uint16_t*, T * H * 2)
   }
 #undef ALLOC
   hipError_t err = hipMemset(L->route_scratch, 0, route_bytes);
+  if (err == hipSuccess) err = hipMemset(L->gqueue, 0, grouped_queue_ints() * 4);
   if (err == hipSuccess) err = launch_special_scan(L->w1s, 2 * I, H, E, L->special1, nullptr);
   if (err == hipSuccess) err = launch_special_scan(L->w2s, H, I, E, L->special2, nullptr);
   if (err == hipSuccess) err = hipDeviceGetAttribute(&L->num_cus, hipDeviceAttributeMultiprocessorCount, device_id);
@@ -399,6 +402,8 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
     g.gated = 1;
     g.alpha = c.swiglu_alpha;
     g.limit = c.swiglu_limit;
+    g.queue = L->gqueue;
+    g.num_cus = L->num_cus;
     g.timer = pf.timer(1);
     HIP_TRY(launch_grouped_mxfp4(g, s), "grouped gate_up launch");
     g.x = L->act;

@@ -179,8 +179,12 @@ struct GroupedArgs {
   uint16_t* gate_up;
   int gated;
   float alpha, limit;
+  int32_t* queue;  // null, or grouped_queue_ints() zeroed ints (persistent grid; left zeroed)
+  int num_cus;     // with a queue: compute units of the device
   KernelTimer timer;
 };
+// Ints of the persistent grouped kernel's tile queue.
+constexpr int grouped_queue_ints() { return 9 * 32; }
 bool grouped_supported(int N, int K, int E);
 hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s);
 

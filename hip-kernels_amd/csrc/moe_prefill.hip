@@ -61,23 +61,34 @@ typedef gx_u32x4 u32x4_t;
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int kGW = 4;                  // waves per work-group (a 64-row weight tile each), two per CU
+#ifndef GX_PREFILL_WAVES
+#define GX_PREFILL_WAVES 4
+#endif
+constexpr int kGW = GX_PREFILL_WAVES;   // waves per work-group (a 64-row weight tile each)
+constexpr int kWGPerCU = 8 / kGW;       // work-groups per CU (two waves per SIMD)
 constexpr int kBM = 128;                // permuted rows per work-group tile
-constexpr int kFrags = kBM / 16;        // 16-token B fragments
-constexpr int kXBytes = kBM * 64;       // tokens: one 32-element bf16 block of kBM rows
-constexpr int kXPerWave = kXBytes / 1024 / kGW;  // token KiBs each wave fills per block
-constexpr int kWOff = kXBytes;          // nibbles: wave w's 64 slots x 16 bytes at kWOff + 1024 w
-constexpr int kSOff = kWOff + kGW * 1024;  // scales: wave w's 16 dwords (+ 48 unread) at kSOff + 256 w
-constexpr int kStageBytes = kSOff + kGW * 256;
-constexpr int kStages = (80 * 1024) / kStageBytes;  // LDS stages (blocks in flight), a ring; two work-groups per CU
-constexpr int kLoadsPerStep = kXPerWave + 2;  // direct LDS loads per wave and block: token KiBs, nibbles, scales
+constexpr int kRingBytes = (kWGPerCU == 1 ? 152 : 76) * 1024;  // LDS ring per work-group, with room to spare
+
+// One LDS ring stage holds a 32-element block of kF 16-token fragments
+// (tile rows 16t..16t+15 in KiB t), each wave's 64 nibble slots (16 bytes
+// each, at kWOff + 1024 w) and its 16 scale dwords (at kSOff + 64 w).  Tiles
+// with fewer rows use smaller stages and so a deeper ring.
+template <int kFrags>
+struct Ring {
+  static constexpr int kF = kFrags;
+  static constexpr int kXPW = kFrags >= kGW ? kFrags / kGW : 1;  // token KiBs per wave (waves past kF load none)
+  static constexpr int kWOff = kFrags * 1024;
+  static constexpr int kSOff = kWOff + kGW * 1024;
+  static constexpr int kBytes = kSOff + kGW * 64;
+  static constexpr int kStages = kRingBytes / kBytes;
+  static constexpr int kMaxLoads = kXPW + 2;  // direct loads per wave and block: token KiBs, nibbles, scales
+  static_assert(kStages >= 5 && kMaxLoads * (kStages - 2) < 64, "ring depth and vmcnt range");
+};
 #ifndef GX_PREFILL_GROUP_M
 #define GX_PREFILL_GROUP_M 4
 #endif
 constexpr int kGroupM = GX_PREFILL_GROUP_M;  // m-tiles per tile group
 constexpr int kExpertsPerLane = kMaxExperts / kWave;
-static_assert(kXPerWave * kGW * 1024 == kXBytes, "token KiBs split evenly over the waves");
-static_assert(kStages >= 5 && kLoadsPerStep * (kStages - 2) < 64, "vmcnt range");
 
 struct GroupedParams {
   const uint16_t* x;         // [*][K] bf16 rows
@@ -92,6 +103,7 @@ struct GroupedParams {
   uint16_t* gate_up;         // gated and optional: [rows][N] bf16 gate/up values
   float alpha, limit;
   int nwt;                   // work-group n-tiles: ceil(N / (64 kGW))
+  int* queue;                // null: one tile per work-group; else per-XCD tile counters (persistent grid)
 };
 
 struct TileCoord {
@@ -102,63 +114,98 @@ struct TileCoord {
   int nt;   // n-tile
 };
 
-// Work-group vb's tile, or false if it has none.  The m-tiles (ceil(M_e /
-// kBM) per expert, in expert order) and n-tiles form total = m-tiles x nwt
-// tiles, ordered group by group (kGroupM m-tiles x nwt n-tiles, m fastest)
-// and cut into 8 contiguous ranges of ceil(total / 8): work-group vb runs
-// on XCD vb % 8 and takes tile (vb % 8) * range + vb / 8.  Every lane
-// returns the same values.
-__device__ __forceinline__ bool map_tile(const int32_t* __restrict__ offsets, int E, int nwt, int vb, int lane,
-                                         TileCoord& tc) {
-  int c[kExpertsPerLane], o[kExpertsPerLane + 1];
+// The tile list.  Expert e's rows form M_e / kBM full m-tiles and, if
+// M_e % kBM != 0, one partial m-tile (its last rows); each m-tile pairs with
+// nwt n-tiles.  The full tiles come first, group by group (kGroupM m-tiles
+// x nwt n-tiles, m fastest: a weight tile is read by the group's m-tiles
+// close together, from L2), then the partial tiles (an m-tile's n-tiles in
+// a row: they share its tokens).  Each part is cut into 8 contiguous chunks
+// and XCD x's queue holds full chunk x then partial chunk x, so every XCD
+// gets an even share of long and short tiles, long ones first.
+struct TileList {
+  int f[kExpertsPerLane];  // full m-tiles of the lane's experts
+  int q[kExpertsPerLane];  // partial m-tiles (0 or 1)
+  int ef, ep;              // lane's exclusive prefix of full / partial m-tiles
+  int F, P;                // totals (every lane)
+};
+
+__device__ __forceinline__ TileList make_tile_list(const int32_t* __restrict__ offsets, int E, int lane) {
+  TileList L;
+  int o[kExpertsPerLane + 1];
   const int e0 = lane * kExpertsPerLane;
 #pragma unroll
   for (int i = 0; i <= kExpertsPerLane; ++i) o[i] = offsets[min(e0 + i, E)];  // all in flight at once
-  int local = 0;
+  int lf = 0, lp = 0;
 #pragma unroll
   for (int i = 0; i < kExpertsPerLane; ++i) {
-    c[i] = e0 + i < E ? (o[i + 1] - o[i] + kBM - 1) / kBM : 0;
-    local += c[i];
+    const int m = e0 + i < E ? o[i + 1] - o[i] : 0;
+    L.f[i] = m / kBM;
+    L.q[i] = m % kBM != 0;
+    lf += L.f[i];
+    lp += L.q[i];
   }
-  int incl = local;
+  // both prefix sums in one scan: full in the low 16 bits, partial above
+  int incl = lf | (lp << 16);
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
     const int t = __shfl_up(incl, d, kWave);
     if (lane >= d) incl += t;
   }
-  const int excl = incl - local;
-  const int mtiles = __builtin_amdgcn_readlane(incl, kWave - 1);
-  const int total = mtiles * nwt;
-  const int range = (total + 7) >> 3;
-  const int i = vb >> 3;
-  if (i >= range) return false;
-  const int v = (vb & 7) * range + i;
-  if (v >= total) return false;
-  const int gsz = kGroupM * nwt;
-  const int grp = v / gsz;
-  const int r = v - grp * gsz;
-  const int gm = min(kGroupM, mtiles - grp * kGroupM);  // m-tiles in this group
-  const int mt = grp * kGroupM + r % gm;
-  tc.nt = r / gm;
-  const bool mine = mt >= excl && mt < incl;
-  const unsigned long long bal = __ballot(mine);
-  const int src = __ffsll(static_cast<long long>(bal)) - 1;  // bal != 0: mt < mtiles
-  int ee = -1, base = excl, run = excl;
+  const int tot = __builtin_amdgcn_readlane(incl, kWave - 1);
+  L.ef = (incl & 0xffff) - lf;
+  L.ep = (incl >> 16) - lp;
+  L.F = tot & 0xffff;
+  L.P = tot >> 16;
+  return L;
+}
+
+// Tiles in XCD x's queue; `lenF` of them full.
+__device__ __forceinline__ int queue_len(const TileList& L, int nwt, int x, int& lenF) {
+  const int totF = L.F * nwt, totP = L.P * nwt;
+  const int cf = (totF + 7) >> 3, cp = (totP + 7) >> 3;
+  lenF = min(max(totF - x * cf, 0), cf);
+  return lenF + min(max(totP - x * cp, 0), cp);
+}
+
+// Coordinates of entry t < queue_len of XCD x's queue.  Every lane returns
+// the same values, in scalar registers (buffer descriptors, branches).
+__device__ __forceinline__ void tile_at(const TileList& L, const int32_t* __restrict__ offsets, int nwt, int x, int t,
+                                        int lenF, int lane, TileCoord& tc) {
+  const int e0 = lane * kExpertsPerLane;
+  int key, nt;  // m-tile index within its part
+  const bool full = t < lenF;
+  if (full) {
+    const int v = x * ((L.F * nwt + 7) >> 3) + t;
+    const int gsz = kGroupM * nwt;
+    const int grp = v / gsz;
+    const int r = v - grp * gsz;
+    const int gm = min(kGroupM, L.F - grp * kGroupM);  // m-tiles in this group
+    key = grp * kGroupM + r % gm;
+    nt = r / gm;
+  } else {
+    const int v = x * ((L.P * nwt + 7) >> 3) + (t - lenF);
+    key = v / nwt;
+    nt = v - key * nwt;
+  }
+  // the lane holding m-tile `key` and its expert
+  int ee = -1, base = 0, run = full ? L.ef : L.ep;
 #pragma unroll
   for (int k = 0; k < kExpertsPerLane; ++k) {
-    if (ee < 0 && mt < run + c[k]) {
+    const int c = full ? L.f[k] : L.q[k];
+    if (ee < 0 && key < run + c) {
       ee = e0 + k;
       base = run;
     }
-    run += c[k];
+    run += c;
   }
-  // wave-uniform values in scalar registers (buffer descriptors, branches)
+  // ee >= 0: key below the lane's end; key >= the lane's start: the one owner
+  const unsigned long long bal = __ballot(ee >= 0 && key >= (full ? L.ef : L.ep));
+  const int src = __ffsll(static_cast<long long>(bal)) - 1;
   tc.e = __builtin_amdgcn_readfirstlane(__shfl(ee, src, kWave));
-  tc.m0 = __builtin_amdgcn_readfirstlane((mt - __shfl(base, src, kWave)) * kBM);
-  tc.nt = __builtin_amdgcn_readfirstlane(tc.nt);
   tc.off = __builtin_amdgcn_readfirstlane(offsets[tc.e]);
   tc.cnt = __builtin_amdgcn_readfirstlane(offsets[tc.e + 1]) - tc.off;
-  return true;
+  tc.m0 = full ? __builtin_amdgcn_readfirstlane((key - __shfl(base, src, kWave)) * kBM) : (tc.cnt / kBM) * kBM;
+  tc.nt = __builtin_amdgcn_readfirstlane(nt);
 }
 
 // s_waitcnt vmcnt(N), other counters untouched.
@@ -169,22 +216,25 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 // s_waitcnt vmcnt(NB * per) for a wave issuing `per` loads per block
-// (wave-uniform, kLoadsPerStep - kXPerWave .. kLoadsPerStep).
-template <int NB>
+// (wave-uniform, 2 .. kMax).
+template <int NB, int kMax>
 __device__ __forceinline__ void wait_blocks(int per) {
-  static_assert(kXPerWave == 2, "three load counts per block");
-  if (per == kLoadsPerStep) wait_vm<NB * kLoadsPerStep>();
-  else if (per == kLoadsPerStep - 1) wait_vm<NB * (kLoadsPerStep - 1)>();
-  else wait_vm<NB * (kLoadsPerStep - 2)>();
+  static_assert(kMax >= 2 && kMax <= 4, "two to four loads per block");
+  if (kMax >= 4 && per >= 4) wait_vm<NB * (kMax >= 4 ? 4 : 2)>();
+  else if (kMax >= 3 && per == 3) wait_vm<NB * (kMax >= 3 ? 3 : 2)>();
+  else wait_vm<NB * 2>();
 }
 
-template <bool kGated, bool kFull>
+template <bool kGated, bool kFull, int kCls>
 __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileCoord& tc, uint8_t* xs, int lane,
                                              int w) {
   const TiledGeom& g = a.g;
   const int K = g.K, N = g.N, nb = g.nb;
   const int mc = min(kBM, tc.cnt - tc.m0);
-  const int nfr = kFull ? kFrags : (mc + 15) >> 4;  // 16-token fragments holding rows
+  using R = Ring<kCls>;
+  constexpr int kFrags = R::kF, kXPerWave = R::kXPW, kStages = R::kStages, kStageBytes = R::kBytes;
+  constexpr int kWOff = R::kWOff, kSOff = R::kSOff;
+  const int nfr = kFull ? kFrags : (mc + 15) >> 4;  // 16-token fragments holding rows (<= kFrags)
   const int tile = tc.nt * kGW + w;
   const bool active = tile < N / kTileRows;  // wave-uniform: rows past N (last n-tile) only stage tokens
 
@@ -204,7 +254,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
     xsrc[c] = a.x + static_cast<size_t>(prow) * K + q * 8;
   }
   // Token KiBs of this wave holding rows (the others are not loaded).
-  const int nxw = kFull ? kXPerWave : max(0, min(kXPerWave, nfr - kXPerWave * w));
+  const int nxw = kFull ? kXPerWave : max(0, min(kXPerWave, nfr - kXPerWave * w));  // <= kFrags - kXPerWave w
   // B fragment t: token 16t + l % 16, quarter l / 16.
   const int bj = lane & 15;
   const int boff = bj * 64 + 16 * ((lane >> 4) ^ ((bj >> 1) & 3));
@@ -233,7 +283,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
         __builtin_amdgcn_global_load_lds(xsrc[c] + static_cast<size_t>(bb) * 32,
                                          (lds_void_t*)(sp + 1024 * (kXPerWave * w + c)), 16, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void_t*)(sp + kWOff + 1024 * w), 16, wvoff, bb * 1024, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_void_t*)(sp + kSOff + 256 * w), 4, svoff, bb * 64, 0, 0);
+    if (lane < 16)  // the 16 distinct scale dwords
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_void_t*)(sp + kSOff + 64 * w), 4, svoff, bb * 64, 0, 0);
   };
   // Software pipeline over blocks: step kb runs block kb's products from
   // registers while the LDS reads of block kb + 1 land and its A operands
@@ -254,7 +305,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
   auto read_stage = [&](int st, u32x4_t& wv, uint32_t& sv, bf16x8_t (&bv)[kFrags]) __attribute__((always_inline)) {
     const uint8_t* sp = xs + st * kStageBytes;
     wv = *reinterpret_cast<const u32x4_t*>(sp + kWOff + 1024 * w + 16 * lane);
-    sv = *reinterpret_cast<const uint32_t*>(sp + kSOff + 256 * w + 4 * (lane & 15));
+    sv = *reinterpret_cast<const uint32_t*>(sp + kSOff + 64 * w + 4 * (lane & 15));
 #pragma unroll
     for (int t = 0; t < kFrags; ++t)
       if (kFull || t < nfr) bv[t] = *reinterpret_cast<const bf16x8_t*>(sp + boff + 1024 * t);
@@ -271,7 +322,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
 
   // Block 0: its loads were followed by those of blocks 1 .. kStages - 2.
   const int per = nxw + 2;  // this wave's loads per block
-  wait_blocks<kStages - 2>(per);
+  wait_blocks<kStages - 2, R::kMaxLoads>(per);
   __builtin_amdgcn_s_barrier();
   if (active) {
     u32x4_t wv;
@@ -288,7 +339,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
       // Blocks kb + 1, kb + 2 were followed by kb + 3 .. kb + kStages - 2.
       // This wave's reads of stages kb - 1 and kb are complete, so after the
       // barrier no wave reads them any more and kb + 1, kb + 2 are visible.
-      wait_blocks<kStages - 4>(per);
+      wait_blocks<kStages - 4, R::kMaxLoads>(per);
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       __builtin_amdgcn_s_barrier();
     }
@@ -298,7 +349,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
       // products of the half of block kb whose fragments it replaces.
       const uint8_t* sp = xs + st1 * kStageBytes;
       const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(sp + kWOff + 1024 * w + 16 * lane);
-      const uint32_t sv = *reinterpret_cast<const uint32_t*>(sp + kSOff + 256 * w + 4 * (lane & 15));
+      const uint32_t sv = *reinterpret_cast<const uint32_t*>(sp + kSOff + 64 * w + 4 * (lane & 15));
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -408,16 +459,67 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
 }
 
 template <bool kGated>
-__global__ __launch_bounds__(kGW * kWave, 2) void grouped_mfma_kernel(GroupedParams a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t xs[kStages * kStageBytes];
+__device__ __forceinline__ void run_tile(const GroupedParams& a, const TileCoord& tc, uint8_t* xs, int lane, int w) {
+  const int mc = min(kBM, tc.cnt - tc.m0);
+  if (mc == kBM)
+    grouped_tile<kGated, true, 8>(a, tc, xs, lane, w);
+  else if (mc > 64)
+    grouped_tile<kGated, false, 8>(a, tc, xs, lane, w);
+  else if (mc > 32)
+    grouped_tile<kGated, false, 4>(a, tc, xs, lane, w);
+  else
+    grouped_tile<kGated, false, 2>(a, tc, xs, lane, w);
+}
+
+// Counters of the persistent grid: XCD x's queue at queue[kQueueStride x],
+// the finished work-groups at queue[kQueueStride * 8].  All start at zero;
+// the last work-group to finish zeroes them for the next launch.
+constexpr int kQueueStride = 32;  // one 128-byte line per counter
+
+template <bool kGated>
+__global__ __launch_bounds__(kGW * kWave, kWGPerCU) void grouped_mfma_kernel(GroupedParams a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[kRingBytes];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  TileCoord tc;
-  if (!map_tile(a.offsets, a.E, a.nwt, static_cast<int>(blockIdx.x), lane, tc)) return;  // the whole work-group
-  if (tc.cnt - tc.m0 >= kBM)
-    grouped_tile<kGated, true>(a, tc, xs, lane, w);
-  else
-    grouped_tile<kGated, false>(a, tc, xs, lane, w);
+  const int vb = static_cast<int>(blockIdx.x);
+  const int x0 = vb & 7;  // work-group vb runs on XCD vb % 8
+  // Without a queue: entry vb / 8 of XCD x0's queue, one tile.  With one
+  // (persistent grid): entries of this XCD's queue, then of the others'; the
+  // taken index is passed through two alternating LDS words past every ring
+  // layout (a wave is at most one round behind: each round has a barrier).
+  int* word = reinterpret_cast<int*>(xs + kRingBytes - 64);
+  const bool persistent = a.queue != nullptr;
+  int k = 0;  // queues found empty
+  for (int round = 0;; ++round) {
+    const int x = (x0 + k) & 7;
+    int t;
+    if (persistent) {
+      if (threadIdx.x == 0) word[round & 1] = atomicAdd(&a.queue[kQueueStride * x], 1);
+      __syncthreads();
+      t = __builtin_amdgcn_readfirstlane(word[round & 1]);
+    } else {
+      if (round > 0) break;
+      t = vb >> 3;
+    }
+    const TileList L = make_tile_list(a.offsets, a.E, lane);
+    int lenF;
+    if (t >= queue_len(L, a.nwt, x, lenF)) {
+      if (!persistent || ++k == 8) break;
+      continue;
+    }
+    TileCoord tc;
+    tile_at(L, a.offsets, a.nwt, x, t, lenF, lane, tc);
+    // Recomputed per tile rather than hoisted out of the loop: values kept
+    // live across tiles would push the tile's registers into scratch.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    run_tile<kGated>(a, tc, xs, ln, w);
+  }
+  if (!persistent) return;
+  if (threadIdx.x == 0 && atomicAdd(&a.queue[kQueueStride * 8], 1) == static_cast<int>(gridDim.x) - 1) {
+#pragma unroll
+    for (int x = 0; x <= 8; ++x) atomicExch(&a.queue[kQueueStride * x], 0);
+  }
 }
 
 }  // namespace
@@ -443,14 +545,20 @@ hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s) {
   p.alpha = a.alpha;
   p.limit = a.limit;
   p.nwt = (a.N / kTileRows + kGW - 1) / kGW;
-  // sum_e ceil(M_e / kBM) <= rows / kBM + (experts with rows); the kernel
-  // counts the real tiles and spreads them evenly over the XCDs
-  const long mt_bound = (a.rows + kBM - 1) / kBM + (a.E < a.rows ? a.E : a.rows);
-  const long total = mt_bound * p.nwt;
-  if (total > (1L << 30) || static_cast<size_t>(a.N) * (a.K / 32) > (1u << 30) ||
+  p.queue = a.queue;
+  // full m-tiles <= rows / kBM, partial ones <= experts with rows; the
+  // kernel counts the real tiles
+  const long fb = static_cast<long>(a.rows / kBM) * p.nwt, pb = static_cast<long>(a.E < a.rows ? a.E : a.rows) * p.nwt;
+  const long per_xcd = (fb + 7) / 8 + (pb + 7) / 8;
+  if (per_xcd > (1L << 27) || fb >= (1L << 16) * p.nwt || static_cast<size_t>(a.N) * (a.K / 32) > (1u << 30) ||
       p.g.nib_bytes >= (static_cast<size_t>(1) << 31))
-    return hipErrorInvalidValue;  // tile and buffer offsets are 32-bit
-  const int grid = static_cast<int>((total + 7) & ~7L);
+    return hipErrorInvalidValue;  // tile counts (16-bit scan fields) and buffer offsets (32-bit)
+  int grid = static_cast<int>(8 * per_xcd);
+  if (a.queue) {
+    const int slots = 8 * ((kWGPerCU * a.num_cus + 7) / 8);  // every work-group slot, a multiple of 8
+    if (a.num_cus <= 0) return hipErrorInvalidValue;
+    grid = grid < slots ? grid : slots;
+  }
   if (a.gated)
     gx_launch(grouped_mfma_kernel<true>, dim3(grid), dim3(kGW * kWave), 0, s, a.timer, p);
   else
