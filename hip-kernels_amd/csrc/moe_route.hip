@@ -6,7 +6,11 @@
 // (moe_permute.cu:184-236, moe_layer.cu:1217-1234), with no host round trip:
 //
 //   logits_kernel      each wave computes whole logits (TT tokens x EPW
-//                      experts) with the gemv_bf16_kernel summation tree;
+//                      experts) with the gemv_bf16_kernel summation tree
+//                      (few tokens);
+//   logits_lds_kernel  (many tokens) the same tree, chains of 64 pairs per
+//                      lane, each pair's butterfly run in one lane after an
+//                      LDS transpose;
 //   topk_plan_kernel   (T <= kTopkPlanMaxT) one work-group of 16 waves selects
 //                      every token's top-k and builds the plan from LDS;
 //   topk_kernel +      (larger T) top-k spread over the device, then the plan
@@ -454,6 +458,92 @@ __global__ __launch_bounds__(kRouteThreads) void logits_kernel(const uint16_t* _
   }
 }
 
+// Logits of 8 tokens x 8 experts per work-group with the same tree, for
+// many tokens.  Wave j is the reference's wave j: lane l chains fmaf over
+// the chunks tau = l + 64 j, tau + 256, ... of all 64 (token, expert) pairs
+// at once (each loaded chunk feeds 8 pairs); the chains then go through LDS
+// so that lane p holds the 64 chains of pair p and runs the xor-butterfly
+// tree of tree_sum_lane0 in registers (level m adds lane l + m into lane l,
+// m = 32 .. 1); lane p of wave 0 adds the four wave sums in order from 0.
+constexpr int kLdsTT = 8, kLdsEPW = 8;
+template <bool F32>
+__global__ __launch_bounds__(kRouteThreads, 2) void logits_lds_kernel(const uint16_t* __restrict__ x,
+                                                                      const uint16_t* __restrict__ W,
+                                                                      const uint16_t* __restrict__ bias, int T, int E,
+                                                                      int H, void* __restrict__ logits) {
+  constexpr int kPairs = kLdsTT * kLdsEPW;  // = kWave: one pair per lane in the tree phase
+  static_assert(kPairs == kWave, "one pair per lane");
+  __shared__ float red[4][kPairs][kWave + 1];  // [wave][pair][lane], padded: conflict-free rows and columns
+  const int lane = threadIdx.x & 63;
+  const int j = threadIdx.x >> 6;
+  const int t0 = blockIdx.y * kLdsTT, e0 = blockIdx.x * kLdsEPW;
+  const int KV = H >> 3;
+  float acc[kLdsTT][kLdsEPW];
+#pragma unroll
+  for (int t = 0; t < kLdsTT; ++t)
+#pragma unroll
+    for (int e = 0; e < kLdsEPW; ++e) acc[t][e] = 0.0f;
+  // rows past T / E read row 0 (their results are not stored)
+  const uint16_t* xr = x + static_cast<size_t>(t0 < T ? t0 : 0) * H;
+  const uint16_t* wr = W + static_cast<size_t>(e0 < E ? e0 : 0) * H;
+  const int tn = min(kLdsTT, T - t0), en = min(kLdsEPW, E - e0);
+  auto load = [&](int c, uint4 (&xv)[kLdsTT], uint4 (&wv4)[kLdsEPW]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < kLdsTT; ++t)
+      xv[t] = *reinterpret_cast<const uint4*>(xr + static_cast<size_t>(t < tn ? t : 0) * H + c * 8);
+#pragma unroll
+    for (int e = 0; e < kLdsEPW; ++e)
+      wv4[e] = *reinterpret_cast<const uint4*>(wr + static_cast<size_t>(e < en ? e : 0) * H + c * 8);
+  };
+  auto fma_chunk = [&](const uint4 (&xv)[kLdsTT], const uint4 (&wv4)[kLdsEPW]) __attribute__((always_inline)) {
+    float wf[kLdsEPW][8];
+#pragma unroll
+    for (int e = 0; e < kLdsEPW; ++e) unpack_bf16x8(wv4[e], wf[e]);
+#pragma unroll
+    for (int t = 0; t < kLdsTT; ++t) {
+      float xf[8];
+      unpack_bf16x8(xv[t], xf);
+#pragma unroll
+      for (int e = 0; e < kLdsEPW; ++e)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[t][e] = __builtin_fmaf(xf[i], wf[e][i], acc[t][e]);
+    }
+  };
+  // Chunks tau, tau + 256, ... in order.
+  for (int c = lane + kWave * j; c < KV; c += kRouteThreads) {
+    uint4 xa[kLdsTT], wa[kLdsEPW];
+    load(c, xa, wa);
+    fma_chunk(xa, wa);
+  }
+#pragma unroll
+  for (int t = 0; t < kLdsTT; ++t)
+#pragma unroll
+    for (int e = 0; e < kLdsEPW; ++e) red[j][t * kLdsEPW + e][lane] = acc[t][e];
+  __syncthreads();
+  float cv[kWave];
+#pragma unroll
+  for (int l = 0; l < kWave; ++l) cv[l] = red[j][lane][l];
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1)
+#pragma unroll
+    for (int l = 0; l < m; ++l) cv[l] = cv[l] + cv[l + m];
+  __syncthreads();  // every row read before the sums overwrite column 0
+  red[j][lane][0] = cv[0];
+  __syncthreads();
+  if (j == 0) {
+    const int t = lane / kLdsEPW, e = lane % kLdsEPW;
+    float v = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) v = v + red[jj][lane][0];
+    if (t < tn && e < en) {
+      if (bias != nullptr) v = v + bf16_to_f32(bias[e0 + e]);
+      const size_t o = static_cast<size_t>(t0 + t) * E + e0 + e;
+      if constexpr (F32) reinterpret_cast<float*>(logits)[o] = v;
+      else reinterpret_cast<uint16_t*>(logits)[o] = f32_to_bf16(v);
+    }
+  }
+}
+
 // Top-k softmax of every token, one token per wave.
 template <bool F32, int NV>
 __global__ __launch_bounds__(kRouteThreads) void topk_kernel(const void* logits, int T, int E, int k, int variant,
@@ -621,8 +711,8 @@ void launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t) {
     gx_launch(logits_kernel<1, 1, 0, F32>, dim3((a.E + 3) / 4, a.T), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b,
               a.T, a.E, a.H, a.logits);
   } else {
-    gx_launch(logits_kernel<8, 4, 0, F32>, dim3((a.E + 15) / 16, (a.T + 7) / 8), dim3(kRouteThreads), 0, s, t, a.x,
-              a.W, a.b, a.T, a.E, a.H, a.logits);
+    gx_launch(logits_lds_kernel<F32>, dim3((a.E + kLdsEPW - 1) / kLdsEPW, (a.T + kLdsTT - 1) / kLdsTT),
+              dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b, a.T, a.E, a.H, a.logits);
   }
 }
 
