@@ -130,13 +130,18 @@ def test_topk_softmax(gpu, orc, torch_mod, T, k, fp32):
     assert np.array_equal(host(tpe), hist)
 
 
-@pytest.mark.parametrize("T,fp32", [(1, False), (8, False), (64, False), (9, True), (4096, True)])
-def test_route_router_topk(gpu, orc, torch_mod, T, fp32):
-    """Router GEMV (gemv_bf16 tree) + top-k in one launch; T=4096 fp32 is
-    logits bit-exact, indices bit-exact, weights bit-exact."""
+@pytest.mark.parametrize("T,fp32,E,H", [(1, False, 128, 2880), (8, False, 128, 2880), (64, False, 128, 2880),
+                                         (9, True, 128, 2880), (4096, True, 128, 2880), (100, False, 20, 512),
+                                         (300, True, 36, 4104), (130, True, 256, 2880)])
+def test_route_router_topk(gpu, orc, torch_mod, T, fp32, E, H):
+    """Router GEMV (gemv_bf16 tree) + top-k; T=4096 fp32 is BASELINE config 1:
+    logits bit-exact, indices bit-exact, weights bit-exact.  The many-token
+    cases also cover partial 8 x 8 blocks (T, E not multiples of 8), a short
+    hidden size (chains past the last chunk stay 0), three chunks per chain
+    (H = 4104) and 256 experts."""
     torch = torch_mod
-    E, H, k = 128, 2880, 4
-    rng = np.random.default_rng(T)
+    k = 4
+    rng = np.random.default_rng(T + E + H)
     x = moe_data.bf16(rng.normal(0, 1, (T, H)))
     W = moe_data.bf16(rng.normal(0, 0.02, (E, H)))
     b = moe_data.bf16(rng.normal(0, 0.02, E))
@@ -153,7 +158,7 @@ def test_route_router_topk(gpu, orc, torch_mod, T, fp32):
     ridx, rw = orc.topk_softmax(lf, k)
     assert np.array_equal(host(idx), ridx)
     assert np.array_equal(host(w).view(np.uint32), rw.view(np.uint32))
-    # repeat: the launch's tickets reset themselves
+    # repeat: nothing carries over between calls
     logits2, idx2, w2 = gpu.route(dev(x, torch), dev(W, torch), dev(b, torch), k, logits_fp32=fp32)
     assert np.array_equal(host(idx2), ridx)
 
