@@ -691,6 +691,112 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_lanes_kernel(const voi
   build_plan<kPlanThreads>([&](int s2) { return s_idx[s2]; }, T, K, E, p);
 }
 
+// The plan of S <= 64 slots (values from LDS) built by one wave with no
+// barrier: lane s holds slot s; its rank among equal experts comes from
+// ballots over the expert bits; the counts go through LDS to the lanes that
+// own the experts (expert lane + 64 j), which scan them into offsets and the
+// ascending active list.  Same outputs as build_plan.  LDS accesses of one
+// wave execute in order, so values written are read back without a wait.
+template <int NV>
+__device__ __forceinline__ void plan_one_wave(const int32_t* s_idx, int S, int k, int E, PlanBufs p, int lane,
+                                              int32_t* s_cnt, int32_t* s_off, int32_t* s_aidx) {
+  const int e = lane < S ? s_idx[lane] : -1;
+  const bool valid = e >= 0 && e < E;
+  unsigned long long peers = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {  // E <= 256
+    const bool bit = valid && ((e >> b) & 1);
+    const unsigned long long mb = __ballot(bit);
+    peers &= bit ? mb : ~mb;
+  }
+  const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s_cnt[lane + kWave * j] = 0;
+  __builtin_amdgcn_wave_barrier();
+  if (valid && rank == 0) s_cnt[e] = __popcll(peers);
+  __builtin_amdgcn_wave_barrier();
+  // experts lane + 64 j: counts, exclusive offsets (scan over j-major order)
+  int base = 0, abase = 0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int ex = lane + kWave * j;
+    const int c = ex < E ? s_cnt[ex] : 0;
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += o;
+    }
+    const int excl = base + incl - c;
+    const bool act = c > 0;
+    const unsigned long long am = __ballot(act);
+    const int aidx = abase + __popcll(am & ((1ull << lane) - 1ull));
+    if (ex < E) {
+      p.counts[ex] = c;
+      p.offsets[ex] = excl;
+      s_off[ex] = excl;
+      if (ex == E - 1) p.offsets[E] = excl + c;
+    }
+    if (act) {
+      p.active[aidx] = ex;
+      s_aidx[ex] = aidx;
+      if (p.tasks) {
+        int32_t* t = p.tasks + static_cast<size_t>(aidx) * kTaskInts;
+        t[0] = ex;
+        t[1] = excl;
+        t[2] = c;
+        t[3] = 0;
+      }
+    }
+    base += __shfl(incl, kWave - 1, kWave);
+    abase += __popcll(am);
+  }
+  const int nact = abase;
+  if (lane == 0) *p.n_active = nact;
+  if (p.tasks) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int r = lane + kWave * j;
+      if (r < E && r >= nact) p.tasks[static_cast<size_t>(r) * kTaskInts] = -1;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (valid) {
+    const int pos = s_off[e] + rank;
+    p.gather_map[lane] = pos;
+    p.perm_token[pos] = lane / k;
+    if (p.tasks && rank < kTaskTokens) p.tasks[static_cast<size_t>(s_aidx[e]) * kTaskInts + 4 + rank] = lane / k;
+  } else if (lane < S) {
+    p.gather_map[lane] = -1;
+  }
+}
+
+// Top-k of T <= kSmallTopkMaxT tokens (wave t: token t, topk_token) and the
+// plan of their T k <= 64 slots by wave 0 after one barrier.
+constexpr int kSmallTopkMaxT = 8;
+template <bool F32, int NV>
+__global__ __launch_bounds__(kSmallTopkMaxT * kWave) void topk_plan_small_kernel(const void* logits, int T, int E,
+                                                                                 int k, int variant, int32_t* idx,
+                                                                                 float* w, PlanBufs p) {
+  __shared__ int32_t s_idx[kSmallTopkMaxT * kMaxTopK];
+  __shared__ float s_w[kSmallTopkMaxT * kMaxTopK];
+  __shared__ int32_t s_cnt[kMaxExperts], s_off[kMaxExperts], s_aidx[kMaxExperts];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (wv < T) {
+    float v[NV];
+    load_token_logits<F32, NV>(logits, wv, E, lane, v);
+    topk_token(v, k, variant, s_idx + wv * k, s_w + wv * k, nullptr, lane);
+  }
+  __syncthreads();
+  if (wv != 0) return;
+  const int S = T * k;
+  if (lane < S) {
+    idx[lane] = s_idx[lane];
+    w[lane] = s_w[lane];
+  }
+  plan_one_wave<NV>(s_idx, S, k, E, p, lane, s_cnt, s_off, s_aidx);
+}
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* idx, int T, int k, int E, PlanBufs p) {
   build_plan<kPlanThreads>([&](int s) { return idx[s]; }, T, k, E, p);
 }
@@ -758,6 +864,25 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
   else launch_logits<false>(a, s, first);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
+  if (fused && a.T <= kSmallTopkMaxT) {
+    const void* lg = a.logits;
+    const int nv = (a.E + kWave - 1) / kWave;
+#define GX_TPS(F_, NV_) gx_launch(topk_plan_small_kernel<F_, NV_>, dim3(1), dim3(kWave * a.T), 0, s, last, lg, a.T, \
+                                  a.E, a.k, variant, a.idx, a.w, a.plan)
+    if (a.logits_fp32) {
+      if (nv <= 1) GX_TPS(true, 1);
+      else if (nv == 2) GX_TPS(true, 2);
+      else if (nv == 3) GX_TPS(true, 3);
+      else GX_TPS(true, 4);
+    } else {
+      if (nv <= 1) GX_TPS(false, 1);
+      else if (nv == 2) GX_TPS(false, 2);
+      else if (nv == 3) GX_TPS(false, 3);
+      else GX_TPS(false, 4);
+    }
+#undef GX_TPS
+    return hipGetLastError();
+  }
   if (fused && a.T <= kLaneTopkMaxT && a.E <= kLaneTopkSlice * (kPlanThreads / kWave) && a.E % kLaneTopkSlice == 0) {
     const void* lg = a.logits;
 #define GX_TPL(F_, K_) gx_launch(topk_plan_lanes_kernel<F_, K_>, dim3(1), dim3(kPlanThreads), 0, s, last, lg, a.T, \
