@@ -18,13 +18,13 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round to nearest even; NaN stays a quiet NaN with its sign.
+// Round to nearest even; NaN stays a quiet NaN with its sign.  Both results
+// are computed and one is selected (no divergent branch in epilogues).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))
-    return static_cast<uint16_t>((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const bool nan = (u & 0x7fffffffu) > 0x7f800000u;
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return static_cast<uint16_t>(nan ? ((u >> 16) | 0x0040u) : rne);
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -32,15 +32,15 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to
 // e^x by Cody-Waite reduction x = n*ln2 + r (|r| <= ln2/2, two-constant
 // split of ln 2 applied with fma) and the degree-7 Taylor polynomial of e^r
 // in Horner form, scaled by 2^n with ldexp.
+// NaN, overflow (inf) and underflow (0) are selected after the polynomial
+// path rather than branched to (the same function, no divergent branch).
 __device__ __forceinline__ float gx_expf(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __builtin_inff();
-  if (x < -103.97208404541015625f) return 0.0f;
   const float log2e = 1.44269502162933349609375f;
   const float ln2_hi = 0.693147182464599609375f;
   const float ln2_lo = -1.904654323148236e-09f;
-  float n = __builtin_rintf(x * log2e);
-  float r = __builtin_fmaf(-n, ln2_hi, x);
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 89.0f);  // keeps n an in-range int
+  float n = __builtin_rintf(xc * log2e);
+  float r = __builtin_fmaf(-n, ln2_hi, xc);
   r = __builtin_fmaf(-n, ln2_lo, r);
   float p = 1.98412698e-4f;
   p = __builtin_fmaf(p, r, 1.38888889e-3f);
@@ -50,7 +50,8 @@ __device__ __forceinline__ float gx_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  return __builtin_ldexpf(p, static_cast<int>(n));
+  const float v = __builtin_ldexpf(p, static_cast<int>(n));
+  return x != x ? x : x > 88.72283935546875f ? __builtin_inff() : x < -103.97208404541015625f ? 0.0f : v;
 }
 
 // GPT-OSS clamped SwiGLU on one (gate, up) pair: gate clamped above at
