@@ -281,6 +281,50 @@ def bench_router(g, torch, T: int = 4096, reps: int = 20):
                 gbs=nbytes / (ms / 1e3) / 1e9)
 
 
+def bench_residual(g, torch, wc, T: int, steps: int = 64):
+    """The decode step's residual add + RMSNorm in front of the MoE:
+    forward_residual (the norm inside the router's launch up to 4 tokens)
+    against fused_residual_rmsnorm_forward + forward_prenormed, each `steps`
+    graph-replayed steps on one layer copy."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77 + T)
+    norm_w = (1.0 + 0.1 * torch.randn((H,), device="cuda", generator=gen)).to(torch.bfloat16)
+    cfg = g.default_config(E, T)
+    L = g.MoELayer().init(cfg, 0, wc["router_w"], wc["router_b"], wc["b1"], wc["b2"], moe_norm_weight=norm_w,
+                          tiled=wc["tiled"])
+    res = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+    delta = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+    normed, ssum, out = (torch.empty((T, H), dtype=torch.bfloat16, device="cuda") for _ in range(3))
+    variants = {
+        "fused": lambda: L.forward_residual(res, delta, residual_out=ssum, out=out),
+        "two_calls": lambda: (g.fused_residual_rmsnorm(res, delta, norm_w, 1e-5, normed=normed, sum_out=ssum),
+                              L.forward_prenormed(normed, ssum, out=out)),
+    }
+    us = {}
+    s = torch.cuda.Stream()
+    for name, fn in variants.items():
+        fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for _ in range(steps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            t0.record(s)
+            graph.replay()
+            t1.record(s)
+        torch.cuda.synchronize()
+        us[name] = t0.elapsed_time(t1) * 1e3 / steps
+        del graph
+    L.destroy()
+    return dict(tokens=T, fused_us=us["fused"], two_calls_us=us["two_calls"],
+                saved_us=us["two_calls"] - us["fused"])
+
+
 def bench_stack(g, torch, layers: int = 36, T: int = 32, steps: int = 256):
     """36 distinct GPT-OSS-120B MoE layers resident (random
     MXFP4 weights, ~61 GB), a decode step at batch 32 = the 36 layer forwards
@@ -418,6 +462,9 @@ def main():
         log("router + top-k T=4096 fp32 logits")
         extra["router"] = bench_router(g, torch)
         log(json.dumps(extra["router"]))
+        log("residual add + RMSNorm in front of the MoE (B=1, 4, 64)")
+        extra["residual_norm"] = [bench_residual(g, torch, copies[0], T) for T in (1, 4, 64)]
+        log(json.dumps(extra["residual_norm"]))
         del copies
         torch.cuda.empty_cache()
         log(f"{args.stack_layers}-layer stack at batch 32")

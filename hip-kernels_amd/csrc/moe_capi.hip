@@ -112,6 +112,7 @@ struct gptoss_moe_layer {
   uint16_t* y = nullptr;
   uint16_t* gate_up = nullptr;
   uint16_t* normed = nullptr;
+  uint16_t* sumres = nullptr;   // residual + delta of forward_residual when the caller keeps no copy
   void* route_scratch = nullptr;
   int32_t* special1 = nullptr;  // [E] W1 / W2 scales hold e8m0 code 0 or 255
   int32_t* special2 = nullptr;
@@ -302,6 +303,7 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   ALLOC(gqueue, int32_t*, grouped_queue_ints() * 4)
   if (L->norm_w != nullptr) {
     ALLOC(normed, uint16_t*, T * H * 2)
+    ALLOC(sumres, uint16_t*, T * H * 2)
   }
 #undef ALLOC
   hipError_t err = hipMemset(L->route_scratch, 0, route_bytes);
@@ -443,11 +445,20 @@ static ProfForward next_prof(gptoss_moe_layer* L, hipStream_t s) {
   return pf;
 }
 
+// The router (optionally with the residual RMSNorm in front: delta != null)
+// then the experts and the combine.
 static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, uint16_t* out,
-                              int T, hipStream_t s) {
+                              int T, hipStream_t s, const uint16_t* delta = nullptr, uint16_t* sum_out = nullptr) {
   const gptoss_moe_config& c = L->cfg;
   RouteArgs ra{};
   ra.x = normed;
+  if (delta != nullptr) {  // normed is the residual stream here
+    ra.delta = delta;
+    ra.norm_w = L->norm_w;
+    ra.eps = c.rms_norm_eps;
+    ra.normed = L->normed;
+    ra.sum_out = sum_out;
+  }
   ra.W = L->router_w;
   ra.b = L->router_b;
   ra.T = T;
@@ -462,6 +473,7 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   const ProfForward pf = next_prof(L, s);
   ra.timer = pf.timer(0);
   HIP_TRY(launch_route(ra, s), "route launch");
+  if (delta != nullptr) return layer_experts(L, L->normed, sum_out, L->w, out, T, s, pf);
   return layer_experts(L, normed, residual, L->w, out, T, s, pf);
 }
 
@@ -496,6 +508,21 @@ int gptoss_moe_layer_forward(gptoss_moe_layer* L, const uint16_t* input, uint16_
   HIP_TRY(launch_rmsnorm(input, L->norm_w, L->normed, T, L->cfg.hidden_size, L->cfg.rms_norm_eps, s),
           "rmsnorm launch");
   return layer_forward_core(L, L->normed, input, out, T, s);
+}
+
+int gptoss_moe_layer_forward_residual(gptoss_moe_layer* L, const uint16_t* residual, const uint16_t* delta,
+                                      uint16_t* residual_out, uint16_t* out, int T, void* stream) {
+  int rc = check_forward_args(L, residual, out, T);
+  if (rc != GPTOSS_OK) return rc;
+  if (L->norm_w == nullptr) return fail(GPTOSS_ERR_STATE, "forward_residual() needs moe_norm_weight (init passed NULL)");
+  if (T == 0) return ok();
+  if (delta == nullptr) return fail(GPTOSS_ERR_INVALID, "null delta");
+  if (!aligned16(delta) || (residual_out && !aligned16(residual_out)))
+    return fail(GPTOSS_ERR_INVALID, "delta and residual_out must be 16-byte aligned");
+  ScopedDevice sd(L->device);
+  if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
+  return layer_forward_core(L, residual, nullptr, out, T, static_cast<hipStream_t>(stream), delta,
+                            residual_out ? residual_out : L->sumres);
 }
 
 int gptoss_moe_layer_forward_routed(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual,
@@ -669,6 +696,21 @@ int gptoss_swiglu_forward(const uint16_t* in, uint16_t* out, int T, int I, float
   if (T == 0) return ok();
   if (!in || !out) return fail(GPTOSS_ERR_INVALID, "null pointer");
   HIP_TRY(launch_swiglu(in, out, T, I, alpha, limit, static_cast<hipStream_t>(stream)), "swiglu launch");
+  return ok();
+}
+
+int gptoss_fused_residual_rmsnorm_forward(const uint16_t* residual, const uint16_t* delta, const uint16_t* weight,
+                                          uint16_t* normed, uint16_t* sum_out, int T, int H, float eps,
+                                          void* stream) {
+  if (T < 0 || H <= 0 || H % 8 != 0)
+    return fail(GPTOSS_ERR_INVALID, "bad shape T=%d H=%d (H a positive multiple of 8)", T, H);
+  if (T == 0) return ok();
+  if (!residual || !delta || !weight || !normed) return fail(GPTOSS_ERR_INVALID, "null pointer");
+  if (!aligned16(residual) || !aligned16(delta) || (sum_out && !aligned16(sum_out)))
+    return fail(GPTOSS_ERR_INVALID, "residual, delta and sum_out must be 16-byte aligned");
+  HIP_TRY(launch_residual_rmsnorm(residual, delta, weight, normed, sum_out, T, H, eps,
+                                  static_cast<hipStream_t>(stream)),
+          "residual rmsnorm launch");
   return ok();
 }
 

@@ -100,6 +100,15 @@ struct RouteArgs {
   int32_t* idx;            // [T][k]
   float* w;                // [T][k]
   PlanBufs plan;           // plan outputs (all may be null to skip the plan)
+  // Fused residual RMSNorm (norm_w != null): x is the residual stream, the
+  // router reads s = x + delta (fp32), normalises it with norm_w / eps, and
+  // writes normed (bf16, the experts' input) and sum_out (bf16(s), the new
+  // residual); the logits are those of normed.
+  const uint16_t* delta;
+  const uint16_t* norm_w;
+  float eps;
+  uint16_t* normed;
+  uint16_t* sum_out;
   KernelTimer timer;       // from the first launch's start to the last one's stop
 };
 

@@ -26,6 +26,7 @@
 
 #include "moe_device.h"
 #include "moe_kernels.h"
+#include "moe_stages.h"
 
 namespace gxmoe {
 
@@ -458,6 +459,136 @@ __global__ __launch_bounds__(kRouteThreads) void logits_kernel(const uint16_t* _
   }
 }
 
+// logits_kernel<TT, EPW, 6> with the residual RMSNorm of rmsnorm.cu:224-337
+// in front: x is the residual stream.  Each wave forms s = x + delta (fp32)
+// for its tokens from the chunks it holds (every chunk c = l + 64 q of the
+// row, q < 6), the sum of squares of s with the router's tree (the chains
+// and butterflies of the logits), inv = 1/sqrt(mean + eps) and the normed
+// bf16 values the products then read.  Wave 0 of the work-groups of experts
+// 0.. also writes normed and sum_out = bf16(s) for the experts' launches.
+template <int TT, int EPW, bool F32>
+__global__ __launch_bounds__(kRouteThreads) void logits_norm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta, const uint16_t* __restrict__ norm_w, float eps,
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias, int T, int E, int H,
+    void* __restrict__ logits, uint16_t* __restrict__ normed, uint16_t* __restrict__ sum_out) {
+  constexpr int NCH = 6;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int e0 = (blockIdx.x * 4 + wv) * EPW;
+  const int t0 = blockIdx.y * TT;
+  if (e0 >= E) return;  // wave-uniform; wave 0 of work-group 0 always has experts
+  const int KV = H >> 3;
+  const uint16_t* wr[EPW];
+#pragma unroll
+  for (int e = 0; e < EPW; ++e) wr[e] = W + static_cast<size_t>(e0 + e < E ? e0 + e : 0) * H;
+  // rows past T read row 0 (their results are not stored)
+  size_t rowo[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) rowo[t] = static_cast<size_t>(t0 + t < T ? t0 + t : 0) * H;
+  uint4 xv[NCH][TT], dv[NCH][TT], wv4[NCH][EPW], nwv[NCH];
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const int c = min(lane + kWave * q, KV - 1);  // positions past KV load a valid chunk, unused
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      xv[q][t] = *reinterpret_cast<const uint4*>(x + rowo[t] + c * 8);
+      dv[q][t] = *reinterpret_cast<const uint4*>(delta + rowo[t] + c * 8);
+    }
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) wv4[q][e] = *reinterpret_cast<const uint4*>(wr[e] + c * 8);
+    nwv[q] = *reinterpret_cast<const uint4*>(norm_w + c * 8);
+  }
+  auto sum8 = [&](int q, int t, float (&s8)[8]) __attribute__((always_inline)) {
+    float a[8], b[8];
+    unpack_bf16x8(xv[q][t], a);
+    unpack_bf16x8(dv[q][t], b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s8[i] = a[i] + b[i];
+  };
+  // sum of squares: chain j = q & 3 takes positions q = j, j + 4 in order
+  float inv[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    float ssa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < NCH; ++q)
+      if (lane + kWave * q < KV) {
+        float s8[8];
+        sum8(q, t, s8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ssa[q & 3] = __builtin_fmaf(s8[i], s8[i], ssa[q & 3]);
+      }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ss = ss + tree_sum_lane0(ssa[j]);
+    ss = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(ss)), 0)));
+    inv[t] = 1.0f / __builtin_sqrtf(ss / static_cast<float>(H) + eps);
+  }
+  // normed chunks (bf16), replacing the x chunks; the designated wave stores them
+  const bool writer = blockIdx.x == 0 && wv == 0;
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    float wn[8];
+    unpack_bf16x8(nwv[q], wn);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      float s8[8];
+      sum8(q, t, s8);
+      uint32_t o[4], so[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] = f32_to_bf16((s8[2 * i] * inv[t]) * wn[2 * i]) |
+               (static_cast<uint32_t>(f32_to_bf16((s8[2 * i + 1] * inv[t]) * wn[2 * i + 1])) << 16);
+        so[i] = f32_to_bf16(s8[2 * i]) | (static_cast<uint32_t>(f32_to_bf16(s8[2 * i + 1])) << 16);
+      }
+      xv[q][t] = make_uint4(o[0], o[1], o[2], o[3]);
+      const int c = lane + kWave * q;
+      if (writer && c < KV && t0 + t < T) {
+        *reinterpret_cast<uint4*>(normed + rowo[t] + c * 8) = xv[q][t];
+        if (sum_out) *reinterpret_cast<uint4*>(sum_out + rowo[t] + c * 8) = make_uint4(so[0], so[1], so[2], so[3]);
+      }
+    }
+  }
+  float acc[TT][EPW][4];
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
+#pragma unroll
+    for (int e = 0; e < EPW; ++e)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[t][e][j] = 0.0f;
+#pragma unroll
+  for (int q = 0; q < NCH; ++q)
+    if (lane + kWave * q < KV) {
+      float wf[EPW][8];
+#pragma unroll
+      for (int e = 0; e < EPW; ++e) unpack_bf16x8(wv4[q][e], wf[e]);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        float xf[8];
+        unpack_bf16x8(xv[q][t], xf);
+#pragma unroll
+        for (int e = 0; e < EPW; ++e)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[t][e][q & 3] = __builtin_fmaf(xf[i], wf[e][i], acc[t][e][q & 3]);
+      }
+    }
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) {
+      float v = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v = v + tree_sum_lane0(acc[t][e][j]);
+      if (lane == 0 && t0 + t < T && e0 + e < E) {
+        if (bias != nullptr) v = v + bf16_to_f32(bias[e0 + e]);
+        const size_t o = static_cast<size_t>(t0 + t) * E + e0 + e;
+        if constexpr (F32) reinterpret_cast<float*>(logits)[o] = v;
+        else reinterpret_cast<uint16_t*>(logits)[o] = f32_to_bf16(v);
+      }
+    }
+  }
+}
+
 // Logits of 8 tokens x 8 experts per work-group with the same tree, for
 // many tokens.  Wave j is the reference's wave j: lane l chains fmaf over
 // the chunks tau = l + 64 j, tau + 256, ... of all 64 (token, expert) pairs
@@ -801,12 +932,32 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* idx, 
   build_plan<kPlanThreads>([&](int s) { return idx[s]; }, T, k, E, p);
 }
 
+constexpr int kNormFusedMaxT = 4;  // tokens up to which the residual RMSNorm runs inside the router
+
 template <bool F32>
-void launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t) {
+hipError_t launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t) {
   // tokens per wave x experts per wave: more waves for few tokens (latency),
   // more reuse of each loaded row for many.  Up to H = 3072 the decode
   // shapes load every chunk up front.
   const bool upfront = (a.H >> 3) <= kWave * 6;
+  if (a.norm_w != nullptr) {
+    if (a.T <= kNormFusedMaxT && upfront) {
+      // the norm fused into the router: each token's row is in registers.
+      // Every wave recomputes its token's norm, which beats a launch of its
+      // own only for a few tokens (measured: 1.5 us saved at 1 token, lost
+      // from 8).
+      gx_launch(logits_norm_kernel<1, 1, F32>, dim3((a.E + 3) / 4, a.T), dim3(kRouteThreads), 0, s, t, a.x, a.delta,
+                a.norm_w, a.eps, a.W, a.b, a.T, a.E, a.H, a.logits, a.normed, a.sum_out);
+      return hipGetLastError();
+    }
+    // more tokens: the norm first (its own launch), then the router on normed
+    const hipError_t e = launch_residual_rmsnorm(a.x, a.delta, a.norm_w, a.normed, a.sum_out, a.T, a.H, a.eps, s);
+    if (e != hipSuccess) return e;
+    RouteArgs b = a;
+    b.x = a.normed;
+    b.norm_w = nullptr;
+    return launch_logits<F32>(b, s, t);
+  }
   if (a.T <= 8 && upfront) {
     gx_launch(logits_kernel<1, 1, 6, F32>, dim3((a.E + 3) / 4, a.T), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b,
               a.T, a.E, a.H, a.logits);
@@ -820,6 +971,7 @@ void launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t) {
     gx_launch(logits_lds_kernel<F32>, dim3((a.E + kLdsEPW - 1) / kLdsEPW, (a.T + kLdsTT - 1) / kLdsTT),
               dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b, a.T, a.E, a.H, a.logits);
   }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -860,9 +1012,7 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
   const bool plan = a.plan.counts != nullptr;
   const bool fused = plan && a.T <= kTopkPlanMaxT;
   const KernelTimer first{a.timer.start, nullptr}, last{nullptr, a.timer.stop};
-  if (a.logits_fp32) launch_logits<true>(a, s, first);
-  else launch_logits<false>(a, s, first);
-  hipError_t err = hipGetLastError();
+  hipError_t err = a.logits_fp32 ? launch_logits<true>(a, s, first) : launch_logits<false>(a, s, first);
   if (err != hipSuccess) return err;
   if (fused && a.T <= kSmallTopkMaxT) {
     const void* lg = a.logits;

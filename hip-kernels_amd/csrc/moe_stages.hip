@@ -175,6 +175,61 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     out[static_cast<size_t>(t) * H + h] = f32_to_bf16((bf16_to_f32(xr[h]) * inv) * bf16_to_f32(w[h]));
 }
 
+// Fused residual + RMSNorm (rmsnorm.cu:224-337): s = r + d in fp32 (kept
+// per chunk: a thread's chunks are kv = tid, tid + 256), sum_out = bf16(s),
+// the sum of squares of s with the same tree as rmsnorm_kernel, then
+// normed = bf16((s * inv) * w).
+__global__ __launch_bounds__(256) void residual_rmsnorm_kernel(const uint16_t* __restrict__ r,
+                                                               const uint16_t* __restrict__ d,
+                                                               const uint16_t* __restrict__ w,
+                                                               uint16_t* __restrict__ normed,
+                                                               uint16_t* __restrict__ sum_out, int H, float eps) {
+  __shared__ float s_w[4];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
+  const size_t row = static_cast<size_t>(t) * H;
+  const int KV = H >> 3;
+  auto sum8 = [&](int kv, float (&s8)[8]) __attribute__((always_inline)) {
+    const uint4 a = reinterpret_cast<const uint4*>(r + row)[kv];
+    const uint4 b = reinterpret_cast<const uint4*>(d + row)[kv];
+    const uint32_t da[4] = {a.x, a.y, a.z, a.w}, db[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s8[2 * i] = __uint_as_float(da[i] << 16) + __uint_as_float(db[i] << 16);
+      s8[2 * i + 1] = __uint_as_float(da[i] & 0xffff0000u) + __uint_as_float(db[i] & 0xffff0000u);
+    }
+  };
+  float acc = 0.0f;
+  for (int kv = tid; kv < KV; kv += 256) {
+    float s8[8];
+    sum8(kv, s8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = __builtin_fmaf(s8[i], s8[i], acc);
+    if (sum_out) {
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = f32_to_bf16(s8[2 * i]) | (static_cast<uint32_t>(f32_to_bf16(s8[2 * i + 1])) << 16);
+      reinterpret_cast<uint4*>(sum_out + row)[kv] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+  for (int kk = KV * 8 + tid; kk < H; kk += 256) {
+    const float v = bf16_to_f32(r[row + kk]) + bf16_to_f32(d[row + kk]);
+    acc = __builtin_fmaf(v, v, acc);
+    if (sum_out) sum_out[row + kk] = f32_to_bf16(v);
+  }
+  acc = wave_butterfly_sum(acc);
+  if (lane == 0) s_w[warp] = acc;
+  __syncthreads();
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss = ss + s_w[i];
+  const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(H) + eps);
+  for (int h = tid; h < H; h += 256) {
+    const float v = bf16_to_f32(r[row + h]) + bf16_to_f32(d[row + h]);
+    normed[row + h] = f32_to_bf16((v * inv) * bf16_to_f32(w[h]));
+  }
+}
+
 int grid_for(size_t total, int threads) {
   size_t b = (total + threads - 1) / threads;
   if (b > 4096) b = 4096;
@@ -220,6 +275,13 @@ hipError_t launch_dequant(const uint8_t* wn, const uint8_t* ws, int N, int K, ui
   const TiledGeom g = tiled_geom(N, K);
   hipLaunchKernelGGL(dequant_kernel, dim3(grid_for(static_cast<size_t>(N) * g.nb, 256)), dim3(256), 0, s, wn, ws, g,
                      out);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual_rmsnorm(const uint16_t* r, const uint16_t* d, const uint16_t* w, uint16_t* normed,
+                                   uint16_t* sum_out, int T, int H, float eps, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(T), dim3(256), 0, s, r, d, w, normed, sum_out, H, eps);
   return hipGetLastError();
 }
 

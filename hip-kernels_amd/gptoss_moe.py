@@ -86,6 +86,7 @@ _sig("gptoss_moe_layer_create", [], _P)
 _sig("gptoss_moe_layer_init", [_P, ctypes.POINTER(MoeConfig), _I, ctypes.POINTER(MoeWeights)])
 _sig("gptoss_moe_layer_forward", [_P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_prenormed", [_P, _P, _P, _P, _I, _P])
+_sig("gptoss_moe_layer_forward_residual", [_P, _P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_routed", [_P, _P, _P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_get_ffn_norm_weight", [_P], _P)
 _sig("gptoss_moe_layer_destroy", [_P], None)
@@ -101,6 +102,7 @@ _sig("gptoss_moe_permute_plan", [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P])
 _sig("gptoss_moe_scatter_tokens", [_P, _P, _P, _I, _I, _I, _P])
 _sig("gptoss_mxfp4_gemv_forward", [_P, _I, _P, _P, _P, _P, _I, _I, _P])
 _sig("gptoss_swiglu_forward", [_P, _P, _I, _I, _F, _F, _P])
+_sig("gptoss_fused_residual_rmsnorm_forward", [_P, _P, _P, _P, _P, _I, _I, _F, _P])
 _sig("gptoss_moe_combine_forward", [_P, _P, _P, _P, _P, _I, _I, _I, _P])
 _sig("gptoss_mxfp4_dequant", [_P, _P, _I, _I, _P, _P])
 _sig("gptoss_moe_grouped_mxfp4_gemm", [_P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _F, _F, _P, _P, _P])
@@ -234,6 +236,17 @@ class MoELayer:
             out = torch.empty_like(normed)
         check(_lib.gptoss_moe_layer_forward_prenormed(self._h, _ptr(normed), _ptr(residual), _ptr(out), T,
                                                       _stream(stream)))
+        return out
+
+    def forward_residual(self, residual, delta, residual_out=None, out=None, stream=None):
+        """The decode step's residual add + RMSNorm + MoE in one call:
+        s = residual + delta; residual_out (optional) = bf16(s);
+        out = bf16(s) + MoE(RMSNorm(s)).  Returns out."""
+        T = residual.shape[0]
+        if out is None:
+            out = torch.empty_like(residual)
+        check(_lib.gptoss_moe_layer_forward_residual(self._h, _ptr(residual), _ptr(delta), _ptr(residual_out),
+                                                     _ptr(out), T, _stream(stream)))
         return out
 
     def forward_routed(self, normed, expert_indices, expert_weights, residual=None, out=None, stream=None):
@@ -373,6 +386,18 @@ def swiglu(gate_up, alpha: float = 1.702, limit: float = 7.0, stream=None):
     out = torch.empty((T, N2 // 2), dtype=gate_up.dtype, device=gate_up.device)
     check(_lib.gptoss_swiglu_forward(_ptr(gate_up), _ptr(out), T, N2 // 2, alpha, limit, _stream(stream)))
     return out
+
+
+def fused_residual_rmsnorm(residual, delta, weight, eps: float = 1e-5, normed=None, sum_out=None, stream=None):
+    """fused_residual_rmsnorm_forward: returns (normed, sum_out)."""
+    T, H = residual.shape
+    if normed is None:
+        normed = torch.empty_like(residual)
+    if sum_out is None:
+        sum_out = torch.empty_like(residual)
+    check(_lib.gptoss_fused_residual_rmsnorm_forward(_ptr(residual), _ptr(delta), _ptr(weight), _ptr(normed),
+                                                     _ptr(sum_out), T, H, eps, _stream(stream)))
+    return normed, sum_out
 
 
 def combine(expert_out, gather_map, weights, residual, T: int, H: int, top_k: int, stream=None):

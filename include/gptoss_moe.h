@@ -112,6 +112,17 @@ int gptoss_moe_layer_init(gptoss_moe_layer* layer, const gptoss_moe_config* cfg,
 /* out = input + MoE(RMSNorm(input))  (moe_layer_forward, moe_layer.cu:982-1005) */
 int gptoss_moe_layer_forward(gptoss_moe_layer* layer, const uint16_t* input, uint16_t* output,
                              int num_tokens, void* stream);
+/* The decode step's residual add + RMSNorm and the MoE in one call: it
+ * replaces fused_residual_rmsnorm_forward(residual, delta, moe_norm_weight,
+ * normed, sum) followed by moe_layer_forward_prenormed(normed, sum, out)
+ * (transformer.cu:696-715, rmsnorm.cu:224-337).  sum = residual + delta is
+ * formed in fp32; residual_out (may be NULL) receives bf16(sum); out =
+ * bf16(sum) + MoE(RMSNorm(sum)).  Up to 4 tokens the norm runs inside the
+ * router's launch (one launch fewer), above in a launch of its own.  Needs
+ * moe_norm_weight. */
+int gptoss_moe_layer_forward_residual(gptoss_moe_layer* layer, const uint16_t* residual,
+                                      const uint16_t* delta, uint16_t* residual_out, uint16_t* output,
+                                      int num_tokens, void* stream);
 /* out = residual + MoE(normed)  (moe_layer_forward_prenormed, moe_layer.cu:960-980);
  * residual may be NULL (out = MoE(normed)). */
 int gptoss_moe_layer_forward_prenormed(gptoss_moe_layer* layer, const uint16_t* normed,
@@ -203,6 +214,15 @@ int gptoss_moe_scatter_tokens(const uint16_t* x, const int32_t* gather_map, uint
 int gptoss_mxfp4_gemv_forward(const uint16_t* x, int M, const uint8_t* tiled_nibbles,
                               const uint8_t* tiled_scales, const uint16_t* bias, uint16_t* y,
                               int N, int K, void* stream);
+
+/* fused_residual_rmsnorm_forward (rmsnorm.cu:224-337): s = residual + delta
+ * (fp32), sum_out = bf16(s) (may be NULL), normed = bf16((s * inv) * weight)
+ * with inv = 1/sqrt(mean(s^2) + eps); the sum of squares follows the
+ * router's gemv_bf16 tree and sqrt / divide are IEEE (the reference uses
+ * rsqrtf). */
+int gptoss_fused_residual_rmsnorm_forward(const uint16_t* residual, const uint16_t* delta,
+                                          const uint16_t* weight, uint16_t* normed, uint16_t* sum_out,
+                                          int num_tokens, int hidden, float eps, void* stream);
 
 /* swiglu_forward (swiglu.cu:178-211): interleaved [T][2I] -> [T][I]. */
 int gptoss_swiglu_forward(const uint16_t* gate_up, uint16_t* out, int num_tokens,

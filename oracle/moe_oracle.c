@@ -391,6 +391,39 @@ void orc_rmsnorm(const uint16_t* x, const uint16_t* w, int T, int H, float eps,
   }
 }
 
+/* fused_residual_rmsnorm_forward (rmsnorm.cu:224-337): s = r + d in fp32,   */
+/* sum_out = bf16(s); the sum of squares of the fp32 s with the gemv tree     */
+/* (the order of orc_rmsnorm); inv = 1/sqrt(mean + eps) (IEEE);               */
+/* normed = bf16((s * inv) * w).  With d = 0 this is orc_rmsnorm of r.        */
+void orc_residual_rmsnorm(const uint16_t* r, const uint16_t* d, const uint16_t* w, int T, int H, float eps,
+                          uint16_t* normed, uint16_t* sum_out) {
+  float* s = (float*)malloc(sizeof(float) * (size_t)H);
+  const int KV = H >> 3;
+  for (int t = 0; t < T; ++t) {
+    const size_t o = (size_t)t * H;
+    for (int h = 0; h < H; ++h) {
+      s[h] = bf(r[o + h]) + bf(d[o + h]);
+      if (sum_out) sum_out[o + h] = orc_f32_to_bf16(s[h]);
+    }
+    float part[256];
+    for (int tid = 0; tid < 256; ++tid) {
+      float acc = 0.0f;
+      for (int kv = tid; kv < KV; kv += 256)
+        for (int i = 0; i < 8; ++i) {
+          const float v = s[(kv << 3) + i];
+          acc = fmaf(v, v, acc);
+        }
+      for (int k = (KV << 3) + tid; k < H; k += 256) acc = fmaf(s[k], s[k], acc);
+      part[tid] = acc;
+    }
+    float ss = 0.0f;
+    for (int wv = 0; wv < 4; ++wv) ss = ss + butterfly64(part + 64 * wv);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int h = 0; h < H; ++h) normed[o + h] = orc_f32_to_bf16((s[h] * inv) * bf(w[h]));
+  }
+  free(s);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Whole layer, multi-threaded over permuted slots.                          */
 /* ------------------------------------------------------------------------ */

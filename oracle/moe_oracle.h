@@ -147,6 +147,10 @@ void orc_moe_forward_routed(const orc_cfg* cfg, const orc_weights* wt,
 /* RMSNorm (rmsnorm.cu:47-83 semantics with an IEEE 1/sqrt): out = bf16(x*inv*w) */
 void orc_rmsnorm(const uint16_t* x, const uint16_t* w, int T, int H, float eps,
                  uint16_t* out);
+/* fused_residual_rmsnorm_forward: s = r + d (fp32), sum_out = bf16(s) (may be
+ * NULL), normed = bf16((s * inv) * w) with inv from the gemv-tree sum of s^2. */
+void orc_residual_rmsnorm(const uint16_t* r, const uint16_t* d, const uint16_t* w, int T, int H, float eps,
+                          uint16_t* normed, uint16_t* sum_out);
 
 #ifdef __cplusplus
 }

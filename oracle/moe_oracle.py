@@ -79,6 +79,7 @@ def lib():
                                              _P, _P, _P, ctypes.POINTER(OrcTrace), _I]
         L.orc_moe_forward_routed.restype = None
         L.orc_rmsnorm.argtypes = [_P, _P, _I, _I, _F, _P]
+        L.orc_residual_rmsnorm.argtypes = [_P, _P, _P, _I, _I, _F, _P, _P]
         _lib = L
     return _lib
 
@@ -182,6 +183,15 @@ def rmsnorm(x, w, eps=1e-5):
     out = np.empty((T, H), np.uint16)
     lib().orc_rmsnorm(_ptr(x), _ptr(w), T, H, eps, _ptr(out))
     return out
+
+
+def residual_rmsnorm(r, d, w, eps=1e-5):
+    """fused_residual_rmsnorm_forward: returns (normed, sum_out) bf16 bits."""
+    T, H = r.shape
+    normed = np.empty((T, H), np.uint16)
+    sum_out = np.empty((T, H), np.uint16)
+    lib().orc_residual_rmsnorm(_ptr(r), _ptr(d), _ptr(w), T, H, eps, _ptr(normed), _ptr(sum_out))
+    return normed, sum_out
 
 
 def set_exp_mode(mode: int) -> None:

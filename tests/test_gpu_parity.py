@@ -314,6 +314,51 @@ def test_layer_forward_with_rmsnorm(gpu, orc, torch_mod):
     assert_bf16_parity(out, ref, "forward (rmsnorm + moe)")
 
 
+@pytest.mark.parametrize("T,H", [(1, 2880), (37, 192), (300, 4104)])
+def test_fused_residual_rmsnorm_stage(gpu, orc, torch_mod, T, H):
+    """fused_residual_rmsnorm_forward: normed and the bf16 sum bit-exact."""
+    torch = torch_mod
+    rng = np.random.default_rng(T + H)
+    r = moe_data.bf16(rng.normal(0, 1, (T, H)))
+    d = moe_data.bf16(rng.normal(0, 0.5, (T, H)))
+    w = moe_data.bf16(rng.normal(1, 0.1, H))
+    say("residual rmsnorm", T, H)
+    normed, s = gpu.fused_residual_rmsnorm(dev(r, torch), dev(d, torch), dev(w, torch), 1e-5)
+    rn, rs = orc.residual_rmsnorm(r, d, w, 1e-5)
+    assert np.array_equal(host(normed), rn)
+    assert np.array_equal(host(s), rs)
+
+
+@pytest.mark.parametrize("T,E,H,I", [(1, 16, 192, 128), (4, 16, 192, 128), (5, 16, 192, 128), (8, 16, 192, 128),
+                                     (9, 16, 192, 128), (64, 16, 192, 128), (100, 16, 192, 128),
+                                     (2, 32, 2880, 2880), (8, 32, 2880, 2880), (64, 32, 2880, 2880)])
+def test_layer_forward_residual(gpu, orc, torch_mod, T, E, H, I):
+    """forward_residual = fused_residual_rmsnorm_forward + forward_prenormed:
+    the new residual bit-exact, the router's logits bit-exact (the norm
+    inside the router's launch up to 4 tokens, its own launch above), the
+    layer output through the exact decode path bit-exact."""
+    torch = torch_mod
+    k = 4
+    w = moe_data.make_layer(60 + T, E, H, I)
+    res, delta = moe_data.make_tokens(60 + T, T, H)
+    norm_w = moe_data.bf16(np.random.default_rng(60 + T).normal(1.0, 0.1, H))
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=128, norm_w=norm_w)
+    say("forward_residual", T, E, H)
+    res_out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    out = host(L.layer.forward_residual(dev(res, torch), dev(delta, torch), residual_out=res_out))
+    torch.cuda.synchronize()
+    rn, rs = orc.residual_rmsnorm(res, delta, norm_w)
+    assert np.array_equal(host(res_out), rs)
+    tr = L.layer.trace()
+    logits = gpu.copy_device_to_tensor(tr.logits, T * E * 2).cpu().numpy().view(np.uint16).reshape(T, E)
+    assert np.array_equal(logits, orc.router(rn, w["router_w"], w["router_b"], logits_fp32=False))
+    ref = orc.moe_forward(w, rn, rs, E, k, H, I)
+    assert_bf16_parity(out, ref, f"forward_residual T={T} E={E}")
+    # without residual_out the sum stays in the layer's scratch; same output
+    out2 = host(L.layer.forward_residual(dev(res, torch), dev(delta, torch)))
+    assert np.array_equal(out2, out)
+
+
 def test_layer_edge_cases(gpu, orc, torch_mod):
     torch = torch_mod
     E, k, H, I = 8, 8, 64, 64

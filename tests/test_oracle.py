@@ -156,6 +156,57 @@ def test_router_vs_fp64(orc):
     assert not np.allclose(lf[:, :16], (xd @ Wd.T)[:, :16][::-1], atol=1e-3)
 
 
+def _norm_fp64(s64, w64, eps):
+    inv = 1.0 / np.sqrt(np.mean(s64 * s64, axis=1, keepdims=True) + eps)
+    return s64 * inv * w64
+
+
+def _within_one_bf16_ulp(got_bits, exact, orc):
+    got = orc.bf16_to_f32(got_bits).astype(np.float64)
+    # one bf16 ulp of the exact value (8 significant bits), floor for tiny values
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact), 2.0 ** -120))) - 7)
+    return np.all(np.abs(got - exact) <= ulp)
+
+
+def test_rmsnorm_vs_fp64(orc):
+    """rmsnorm.cu:47-83: out = x / sqrt(mean(x^2) + eps) * w.  fp32 with the
+    gemv tree is within one bf16 ulp of the fp64 value; a dropped eps, a sum
+    instead of a mean or a missing weight fails."""
+    T, H, eps = 6, 2880, 1e-5
+    rng = np.random.default_rng(31)
+    x = moe_data.bf16(rng.normal(0, 1, (T, H)))
+    x[5] = moe_data.bf16(rng.normal(0, 1e-3, H))  # small row: eps matters at 1e-5 relative
+    w = moe_data.bf16(rng.normal(1, 0.1, H))
+    out = orc.rmsnorm(x, w, eps)
+    exact = _norm_fp64(orc.bf16_to_f32(x).astype(np.float64), orc.bf16_to_f32(w).astype(np.float64), eps)
+    assert _within_one_bf16_ulp(out, exact, orc)
+    assert not _within_one_bf16_ulp(out, _norm_fp64(orc.bf16_to_f32(x).astype(np.float64),
+                                                   orc.bf16_to_f32(w).astype(np.float64), 1e-2), orc)
+
+
+def test_residual_rmsnorm(orc):
+    """fused_residual_rmsnorm_forward (rmsnorm.cu:224-337): sum_out = bf16(r + d)
+    (fp32 add), normed from the fp32 sum.  With d = 0 it is rmsnorm of r bit
+    for bit; otherwise within one bf16 ulp of fp64; symmetric in r and d."""
+    T, H, eps = 5, 2880, 1e-5
+    rng = np.random.default_rng(32)
+    r = moe_data.bf16(rng.normal(0, 1, (T, H)))
+    d = moe_data.bf16(rng.normal(0, 0.5, (T, H)))
+    w = moe_data.bf16(rng.normal(1, 0.1, H))
+    normed, sum_out = orc.residual_rmsnorm(r, d, w, eps)
+    s32 = orc.bf16_to_f32(r) + orc.bf16_to_f32(d)  # fp32 sum, as the kernel
+    ref_sum = torch.from_numpy(s32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(sum_out, ref_sum)
+    s64 = orc.bf16_to_f32(r).astype(np.float64) + orc.bf16_to_f32(d).astype(np.float64)
+    assert _within_one_bf16_ulp(normed, _norm_fp64(s64, orc.bf16_to_f32(w).astype(np.float64), eps), orc)
+    n2, s2 = orc.residual_rmsnorm(d, r, w, eps)
+    assert np.array_equal(n2, normed) and np.array_equal(s2, sum_out)
+    z = np.zeros_like(r)
+    n0, s0 = orc.residual_rmsnorm(r, z, w, eps)
+    assert np.array_equal(n0, orc.rmsnorm(r, w, eps))
+    assert np.array_equal(s0, r)
+
+
 def test_router_tree_cancellation(orc):
     """Only the gemv_bf16_kernel tree gives 1.0 here: thread 0 holds 1,
     thread 1 holds 2^24, thread 16 holds -2^24.  The xor-16 butterfly step adds
