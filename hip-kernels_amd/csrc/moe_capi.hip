@@ -17,25 +17,49 @@
 #include "../../include/gptoss_moe.h"
 #include "moe_kernels.h"
 #include "moe_stages.h"
+#include "moe_status.h"
+#include "moe_checkpoint.h"
 
 using namespace gxmoe;
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
 
-int fail(int code, const char* fmt, ...) {
+namespace gxmoe {
+
+int vset_error(int code, const char* fmt, va_list ap) {
   char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
   vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
   g_last_error = buf;
   return code;
 }
 
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vset_error(code, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+}  // namespace gxmoe
+
+namespace {
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vset_error(code, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
 int ok() {
-  g_last_error.clear();
+  clear_error();
   return GPTOSS_OK;
 }
 
@@ -338,6 +362,39 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
     return hip_fail(err, "layer init");
   }
   L->initialized = true;
+  return ok();
+}
+
+// One allocation with every weight of the layer (the checkpoint reader
+// fills it and tiles the experts), then the borrowed-tiled init over it; the
+// layer takes the allocation over.
+int gptoss_moe_layer_init_from_checkpoint(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
+                                          const gptoss_checkpoint* ckpt, int layer_index) {
+  if (L == nullptr || cfg == nullptr || ckpt == nullptr) return fail(GPTOSS_ERR_INVALID, "null argument");
+  if (L->initialized) return fail(GPTOSS_ERR_STATE, "layer already initialised");
+  const int H = cfg->hidden_size, E = cfg->num_experts, I = cfg->intermediate_size;
+  if (E < 1 || E > kMaxExperts) return fail(GPTOSS_ERR_UNSUPPORTED, "num_experts=%d outside [1, %d]", E, kMaxExperts);
+  int rc = check_mxfp4_shape(2 * I, H);
+  if (rc != GPTOSS_OK) return rc;
+  if ((rc = check_mxfp4_shape(H, I)) != GPTOSS_OK) return rc;
+  // names, shapes and dtypes first, on the host
+  LayerSource* src = nullptr;
+  if ((rc = ckpt_resolve_layer(ckpt, *cfg, layer_index, &src)) != GPTOSS_OK) return rc;
+  ScopedDevice sd(device_id);
+  if (sd.err != hipSuccess) {
+    ckpt_free_source(src);
+    return hip_fail(sd.err, "hipSetDevice");
+  }
+  void* blob = nullptr;
+  gptoss_moe_weights wt{};
+  rc = ckpt_upload_layer(src, &blob, &wt);
+  ckpt_free_source(src);
+  if (rc != GPTOSS_OK) return rc;
+  if ((rc = gptoss_moe_layer_init(L, cfg, device_id, &wt)) != GPTOSS_OK) {
+    (void)hipFree(blob);
+    return rc;
+  }
+  L->owned.push_back(blob);
   return ok();
 }
 

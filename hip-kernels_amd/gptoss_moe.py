@@ -36,6 +36,8 @@ GPTOSS_ERR_UNSUPPORTED = 2
 GPTOSS_ERR_HIP = 3
 GPTOSS_ERR_STATE = 4
 GPTOSS_ERR_OOM = 5
+GPTOSS_ERR_NOT_FOUND = 6
+GPTOSS_ERR_IO = 7
 
 
 class GptossError(RuntimeError):
@@ -70,6 +72,11 @@ class MoeTrace(ctypes.Structure):
                 ("n_active", _P), ("gate_up", _P), ("act", _P), ("expert_out", _P)]
 
 
+class TensorInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_char_p), ("ndim", _I),
+                ("shape", ctypes.c_int64 * 8), ("nbytes", ctypes.c_uint64), ("data", _P), ("shard", _I)]
+
+
 def _sig(name, args, res=_I):
     f = getattr(_lib, name)
     f.argtypes = args
@@ -90,6 +97,13 @@ _sig("gptoss_moe_layer_forward_residual", [_P, _P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_routed", [_P, _P, _P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_get_ffn_norm_weight", [_P], _P)
 _sig("gptoss_moe_layer_destroy", [_P], None)
+_sig("gptoss_moe_layer_init_from_checkpoint", [_P, ctypes.POINTER(MoeConfig), _I, _P, _I])
+_sig("gptoss_checkpoint_open", [ctypes.c_char_p, ctypes.POINTER(_P)])
+_sig("gptoss_checkpoint_close", [_P], None)
+_sig("gptoss_checkpoint_num_tensors", [_P])
+_sig("gptoss_checkpoint_tensor_at", [_P, _I, ctypes.POINTER(TensorInfo)])
+_sig("gptoss_checkpoint_find", [_P, ctypes.c_char_p, ctypes.POINTER(TensorInfo)])
+_sig("gptoss_checkpoint_set_staging_bytes", [_P, _SZ])
 _sig("gptoss_moe_layer_trace", [_P, ctypes.POINTER(MoeTrace)])
 _sig("gptoss_moe_layer_set_trace_gate_up", [_P, _I])
 _sig("gptoss_moe_layer_set_profiling", [_P, _I])
@@ -221,6 +235,16 @@ class MoELayer:
         self.cfg = cfg
         return self
 
+    def init_from_checkpoint(self, cfg: MoeConfig, device_id: int, ckpt: "Checkpoint",
+                             layer_index: int) -> "MoELayer":
+        """Layer `layer_index` of a safetensors checkpoint (WeightLoader's MoE
+        part, weight_loader.cu:1083-1165): the layer owns one device
+        allocation with every weight, the experts already tiled."""
+        check(_lib.gptoss_moe_layer_init_from_checkpoint(self._h, ctypes.byref(cfg), device_id, ckpt._h,
+                                                         layer_index))
+        self.cfg = cfg
+        return self
+
     def forward(self, x, out=None, stream=None):
         """out = x + MoE(RMSNorm(x)) (moe_layer_forward)."""
         T = x.shape[0]
@@ -289,6 +313,78 @@ class MoELayer:
     def __del__(self):
         try:
             self.destroy()
+        except Exception:
+            pass
+
+
+class Checkpoint:
+    """A safetensors checkpoint (a directory of shards or one file), mapped
+    read-only: WeightLoader's shard scan, header parse and name index
+    (weight_loader.cu:297-345, 456-575).  Host-only: opening and reading
+    tensors needs no GPU."""
+
+    _NP = {"BF16": "<u2", "F16": "<f2", "F32": "<f4", "F64": "<f8", "U8": "u1", "I8": "i1", "BOOL": "u1",
+           "I16": "<i2", "U16": "<u2", "I32": "<i4", "U32": "<u4", "I64": "<i8", "U64": "<u8"}
+
+    def __init__(self, path: str):
+        h = _P()
+        check(_lib.gptoss_checkpoint_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h.value
+
+    def __len__(self) -> int:
+        return _lib.gptoss_checkpoint_num_tensors(self._h)
+
+    @staticmethod
+    def _info(ti: TensorInfo) -> dict:
+        return {"name": ti.name.decode(), "dtype": ti.dtype.decode(), "shape": tuple(ti.shape[:ti.ndim]),
+                "nbytes": ti.nbytes, "data": ti.data or 0, "shard": ti.shard}
+
+    def names(self):
+        out = []
+        ti = TensorInfo()
+        for i in range(len(self)):
+            check(_lib.gptoss_checkpoint_tensor_at(self._h, i, ctypes.byref(ti)))
+            out.append(ti.name.decode())
+        return out
+
+    def info(self, name: str):
+        """dict(name, dtype, shape, nbytes, data, shard), or None when absent."""
+        ti = TensorInfo()
+        rc = _lib.gptoss_checkpoint_find(self._h, name.encode(), ctypes.byref(ti))
+        if rc == GPTOSS_ERR_NOT_FOUND:
+            return None
+        check(rc)
+        return self._info(ti)
+
+    def numpy(self, name: str):
+        """A copy of the tensor as a numpy array (bf16 as uint16; dtypes
+        outside the safetensors list as flat bytes)."""
+        import numpy as np
+        inf = self.info(name)
+        if inf is None:
+            raise KeyError(name)
+        raw = ctypes.string_at(inf["data"], inf["nbytes"]) if inf["nbytes"] else b""
+        dt = self._NP.get(inf["dtype"])
+        a = np.frombuffer(raw, dtype=dt or "u1")
+        return (a.reshape(inf["shape"]) if dt else a).copy()
+
+    def set_staging_bytes(self, nbytes: int) -> None:
+        check(_lib.gptoss_checkpoint_set_staging_bytes(self._h, nbytes))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.gptoss_checkpoint_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
 

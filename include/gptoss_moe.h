@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GPTOSS_MOE_ABI_VERSION 3
+#define GPTOSS_MOE_ABI_VERSION 4
 
 enum {
   GPTOSS_OK = 0,
@@ -33,7 +33,9 @@ enum {
   GPTOSS_ERR_UNSUPPORTED = 2,  /* valid but not supported by this build (shape limits) */
   GPTOSS_ERR_HIP = 3,          /* a HIP runtime call failed */
   GPTOSS_ERR_STATE = 4,        /* object not initialised / already initialised */
-  GPTOSS_ERR_OOM = 5           /* device allocation failed */
+  GPTOSS_ERR_OOM = 5,          /* device allocation failed */
+  GPTOSS_ERR_NOT_FOUND = 6,    /* checkpoint tensor or shard file not found */
+  GPTOSS_ERR_IO = 7            /* checkpoint file unreadable or not valid safetensors */
 };
 
 /* Message of the last failing call on this thread ("" if none). */
@@ -140,6 +142,50 @@ int gptoss_moe_layer_forward_routed(gptoss_moe_layer* layer, const uint16_t* nor
                                     void* stream);
 const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* layer);
 void gptoss_moe_layer_destroy(gptoss_moe_layer* layer);           /* moe_layer_destroy */
+
+/* ---- Checkpoints (src/memory/weight_loader.cu) ---------------------------
+ * A safetensors checkpoint: every `*.safetensors` file of a directory in
+ * name order (weight_loader.cu:456-482), or one file, mapped read-only
+ * (:488-537).  The index maps names to tensors; a name present in several
+ * shards resolves to the last shard in name order (:543-551). */
+typedef struct gptoss_checkpoint gptoss_checkpoint;
+
+typedef struct gptoss_tensor_info {
+  const char* name;   /* valid while the checkpoint is open */
+  const char* dtype;  /* as in the header: "BF16", "F32", "U8", ... */
+  int ndim;           /* at most 8 */
+  int64_t shape[8];
+  uint64_t nbytes;    /* data_offsets end - begin */
+  const void* data;   /* host address inside the read-only mapping */
+  int shard;          /* shard index in name order */
+} gptoss_tensor_info;
+
+/* WeightLoader::init's shard scan, mmap and header parse
+ * (weight_loader.cu:297-345, 456-540).  Malformed files return
+ * GPTOSS_ERR_IO instead of aborting. */
+int gptoss_checkpoint_open(const char* path, gptoss_checkpoint** out);
+void gptoss_checkpoint_close(gptoss_checkpoint* ckpt);              /* WeightLoader::destroy */
+int gptoss_checkpoint_num_tensors(const gptoss_checkpoint* ckpt);
+int gptoss_checkpoint_tensor_at(const gptoss_checkpoint* ckpt, int i, gptoss_tensor_info* info);
+/* has_tensor / get_tensor_data (weight_loader.cu:556-575): GPTOSS_ERR_NOT_FOUND
+ * when absent. */
+int gptoss_checkpoint_find(const gptoss_checkpoint* ckpt, const char* name, gptoss_tensor_info* info);
+/* Size of each of the two pinned host and two device staging slots that
+ * gptoss_moe_layer_init_from_checkpoint streams experts through (default
+ * 64 MiB; a slot always holds at least one expert matrix). */
+int gptoss_checkpoint_set_staging_bytes(gptoss_checkpoint* ckpt, size_t bytes);
+
+/* One MoE layer from a checkpoint: WeightLoader::load_layer_weights' MoE part
+ * (weight_loader.cu:1083-1165) with load_packed_experts (:818-842) or
+ * load_per_expert_weights (:847-895), then moe_layer_init.  Names under
+ * "model.layers.<layer_index>.": mlp.gate|router.{weight,bias},
+ * post_attention_layernorm.weight, mlp.experts.{gate_up,down}_proj_{blocks,
+ * scales,bias} or mlp.experts.<e>.{mlp1|gate_up_proj|w1, mlp2|down_proj|w2}
+ * .weight[_scale].  bf16 tensors stored as F32 or F16 are rounded to bf16
+ * (nearest even).  The layer owns one device allocation holding every
+ * weight, the experts already tiled; shapes are checked against cfg. */
+int gptoss_moe_layer_init_from_checkpoint(gptoss_moe_layer* layer, const gptoss_moe_config* cfg,
+                                          int device_id, const gptoss_checkpoint* ckpt, int layer_index);
 
 /* Device views of the layer's scratch after the last forward on `stream`
  * (valid until the next forward): routing and per-slot intermediates in the
