@@ -325,6 +325,61 @@ def bench_residual(g, torch, wc, T: int, steps: int = 64):
                 saved_us=us["two_calls"] - us["fused"])
 
 
+def bench_checkpoint_load(g, torch, n_experts: int = 32, reps: int = 3):
+    """One GPT-OSS-20B-shaped MoE layer (E=32, H=I=2880; random MXFP4) written
+    as a safetensors file under the Hugging Face export's names, then loaded
+    with init_from_checkpoint: shard mapping, header parse, bf16 tensors,
+    experts streamed through the pinned staging and repacked into the tiled
+    layout, layer init.  The page cache is warm (the file was just written),
+    so this is the host-memory -> HBM rate, not a disk rate.  load_ms is the
+    best later load from the same open checkpoint (a model's layers after the
+    first); first_load_ms also pins the staging.  Beside it: a pageable
+    host -> device copy of the same tensors, one copy per tensor."""
+    import shutil
+    import tempfile
+    from safetensors.torch import save_file
+    gen = torch.Generator()
+    gen.manual_seed(5)
+    Ec, P = n_experts, "model.layers.0."
+    bf = lambda *shape: (0.02 * torch.randn(shape, generator=gen)).to(torch.bfloat16)  # noqa: E731
+    u8 = lambda lo, hi, *shape: torch.randint(lo, hi, shape, generator=gen, dtype=torch.uint8)  # noqa: E731
+    t = {P + "mlp.router.weight": bf(Ec, H), P + "mlp.router.bias": bf(Ec),
+         P + "post_attention_layernorm.weight": bf(H),
+         P + "mlp.experts.gate_up_proj_bias": bf(Ec, 2 * I), P + "mlp.experts.down_proj_bias": bf(Ec, H),
+         P + "mlp.experts.gate_up_proj_blocks": u8(0, 256, Ec, 2 * I, H // 32, 16),
+         P + "mlp.experts.gate_up_proj_scales": u8(119, 124, Ec, 2 * I, H // 32),
+         P + "mlp.experts.down_proj_blocks": u8(0, 256, Ec, H, I // 32, 16),
+         P + "mlp.experts.down_proj_scales": u8(119, 124, Ec, H, I // 32)}
+    nbytes = sum(v.numel() * v.element_size() for v in t.values())
+    d = tempfile.mkdtemp(prefix="gptoss_ckpt_")
+    try:
+        save_file(t, os.path.join(d, "model-00001-of-00001.safetensors"))
+        cfg = g.default_config(Ec, 64)
+        times = []
+        with g.Checkpoint(d) as ck:
+            for _ in range(reps + 1):  # the first load also pins the staging
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                L = g.MoELayer().init_from_checkpoint(cfg, 0, ck, 0)
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                L.destroy()
+        plain = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            on_dev = [v.to("cuda") for v in t.values()]
+            torch.cuda.synchronize()
+            plain.append(time.perf_counter() - t0)
+            del on_dev
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    best, pbest = min(times[1:]), min(plain)
+    return dict(experts=Ec, checkpoint_bytes=nbytes, first_load_ms=times[0] * 1e3, load_ms=best * 1e3,
+                load_gbs=nbytes / best / 1e9, pageable_copy_ms=pbest * 1e3, pageable_copy_gbs=nbytes / pbest / 1e9,
+                reps=reps)
+
+
 def bench_stack(g, torch, layers: int = 36, T: int = 32, steps: int = 256):
     """36 distinct GPT-OSS-120B MoE layers resident (random
     MXFP4 weights, ~61 GB), a decode step at batch 32 = the 36 layer forwards
@@ -465,6 +520,9 @@ def main():
         log("residual add + RMSNorm in front of the MoE (B=1, 4, 64)")
         extra["residual_norm"] = [bench_residual(g, torch, copies[0], T) for T in (1, 4, 64)]
         log(json.dumps(extra["residual_norm"]))
+        log("checkpoint load: one GPT-OSS-20B-shaped layer from safetensors")
+        extra["checkpoint_load"] = bench_checkpoint_load(g, torch)
+        log(json.dumps(extra["checkpoint_load"]))
         del copies
         torch.cuda.empty_cache()
         log(f"{args.stack_layers}-layer stack at batch 32")

@@ -24,6 +24,8 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <memory>
+#include <mutex>
 #include <cerrno>
 #include <cstdint>
 #include <cstring>
@@ -43,7 +45,7 @@ using namespace gxmoe;
 namespace {
 
 constexpr size_t kMaxHeaderBytes = size_t(100) << 20;  // safetensors' own header limit
-constexpr size_t kDefaultStaging = size_t(64) << 20;
+constexpr size_t kDefaultStaging = size_t(32) << 20;
 constexpr int kMaxDims = 8;
 
 struct Shard {
@@ -403,6 +405,42 @@ void prefetch(const uint8_t* p, size_t n) {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Two pinned host slots and two device slots on one device; slot i is free
+// again once its event has completed.  A checkpoint keeps its staging per
+// device between layer loads, so a model load pins host memory once.
+struct Staging {
+  int device = 0;
+  uint8_t* host = nullptr;
+  uint8_t* dev = nullptr;
+  size_t slot = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  bool pending[2] = {false, false};
+  int next = 0;
+
+  hipError_t init(int device_id, size_t bytes) {
+    device = device_id;
+    slot = bytes;
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&host), 2 * slot, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&dev), 2 * slot);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
+    return e;
+  }
+  ~Staging() {
+    int prev = -1;
+    const bool swap = hipGetDevice(&prev) == hipSuccess && prev != device && hipSetDevice(device) == hipSuccess;
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (hipEvent_t x : ev)
+      if (x) (void)hipEventDestroy(x);
+    if (stream) (void)hipStreamDestroy(stream);
+    if (dev) (void)hipFree(dev);
+    if (host) (void)hipHostFree(host);
+    if (swap) (void)hipSetDevice(prev);
+  }
+};
+
+
 }  // namespace
 
 struct gptoss_checkpoint {
@@ -410,8 +448,30 @@ struct gptoss_checkpoint {
   std::vector<Tensor> tensors;
   std::unordered_map<std::string, int> index;
   size_t staging = kDefaultStaging;
+  // staging per device, kept between layer loads; loads from one checkpoint
+  // take the lock, so they run one at a time
+  mutable std::mutex mu;
+  mutable std::vector<std::unique_ptr<Staging>> stagings;
+
+  // The staging of `device` with slots of `slot` bytes, made or remade on
+  // demand.  Caller holds mu; `device` is current.
+  Staging* staging_for(int device, size_t slot, hipError_t* err) const {
+    *err = hipSuccess;
+    for (auto& st : stagings) {
+      if (st->device != device) continue;
+      if (st->slot == slot) return st.get();
+      st.reset();
+      st = std::unique_ptr<Staging>(new Staging());
+      *err = st->init(device, slot);
+      return *err == hipSuccess ? st.get() : nullptr;
+    }
+    stagings.emplace_back(new Staging());
+    *err = stagings.back()->init(device, slot);
+    return *err == hipSuccess ? stagings.back().get() : nullptr;
+  }
 
   ~gptoss_checkpoint() {
+    stagings.clear();
     for (Shard& s : shards) {
       if (s.base) munmap(s.base, s.size);
       if (s.fd >= 0) close(s.fd);
@@ -612,35 +672,6 @@ int per_expert_source(const gptoss_checkpoint* ck, const std::string& prefix, in
   return GPTOSS_OK;
 }
 
-// Two pinned host slots and two device slots; slot i is free again once
-// its event has completed.
-struct Staging {
-  uint8_t* host = nullptr;
-  uint8_t* dev = nullptr;
-  size_t slot = 0;
-  hipStream_t stream = nullptr;
-  hipEvent_t ev[2] = {nullptr, nullptr};
-  bool pending[2] = {false, false};
-  int next = 0;
-
-  hipError_t init(size_t bytes) {
-    slot = bytes;
-    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&host), 2 * slot, hipHostMallocDefault);
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&dev), 2 * slot);
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
-    for (int i = 0; i < 2 && e == hipSuccess; ++i) e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
-    return e;
-  }
-  ~Staging() {
-    if (stream) (void)hipStreamSynchronize(stream);
-    for (hipEvent_t x : ev)
-      if (x) (void)hipEventDestroy(x);
-    if (stream) (void)hipStreamDestroy(stream);
-    if (dev) (void)hipFree(dev);
-    if (host) (void)hipHostFree(host);
-  }
-};
-
 // Stream E expert matrices [N][K] from the mapping into the tiled buffers:
 // chunks of experts fill a pinned slot (threads copying out of the mapping),
 // one host-to-device copy moves the slot, and one repack launch per expert
@@ -768,8 +799,8 @@ int gptoss_checkpoint_set_staging_bytes(gptoss_checkpoint* ckpt, size_t bytes) {
 namespace gxmoe {
 
 struct LayerSource {
+  const gptoss_checkpoint* ck = nullptr;
   int E = 0, H = 0, I = 0;
-  size_t staging = 0;
   std::vector<uint16_t> v_rw, v_rb, v_nw, v_b1, v_b2;  // bf16, converted on the host
   ExpertSource s1, s2;                                // gate_up [2I][H], down [H][I]
 };
@@ -783,7 +814,7 @@ int resolve(const gptoss_checkpoint* ck, const gptoss_moe_config& cfg, int layer
   L.E = E;
   L.H = H;
   L.I = I;
-  L.staging = ck->staging;
+  L.ck = ck;
   if (layer < 0) return set_error(GPTOSS_ERR_INVALID, "layer_index=%d must be >= 0", layer);
   const std::string P = "model.layers." + std::to_string(layer) + ".";
   auto first = [&](std::initializer_list<const char*> names) -> const Tensor* {
@@ -881,23 +912,24 @@ int ckpt_upload_layer(const LayerSource* src, void** blob, gptoss_moe_weights* w
   {
     const size_t per1 = align_up(static_cast<size_t>(2 * I) * H / 2, 256) + align_up(static_cast<size_t>(2 * I) * H / 32, 256);
     const size_t per2 = align_up(static_cast<size_t>(H) * I / 2, 256) + align_up(static_cast<size_t>(H) * I / 32, 256);
-    const size_t want = std::max({src->staging, per1, per2});
+    const gptoss_checkpoint* ck = src->ck;
+    const size_t want = std::max({ck->staging, per1, per2});
     // slots hold whole experts: no more than the larger matrix's experts need
-    const size_t slot = std::min(want, std::max(per1, per2) * static_cast<size_t>(E));
-    Staging st;
-    e = st.init(align_up(slot, 256));
-    if (e != hipSuccess) {
+    const size_t slot = align_up(std::min(want, std::max(per1, per2) * static_cast<size_t>(E)), 256);
+    std::lock_guard<std::mutex> lock(ck->mu);
+    int device = 0;
+    e = hipGetDevice(&device);
+    Staging* st = e == hipSuccess ? ck->staging_for(device, slot, &e) : nullptr;
+    if (st == nullptr) {
       (void)hipFree(base);
       return set_error(GPTOSS_ERR_OOM, "staging buffers (2 x %zu bytes): %s", slot, hipGetErrorString(e));
     }
-    rc = upload_experts(st, src->s1, E, 2 * I, H, base + o_w1n, base + o_w1s);
-    if (rc == GPTOSS_OK) rc = upload_experts(st, src->s2, E, H, I, base + o_w2n, base + o_w2s);
-    if (rc == GPTOSS_OK) {
-      e = hipStreamSynchronize(st.stream);
-      if (e != hipSuccess) rc = set_error(GPTOSS_ERR_HIP, "expert upload: %s", hipGetErrorString(e));
-    }
+    st->pending[0] = st->pending[1] = false;  // the previous load ended with a stream sync
+    rc = upload_experts(*st, src->s1, E, 2 * I, H, base + o_w1n, base + o_w1s);
+    if (rc == GPTOSS_OK) rc = upload_experts(*st, src->s2, E, H, I, base + o_w2n, base + o_w2s);
+    e = hipStreamSynchronize(st->stream);
+    if (rc == GPTOSS_OK && e != hipSuccess) rc = set_error(GPTOSS_ERR_HIP, "expert upload: %s", hipGetErrorString(e));
     if (rc != GPTOSS_OK) {
-      (void)hipStreamSynchronize(st.stream);
       (void)hipFree(base);
       return rc;
     }

@@ -147,7 +147,7 @@ void gptoss_moe_layer_destroy(gptoss_moe_layer* layer);           /* moe_layer_d
  * A safetensors checkpoint: every `*.safetensors` file of a directory in
  * name order (weight_loader.cu:456-482), or one file, mapped read-only
  * (:488-537).  The index maps names to tensors; a name present in several
- * shards resolves to the last shard in name order (:543-551). */
+ * shards resolves to the last shard in name order (:546-555). */
 typedef struct gptoss_checkpoint gptoss_checkpoint;
 
 typedef struct gptoss_tensor_info {
@@ -172,7 +172,9 @@ int gptoss_checkpoint_tensor_at(const gptoss_checkpoint* ckpt, int i, gptoss_ten
 int gptoss_checkpoint_find(const gptoss_checkpoint* ckpt, const char* name, gptoss_tensor_info* info);
 /* Size of each of the two pinned host and two device staging slots that
  * gptoss_moe_layer_init_from_checkpoint streams experts through (default
- * 64 MiB; a slot always holds at least one expert matrix). */
+ * 32 MiB; a slot always holds at least one expert matrix).  The checkpoint
+ * keeps the staging of each device it has loaded a layer onto until it is
+ * closed, so the layers of a model reuse one pinned allocation. */
 int gptoss_checkpoint_set_staging_bytes(gptoss_checkpoint* ckpt, size_t bytes);
 
 /* One MoE layer from a checkpoint: WeightLoader::load_layer_weights' MoE part
@@ -183,7 +185,9 @@ int gptoss_checkpoint_set_staging_bytes(gptoss_checkpoint* ckpt, size_t bytes);
  * scales,bias} or mlp.experts.<e>.{mlp1|gate_up_proj|w1, mlp2|down_proj|w2}
  * .weight[_scale].  bf16 tensors stored as F32 or F16 are rounded to bf16
  * (nearest even).  The layer owns one device allocation holding every
- * weight, the experts already tiled; shapes are checked against cfg. */
+ * weight, the experts already tiled; names, shapes and dtypes are checked
+ * against cfg before any device work.  Loads from one checkpoint run one at
+ * a time (they share its staging). */
 int gptoss_moe_layer_init_from_checkpoint(gptoss_moe_layer* layer, const gptoss_moe_config* cfg,
                                           int device_id, const gptoss_checkpoint* ckpt, int layer_index);
 

@@ -122,3 +122,30 @@ def test_checkpoint_full_gptoss_shape(gpu, torch_mod, tmp_path):
         torch.cuda.synchronize()
         assert np.array_equal(out, out_ref), T
     L.destroy()
+
+
+def test_checkpoint_layers_share_staging(gpu, torch_mod, tmp_path):
+    """Several layers from one open checkpoint: the staging is kept between
+    loads, and remade when the staging size changes; every layer matches its
+    pointer-table twin."""
+    torch = torch_mod
+    E, k, H, I, T = 8, 4, 256, 128, 8
+    ws = [moe_data.make_layer(100 + l, E, H, I, bias="random") for l in range(3)]
+    t = {}
+    for l, w in enumerate(ws):
+        t.update(ckpt_data.layer_tensors(l, w, E, H, I))
+    ckpt_data.write_shards(str(tmp_path), t, n_shards=2)
+    cfg = gpu.default_config(E, T, decode_exact=True)
+    cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, k
+    x, res = moe_data.make_tokens(105, T, H)
+    with gpu.Checkpoint(str(tmp_path)) as ck:
+        for l, staging in ((0, None), (1, None), (2, 1), (0, 1)):
+            if staging is not None:
+                ck.set_staging_bytes(staging)
+            L = gpu.MoELayer().init_from_checkpoint(cfg, 0, ck, l)
+            ref = DeviceLayer(gpu, torch, ws[l], E, k, H, I, max_tokens=T)
+            out = host(L.forward_prenormed(dev(x, torch), dev(res, torch)))
+            out_ref = host(ref.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+            torch.cuda.synchronize()
+            assert np.array_equal(out, out_ref), (l, staging)
+            L.destroy()
