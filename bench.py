@@ -382,51 +382,42 @@ def bench_checkpoint_load(g, torch, n_experts: int = 32, reps: int = 3):
 
 def bench_stack(g, torch, layers: int = 36, T: int = 32, steps: int = 256):
     """36 distinct GPT-OSS-120B MoE layers resident (random
-    MXFP4 weights, ~61 GB), a decode step at batch 32 = the 36 layer forwards
-    chained through the residual stream, captured once in a hipGraph and
-    replayed `steps` times."""
-    cps = [make_copy(g, torch, 5000 + l) for l in range(layers)]
-    Ls = [g.MoELayer().init(g.default_config(E, T), 0, c["router_w"], c["router_b"], c["b1"], c["b2"],
-                            tiled=c["tiled"]) for c in cps]
+    MXFP4 weights, ~61 GB) in one MoEStack.  A decode step at batch 32 is the
+    engine's per-layer MoE sequence over all 36 layers -- residual += delta
+    (random, standing in for attention), RMSNorm, MoE, in place -- captured by
+    the library as one hipGraph and replayed `steps` times."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(32)
-    h0 = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
-    hs = [h0] + [torch.empty_like(h0) for _ in range(layers)]
-
-    def step():
-        for l, L in enumerate(Ls):
-            # prenormed input = the residual stream itself (no attention or norm in this stack)
-            L.forward_prenormed(hs[l], hs[l], out=hs[l + 1])
-
-    step()
+    cps = [make_copy(g, torch, 5000 + l) for l in range(layers)]
+    norms = [(1.0 + 0.1 * torch.randn((H,), device="cuda", generator=gen)).to(torch.bfloat16) for _ in range(layers)]
+    Ls = [g.MoELayer().init(g.default_config(E, T), 0, c["router_w"], c["router_b"], c["b1"], c["b2"],
+                            moe_norm_weight=n, tiled=c["tiled"]) for c, n in zip(cps, norms)]
+    st = g.MoEStack.from_layers(Ls)
+    st.residual.copy_(torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16))
+    st.deltas.copy_(torch.randn((layers, T, H), device="cuda", generator=gen).to(torch.bfloat16))
+    st.decode_step(T, use_graph=False)
     torch.cuda.synchronize()
-    U = []
-    for L in Ls:
-        U.append(int(g.copy_device_to_tensor(L.trace().n_active, 4, torch.int32).item()))
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=s):
-        step()
-    graph.replay()
+    U = [int(g.copy_device_to_tensor(st.layer(l).trace().n_active, 4, torch.int32).item()) for l in range(layers)]
+    st.decode_step(T)  # captures the step's graph
     torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):
-        t0.record(s)
-        for _ in range(steps):
-            graph.replay()
-        t1.record(s)
+    t0.record(s)
+    for _ in range(steps):
+        st.decode_step(T)
+    t1.record(s)
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
-    del graph
+    st.destroy()
     for L in Ls:
         L.destroy()
     nbytes = sum(layer_bytes(u, T) for u in U)
     return dict(layers=layers, batch=T, steps=steps, ms_per_step=ms, tokens_per_s=T / (ms / 1e3),
                 experts_touched_mean=sum(U) / len(U), algorithmic_bytes_per_step=nbytes,
                 hbm_gbs=nbytes / (ms / 1e3) / 1e9, hbm_frac=nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
-                weights_gb=layers * E * (W1_EXPERT_BYTES + W2_EXPERT_BYTES) / 1e9)
+                weights_gb=layers * E * (W1_EXPERT_BYTES + W2_EXPERT_BYTES) / 1e9,
+                step="per layer: residual += delta, RMSNorm, MoE (gptoss_moe_stack_decode_step, one hipGraph)")
 
 
 def cpu_baseline(seconds: float, threads: int):

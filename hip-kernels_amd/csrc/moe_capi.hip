@@ -604,6 +604,13 @@ const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* L) 
   return L ? L->norm_w : nullptr;
 }
 
+int gptoss_moe_layer_get_config(const gptoss_moe_layer* L, gptoss_moe_config* cfg, int* device_id) {
+  if (L == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
+  if (cfg) *cfg = L->cfg;
+  if (device_id) *device_id = L->device;
+  return ok();
+}
+
 int gptoss_moe_layer_set_trace_gate_up(gptoss_moe_layer* L, int enable) {
   if (L == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
   if (enable && L->gate_up == nullptr) {

@@ -104,6 +104,15 @@ _sig("gptoss_checkpoint_num_tensors", [_P])
 _sig("gptoss_checkpoint_tensor_at", [_P, _I, ctypes.POINTER(TensorInfo)])
 _sig("gptoss_checkpoint_find", [_P, ctypes.c_char_p, ctypes.POINTER(TensorInfo)])
 _sig("gptoss_checkpoint_set_staging_bytes", [_P, _SZ])
+_sig("gptoss_moe_layer_get_config", [_P, ctypes.POINTER(MoeConfig), ctypes.POINTER(_I)])
+_HOOK = ctypes.CFUNCTYPE(None, _P, _I, _P, _P, _I, _P)
+_sig("gptoss_moe_stack_create", [ctypes.POINTER(MoeConfig), _I, _P, _I, _I, ctypes.POINTER(_P)])
+_sig("gptoss_moe_stack_create_from_layers", [ctypes.POINTER(_P), _I, ctypes.POINTER(_P)])
+_sig("gptoss_moe_stack_io", [_P, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_I), ctypes.POINTER(_I)])
+_sig("gptoss_moe_stack_bind", [_P, _P, _P])
+_sig("gptoss_moe_stack_layer", [_P, _I, ctypes.POINTER(_P)])
+_sig("gptoss_moe_stack_decode_step", [_P, _I, _HOOK, _P, _I, _P])
+_sig("gptoss_moe_stack_destroy", [_P], None)
 _sig("gptoss_moe_layer_trace", [_P, ctypes.POINTER(MoeTrace)])
 _sig("gptoss_moe_layer_set_trace_gate_up", [_P, _I])
 _sig("gptoss_moe_layer_set_profiling", [_P, _I])
@@ -206,7 +215,17 @@ class MoELayer:
         if not self._h:
             raise GptossError(GPTOSS_ERR_OOM, "gptoss_moe_layer_create failed")
         self._keep = []
+        self._owned = True
         self.cfg = None
+
+    @classmethod
+    def _borrow(cls, handle: int) -> "MoELayer":
+        """A view of a layer owned elsewhere (a stack's); destroy() is a no-op."""
+        self = cls.__new__(cls)
+        self._h, self._keep, self._owned = handle, [], False
+        self.cfg = MoeConfig()
+        check(_lib.gptoss_moe_layer_get_config(handle, ctypes.byref(self.cfg), None))
+        return self
 
     def init(self, cfg: MoeConfig, device_id: int, router_weight, router_bias=None, gate_up_bias=None,
              down_bias=None, moe_norm_weight=None, mlp1=None, mlp2=None, tiled=None) -> "MoELayer":
@@ -307,7 +326,8 @@ class MoELayer:
 
     def destroy(self) -> None:
         if self._h:
-            _lib.gptoss_moe_layer_destroy(self._h)
+            if self._owned:
+                _lib.gptoss_moe_layer_destroy(self._h)
             self._h = None
 
     def __del__(self):
@@ -368,6 +388,35 @@ class Checkpoint:
         a = np.frombuffer(raw, dtype=dt or "u1")
         return (a.reshape(inf["shape"]) if dt else a).copy()
 
+    def _router_weight(self, layer: int):
+        for n in ("mlp.gate.weight", "mlp.router.weight"):
+            inf = self.info(f"model.layers.{layer}.{n}")
+            if inf is not None:
+                return inf
+        return None
+
+    def num_moe_layers(self) -> int:
+        """Layers 0, 1, ... that have a router weight."""
+        n = 0
+        while self._router_weight(n) is not None:
+            n += 1
+        return n
+
+    def moe_shape(self, layer: int = 0):
+        """(E, H, I) of a layer, from its router weight [E][H] and its gate_up
+        blocks or biases ([E][2I]...)."""
+        rw = self._router_weight(layer)
+        if rw is None:
+            raise GptossError(GPTOSS_ERR_NOT_FOUND, f"no router weight for layer {layer}")
+        E, H = rw["shape"]
+        P = f"model.layers.{layer}.mlp.experts."
+        for n in ("gate_up_proj_blocks", "gate_up_proj_bias", "0.mlp1.weight", "0.gate_up_proj.weight",
+                  "0.w1.weight"):
+            inf = self.info(P + n)
+            if inf is not None:
+                return E, H, inf["shape"][1 if n.startswith("gate_up") else 0] // 2
+        raise GptossError(GPTOSS_ERR_NOT_FOUND, f"no gate_up tensor for layer {layer}")
+
     def set_staging_bytes(self, nbytes: int) -> None:
         check(_lib.gptoss_checkpoint_set_staging_bytes(self._h, nbytes))
 
@@ -387,6 +436,157 @@ class Checkpoint:
             self.close()
         except Exception:
             pass
+
+
+class MoEStack:
+    """The MoE half of the engine's decode step over a stack of layers
+    (transformer.cu:653-753): per layer, an optional hook writes the layer's
+    delta from the current residual (the engine's attention), then
+    residual = bf16(residual + delta) + MoE(RMSNorm(residual + delta)),
+    in place.  decode_step(use_graph=True) replays one hipGraph per token
+    count, captured on first use.  The residual and deltas live in torch
+    tensors bound to the stack: `residual` [max_tokens][H] and `deltas`
+    [num_layers][max_tokens][H], bf16."""
+
+    def __init__(self, handle: int, layers=None):
+        self._h = handle
+        self._layers = layers  # layers borrowed by the stack, kept alive here
+        self._hooks = {}
+        r, d, mt, nl = _P(), _P(), _I(), _I()
+        check(_lib.gptoss_moe_stack_io(self._h, ctypes.byref(r), ctypes.byref(d), ctypes.byref(mt), ctypes.byref(nl)))
+        self.max_tokens, self.num_layers = mt.value, nl.value
+        L0 = _P()
+        check(_lib.gptoss_moe_stack_layer(self._h, 0, ctypes.byref(L0)))
+        cfg, dev = MoeConfig(), _I()
+        check(_lib.gptoss_moe_layer_get_config(L0.value, ctypes.byref(cfg), ctypes.byref(dev)))
+        self.cfg, self.device = cfg, dev.value
+        H = cfg.hidden_size
+        device = torch.device("cuda", self.device)
+        self.residual = torch.zeros((self.max_tokens, H), dtype=torch.bfloat16, device=device)
+        self.deltas = torch.zeros((self.num_layers, self.max_tokens, H), dtype=torch.bfloat16, device=device)
+        check(_lib.gptoss_moe_stack_bind(self._h, _ptr(self.residual), _ptr(self.deltas)))
+
+    @classmethod
+    def from_checkpoint(cls, cfg: MoeConfig, device_id: int, ckpt: "Checkpoint", first_layer: int = 0,
+                        num_layers: int | None = None) -> "MoEStack":
+        if num_layers is None:
+            num_layers = ckpt.num_moe_layers() - first_layer
+        h = _P()
+        check(_lib.gptoss_moe_stack_create(ctypes.byref(cfg), device_id, ckpt._h, first_layer, num_layers,
+                                           ctypes.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def from_layers(cls, layers) -> "MoEStack":
+        arr = (_P * len(layers))(*[L._h for L in layers])
+        h = _P()
+        check(_lib.gptoss_moe_stack_create_from_layers(arr, len(layers), ctypes.byref(h)))
+        return cls(h.value, layers=list(layers))
+
+    def layer(self, i: int) -> MoELayer:
+        h = _P()
+        check(_lib.gptoss_moe_stack_layer(self._h, i, ctypes.byref(h)))
+        return MoELayer._borrow(h.value)
+
+    def _c_hook(self, hook):
+        """One C function pointer per Python hook, so that the same hook
+        finds its captured graph again."""
+        if hook is None:
+            return _HOOK()
+        key = id(hook)
+        if key not in self._hooks:
+            def tramp(_user, layer, residual, delta, T, stream, _hook=hook):
+                _hook(layer, residual or 0, delta or 0, T, stream or 0)
+            self._hooks[key] = (hook, _HOOK(tramp))
+        return self._hooks[key][1]
+
+    def decode_step(self, T: int, hook=None, use_graph: bool = True, stream=None) -> torch.Tensor:
+        """One step on residual[:T] with deltas[:, :T].  hook(layer,
+        residual_ptr, delta_ptr, T, stream_ptr) runs before each layer (only
+        while a graph is captured when use_graph).  Returns residual[:T]."""
+        check(_lib.gptoss_moe_stack_decode_step(self._h, T, self._c_hook(hook), None, 1 if use_graph else 0,
+                                                _stream(stream)))
+        return self.residual[:T]
+
+    def destroy(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.gptoss_moe_stack_destroy(self._h)
+            self._h = None
+        self._layers = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class ModelConfig:
+    """The MoE constants of GPT-OSS-120B, as the reference's read-only
+    gptoss.ModelConfig exposes them (bindings.cpp:317-400, config.h)."""
+    num_layers = 36
+    hidden_size = 2880
+    num_experts = 128
+    num_active_experts = 4
+    expert_intermediate_size = 2880
+    rms_norm_eps = 1e-5
+    swiglu_alpha = 1.702
+    swiglu_limit = 7.0
+
+
+class MoEEngine:
+    """The InferenceEngine lifecycle (bindings.cpp:221-311: init(weights_dir),
+    shutdown(), is_initialized) over the MoE half of the model: init() loads
+    every MoE layer of a safetensors checkpoint into one stack on one GPU;
+    decode_step() runs the per-layer residual add + RMSNorm + MoE of the
+    decode step for all layers, as one cached hipGraph per batch size.  The
+    attention that produces each layer's delta is the caller's (a hook, or
+    deltas written beforehand)."""
+
+    def __init__(self):
+        self._stack = None
+
+    def init(self, weights_dir: str, max_tokens: int = 64, device_id: int = 0, num_layers: int | None = None,
+             top_k: int = ModelConfig.num_active_experts) -> "MoEEngine":
+        if self._stack is not None:
+            raise GptossError(GPTOSS_ERR_STATE, "[MoEEngine] Already initialized")
+        with Checkpoint(weights_dir) as ck:
+            E, H, I = ck.moe_shape(0)
+            cfg = default_config(E, max_tokens)
+            cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, top_k
+            self._stack = MoEStack.from_checkpoint(cfg, device_id, ck, 0, num_layers)
+        return self
+
+    @property
+    def is_initialized(self) -> bool:
+        return self._stack is not None
+
+    @property
+    def stack(self) -> MoEStack:
+        if self._stack is None:
+            raise GptossError(GPTOSS_ERR_STATE, "[MoEEngine] Not initialized")
+        return self._stack
+
+    def decode_step(self, hidden: torch.Tensor, deltas: torch.Tensor | None = None, hook=None,
+                    use_graph: bool = True) -> torch.Tensor:
+        """hidden [T][H] bf16 (the residual stream entering layer 0); deltas
+        [num_layers][T][H] (or a hook).  Returns the residual after the last
+        layer, [T][H]."""
+        st = self.stack
+        T = hidden.shape[0]
+        st.residual[:T].copy_(hidden)
+        if deltas is not None:
+            st.deltas[:, :T].copy_(deltas)
+        return st.decode_step(T, hook=hook, use_graph=use_graph).clone()
+
+    def shutdown(self) -> None:
+        if self._stack is not None:
+            self._stack.destroy()
+            self._stack = None
+
+    def __repr__(self) -> str:
+        n = self._stack.num_layers if self._stack is not None else 0
+        return f"<gptoss_moe.MoEEngine initialized={self.is_initialized} layers={n}>"
 
 
 # ---------------------------------------------------------------------------

@@ -141,6 +141,8 @@ int gptoss_moe_layer_forward_routed(gptoss_moe_layer* layer, const uint16_t* nor
                                     const float* expert_weights, uint16_t* output, int num_tokens,
                                     void* stream);
 const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* layer);
+/* The config and device the layer was initialised with. */
+int gptoss_moe_layer_get_config(const gptoss_moe_layer* layer, gptoss_moe_config* cfg, int* device_id);
 void gptoss_moe_layer_destroy(gptoss_moe_layer* layer);           /* moe_layer_destroy */
 
 /* ---- Checkpoints (src/memory/weight_loader.cu) ---------------------------
@@ -190,6 +192,50 @@ int gptoss_checkpoint_set_staging_bytes(gptoss_checkpoint* ckpt, size_t bytes);
  * a time (they share its staging). */
 int gptoss_moe_layer_init_from_checkpoint(gptoss_moe_layer* layer, const gptoss_moe_config* cfg,
                                           int device_id, const gptoss_checkpoint* ckpt, int layer_index);
+
+/* ---- Layer stack: the MoE half of the engine's decode step ----------------
+ * The engine's decode step (transformer.cu:653-753) runs, per layer,
+ * attention (a delta), fused_residual_rmsnorm_forward and
+ * moe_layer_forward_prenormed, and is never graph-captured because the
+ * reference MoE synchronises the host (engine.cu:309-320).  A stack runs the
+ * same per-layer sequence over its layers, in place on a residual buffer it
+ * owns:
+ *     hook(layer, residual, delta[layer])            (optional: attention)
+ *     residual = bf16(residual + delta[layer]) + MoE_layer(RMSNorm(...))
+ * and, since nothing in it synchronises the host, can capture the whole step
+ * in one hipGraph per token count, kept and replayed by later steps. */
+typedef struct gptoss_moe_stack gptoss_moe_stack;
+
+/* Writes layer `layer`'s delta [T][H] from the current residual [T][H] with
+ * launches on `stream` (the engine's attention).  With graph replay the hook
+ * runs once, while its step is captured: its launches are replayed as
+ * captured, so they must not synchronise the host or change pointers. */
+typedef void (*gptoss_layer_hook)(void* user, int layer, const uint16_t* residual, uint16_t* delta,
+                                  int num_tokens, void* stream);
+
+/* num_layers layers from first_layer on, each loaded as
+ * gptoss_moe_layer_init_from_checkpoint does (needs
+ * post_attention_layernorm.weight). */
+int gptoss_moe_stack_create(const gptoss_moe_config* cfg, int device_id, const gptoss_checkpoint* ckpt,
+                            int first_layer, int num_layers, gptoss_moe_stack** out);
+/* Over initialised layers (borrowed; one device, one shape, each with
+ * moe_norm_weight). */
+int gptoss_moe_stack_create_from_layers(gptoss_moe_layer* const* layers, int num_layers,
+                                        gptoss_moe_stack** out);
+/* The stack's device buffers: residual [max_tokens][H] and deltas
+ * [num_layers][max_tokens][H], bf16.  Any output may be NULL. */
+int gptoss_moe_stack_io(gptoss_moe_stack* stack, uint16_t** residual, uint16_t** deltas, int* max_tokens,
+                        int* num_layers);
+/* Step on caller-owned buffers of the same shapes instead (NULL: back to the
+ * stack's own); drops the captured graphs, which hold the old pointers. */
+int gptoss_moe_stack_bind(gptoss_moe_stack* stack, uint16_t* residual, uint16_t* deltas);
+int gptoss_moe_stack_layer(gptoss_moe_stack* stack, int index, gptoss_moe_layer** layer);
+/* One step over every layer, ordered on `stream`.  use_graph = 1: replay
+ * the step's graph for num_tokens (captured on first use, and again when
+ * hook or user change). */
+int gptoss_moe_stack_decode_step(gptoss_moe_stack* stack, int num_tokens, gptoss_layer_hook hook, void* user,
+                                 int use_graph, void* stream);
+void gptoss_moe_stack_destroy(gptoss_moe_stack* stack);
 
 /* Device views of the layer's scratch after the last forward on `stream`
  * (valid until the next forward): routing and per-slot intermediates in the

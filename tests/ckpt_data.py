@@ -18,7 +18,7 @@ from safetensors.torch import save_file
 
 
 def bf16_tensor(u16) -> torch.Tensor:
-    return torch.from_numpy(np.ascontiguousarray(u16, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
+    return torch.from_numpy(np.array(u16, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
 
 
 def layer_tensors(layer: int, w: dict, E: int, H: int, I: int, fmt: str = "packed", norm_w=None,

@@ -227,3 +227,41 @@ def test_layer_loader_accepts_valid_layouts_on_host(g, tmp_path, fmt, kw):
     with pytest.raises(g.GptossError) as e:
         _init(g, _layer_dir(tmp_path, fmt=fmt, **kw))
     assert e.value.code == g.GPTOSS_ERR_HIP, str(e.value)
+
+
+def test_stack_and_engine_host_errors(g, tmp_path):
+    """Argument errors of the stack and the engine surface, caught before any
+    device work."""
+    import ctypes
+    out = ctypes.c_void_p()
+    assert g.lib.gptoss_moe_stack_create_from_layers(None, 1, ctypes.byref(out)) == g.GPTOSS_ERR_INVALID
+    L = g.MoELayer()  # created, never initialised
+    arr = (ctypes.c_void_p * 1)(L._h)
+    assert g.lib.gptoss_moe_stack_create_from_layers(arr, 0, ctypes.byref(out)) == g.GPTOSS_ERR_INVALID
+    assert g.lib.gptoss_moe_stack_create_from_layers(arr, 1, ctypes.byref(out)) == g.GPTOSS_ERR_STATE
+    assert b"not initialised" in g.lib.gptoss_last_error()
+    L.destroy()
+    assert g.lib.gptoss_moe_stack_decode_step(None, 1, g._HOOK(), None, 1, None) == g.GPTOSS_ERR_INVALID
+    cfg = g.default_config(4, 8)
+    assert g.lib.gptoss_moe_stack_create(ctypes.byref(cfg), 0, None, 0, 1, ctypes.byref(out)) == g.GPTOSS_ERR_INVALID
+    eng = g.MoEEngine()
+    assert not eng.is_initialized and repr(eng) == "<gptoss_moe.MoEEngine initialized=False layers=0>"
+    with pytest.raises(g.GptossError) as e:
+        eng.init(str(tmp_path / "missing"))
+    assert e.value.code == g.GPTOSS_ERR_NOT_FOUND
+    with pytest.raises(g.GptossError):
+        eng.stack
+    assert (g.ModelConfig.num_layers, g.ModelConfig.num_experts, g.ModelConfig.num_active_experts) == (36, 128, 4)
+
+
+def test_checkpoint_moe_shape_detection(g, tmp_path):
+    for fmt, kw in (("packed", {}), ("per_expert", {"expert_names": ("gate_up_proj", "down_proj")})):
+        d = tmp_path / fmt
+        w = moe_data.make_layer(3, E, H, I)
+        t = {}
+        for l in range(3):
+            t.update(ckpt_data.layer_tensors(l, w, E, H, I, fmt=fmt, **kw))
+        ckpt_data.write_shards(str(d), t, n_shards=2)
+        with g.Checkpoint(str(d)) as ck:
+            assert ck.moe_shape(0) == (E, H, I)
+            assert ck.num_moe_layers() == 3
