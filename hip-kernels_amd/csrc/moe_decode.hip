@@ -441,14 +441,15 @@ hipError_t launch_mc_shape(const McParams& p, int P, int D, int NC, int max_item
   return hipErrorInvalidValue;
 }
 
-// Default shape for nb blocks and S routed slots (measured on MI355X at the
-// GPT-OSS-120B shape; the shapes differ by a few percent): one token takes
-// three K-parts with a short ring, a few tokens two parts, larger batches
-// six parts with each wave's whole part (15 blocks) in flight.
+// Default shape for nb blocks and S routed slots, measured on MI355X at the
+// GPT-OSS-120B shape (graph-replayed steps at 1..64 tokens; the shapes differ
+// by a few percent): three K-parts with a short ring up to 2 tokens and at
+// 8, two parts at 4, six parts with each wave's whole part (15 blocks) in
+// flight from 16 tokens.
 void pick_shape(int nb, int S, int& P, int& D, int& NC) {
   NC = 1;
   if (nb == kNbGptOss) {
-    if (S <= 4) { P = 3; D = 5; }
+    if (S <= 8 || (S > 16 && S <= 32)) { P = 3; D = 5; }
     else if (S <= 16) { P = 2; D = 9; }
     else { P = 6; D = 15; }
     return;
