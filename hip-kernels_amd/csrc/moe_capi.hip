@@ -411,7 +411,7 @@ constexpr int kProfEvents = 8;
 // kernels, on the matrix cores or exact; prefill: grouped matrix-core GEMMs).
 // w: routing weights [T][k].
 static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, const float* w,
-                         uint16_t* out, int T, hipStream_t s, const ProfForward& pf) {
+                         uint16_t* out, int T, hipStream_t s, const ProfForward& pf, bool route_in_w1 = false) {
   const gptoss_moe_config& c = L->cfg;
   ExpertArgs ea{};
   ea.x = normed;
@@ -444,6 +444,13 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
   ea.mc_shape[0] = L->mc_shape[0];
   ea.mc_shape[1] = L->mc_shape[1];
   ea.mc_shape[2] = L->mc_shape[2];
+  if (route_in_w1) {  // the gate_up launch selects the experts from the router's logits
+    ea.route_logits = L->logits;
+    ea.route_fp32 = c.logits_fp32;
+    ea.route_variant = 1;  // T <= 8 (topk_softmax.cu:399)
+    ea.route_idx = L->idx;
+    ea.route_w = L->w;
+  }
   if (c.prefill_min_tokens > 0 && T >= c.prefill_min_tokens) {
     GroupedArgs g{};
     g.x = normed;
@@ -527,11 +534,19 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ra.idx = L->idx;
   ra.w = L->w;
   ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks};
+  // Up to 8 tokens on the matrix-core decode path, the gate_up launch makes
+  // the top-k and plan itself: the router launch computes the logits only.
+  const bool prefill = c.prefill_min_tokens > 0 && T >= c.prefill_min_tokens;
+  const bool route_in_w1 = !prefill && !c.decode_exact && !L->special_any1 &&
+                           decode_mc_supported(T, c.top_k, c.num_experts, c.hidden_size, c.intermediate_size) &&
+                           decode_route_in_w1(T, c.top_k, c.num_experts, c.hidden_size, c.intermediate_size,
+                                              L->mc_shape);
+  ra.logits_only = route_in_w1 ? 1 : 0;
   const ProfForward pf = next_prof(L, s);
   ra.timer = pf.timer(0);
   HIP_TRY(launch_route(ra, s), "route launch");
-  if (delta != nullptr) return layer_experts(L, L->normed, sum_out, L->w, out, T, s, pf);
-  return layer_experts(L, normed, residual, L->w, out, T, s, pf);
+  if (delta != nullptr) return layer_experts(L, L->normed, sum_out, L->w, out, T, s, pf, route_in_w1);
+  return layer_experts(L, normed, residual, L->w, out, T, s, pf, route_in_w1);
 }
 
 static int check_forward_args(gptoss_moe_layer* L, const void* in, const void* out, int T) {

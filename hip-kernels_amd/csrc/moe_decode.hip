@@ -42,6 +42,7 @@
 
 #include "moe_device.h"
 #include "moe_kernels.h"
+#include "moe_topk.h"
 
 namespace gxmoe {
 namespace {
@@ -64,6 +65,15 @@ struct McParams {
   int bpp;                    // blocks per K-part: nb / P, a multiple of D
   float alpha, limit;
   TiledGeom g;
+  // Routing in the gate_up prologue (kRoute): every work-group selects the
+  // top-k of the r_T <= kSmallTopkMaxT tokens from the router's logits and
+  // builds the plan in LDS; work-group 0 also writes r_idx, r_w and r_plan
+  // for the launches after this one.
+  const void* r_logits;
+  int r_fp32, r_T, r_E, r_k, r_variant;
+  int32_t* r_idx;
+  float* r_w;
+  PlanBufs r_plan;
 };
 
 constexpr int kLdsSlots = 1024;       // slot -> token map staged in LDS up to this many slots
@@ -101,14 +111,20 @@ struct McSrc {
 // registers in the block loop).  BPP: blocks per K-part when known at compile
 // time (a step is then straight-line code, so the compiler's load waits see
 // exactly which ring slot each block needs); 0 = a.bpp, a multiple of D.
-template <bool kGated, int P, int D, int NC, bool kSpec, int BPP>
+// kRoute (gate_up, T <= kSmallTopkMaxT): the routing plan is made in the
+// prologue (McParams r_*) instead of read from a plan launch.
+template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false>
 __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   constexpr int kFr = 4 * NC;   // accumulator fragments: (sub-tile, chunk)
   constexpr int kTok = 16 * NC; // token columns per step
   constexpr int kRed = P > 1 ? 2 * P * kFr * kWave : 1;
   constexpr int kOwn = (kFr + P - 1) / P;  // fragments this wave finishes
+  // the routing prologue's selections and plan scratch (ints), dead before
+  // the epilogue's first use of red, live in red
+  constexpr int kRouteInts = 2 * kSmallTopkMaxT * kMaxTopK + 3 * kMaxExperts;
+  constexpr int kRedAll = kRoute && kRed * 4 < kRouteInts ? (kRouteInts + 3) / 4 : kRed;
   __shared__ int2 hdr[kMaxExperts];
-  __shared__ f32x4 red[kRed];  // [2 buffers][P][kFr][64 lanes]
+  __shared__ f32x4 red[kRedAll];  // [2 buffers][P][kFr][64 lanes]
   __shared__ int32_t tok[kGated ? kLdsSlots : 1];  // slot -> token (gate_up, S <= kLdsSlots)
 
   const TiledGeom& g = a.g;
@@ -119,22 +135,58 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   const int G = gridDim.x;  // a multiple of 8: block b runs on XCD b % 8
   const int vb = static_cast<int>(blockIdx.x);
   const int v = (vb & 7) * (G >> 3) + (vb >> 3);
-  const int nact = __builtin_amdgcn_readfirstlane(*a.n_active);
-  const int n_items = nact * ntiles;
-  if (v >= n_items) return;  // the whole work-group, before any barrier
-
-  // Task headers: {expert | special << 8 | count << 9, offset}.
-  for (int i = threadIdx.x; i < nact; i += P * kWave) {
-    const int4 h = reinterpret_cast<const int4*>(a.tasks)[static_cast<size_t>(i) * (kTaskInts / 4)];
-    const int sp = a.special ? (a.special[h.x] != 0) : 1;
-    hdr[i] = make_int2(h.x | (sp << 8) | (h.z << 9), h.y);
+  int nact;
+  if constexpr (kRoute) {
+    static_assert(kGated && !kSpec, "the routing prologue is a gate_up variant for regular scale codes");
+    // Wave w selects tokens w, w + P, ... (topk_token, as the router's own
+    // small top-k launch does); wave 0 then builds the task headers and the
+    // slot -> token map in LDS.  Every work-group computes the same plan.
+    int32_t* r_idx = reinterpret_cast<int32_t*>(red);
+    float* r_w = reinterpret_cast<float*>(r_idx + kSmallTopkMaxT * kMaxTopK);
+    int32_t* r_cnt = reinterpret_cast<int32_t*>(r_w + kSmallTopkMaxT * kMaxTopK);
+    int32_t* r_off = r_cnt + kMaxExperts;
+    int32_t* r_aidx = r_off + kMaxExperts;
+    __shared__ int r_nact;
+    for (int t = p; t < a.r_T; t += P) {
+      float lv[kMaxExperts / kWave];
+      if (a.r_fp32) load_token_logits<true, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
+      else load_token_logits<false, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
+      topk_token(lv, a.r_k, a.r_variant, r_idx + t * a.r_k, r_w + t * a.r_k, nullptr, lane);
+    }
+    __syncthreads();
+    if (p == 0) {
+      const int S = a.r_T * a.r_k;
+      const bool w0 = blockIdx.x == 0;
+      if (w0 && lane < S) {
+        a.r_idx[lane] = r_idx[lane];
+        a.r_w[lane] = r_w[lane];
+      }
+      const int na = plan_one_wave<kMaxExperts / kWave>(r_idx, S, a.r_k, a.r_E, w0 ? a.r_plan : PlanBufs{}, lane,
+                                                        r_cnt, r_off, r_aidx, hdr, tok);
+      if (lane == 0) r_nact = na;
+    }
+    __syncthreads();
+    nact = __builtin_amdgcn_readfirstlane(r_nact);
+  } else {
+    nact = __builtin_amdgcn_readfirstlane(*a.n_active);
   }
-  // The next step's token ids are read while the weight stream is in flight:
-  // from LDS they need no wait on the loads ahead of them (slots <=
-  // kLdsSlots, checked at launch).
-  if constexpr (kGated)
-    for (int i = threadIdx.x; i < a.slots; i += P * kWave) tok[i] = a.perm_token[i];
-  __syncthreads();
+  const int n_items = nact * ntiles;
+  if (v >= n_items) return;  // the whole work-group, before any further barrier
+
+  if constexpr (!kRoute) {
+    // Task headers: {expert | special << 8 | count << 9, offset}.
+    for (int i = threadIdx.x; i < nact; i += P * kWave) {
+      const int4 h = reinterpret_cast<const int4*>(a.tasks)[static_cast<size_t>(i) * (kTaskInts / 4)];
+      const int sp = a.special ? (a.special[h.x] != 0) : 1;
+      hdr[i] = make_int2(h.x | (sp << 8) | (h.z << 9), h.y);
+    }
+    // The next step's token ids are read while the weight stream is in
+    // flight: from LDS they need no wait on the loads ahead of them (slots
+    // <= kLdsSlots, checked at launch).
+    if constexpr (kGated)
+      for (int i = threadIdx.x; i < a.slots; i += P * kWave) tok[i] = a.perm_token[i];
+    __syncthreads();
+  }
 
   const __amdgpu_buffer_rsrc_t rA = make_rsrc(a.wn, a.wn_bytes);
   const __amdgpu_buffer_rsrc_t rS = make_rsrc(a.ws, a.ws_bytes);
@@ -371,12 +423,12 @@ __global__ void special_scan_kernel(const uint8_t* __restrict__ ws, TiledGeom g,
   }
 }
 
-template <bool kGated, int P, int D, int NC, bool kSpec, int BPP>
+template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false>
 hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_t s, const KernelTimer& timer) {
   static const int per_cu = [] {  // resident work-groups per CU (a property of the kernel)
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mc_stream_kernel<kGated, P, D, NC, kSpec, BPP>, P * kWave,
-                                                     0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute>,
+                                                     P * kWave, 0) != hipSuccess ||
         n < 1)
       n = 1;
     return n;
@@ -386,8 +438,8 @@ hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_
   grid = (grid + 7) & ~7L;  // a multiple of 8 for the XCD-grouped block order
   McParams q = p;
   q.bpp = p.g.nb / P;
-  gx_launch(mc_stream_kernel<kGated, P, D, NC, kSpec, BPP>, dim3(static_cast<unsigned>(grid)), dim3(P * kWave), 0, s,
-            timer, q);
+  gx_launch(mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute>, dim3(static_cast<unsigned>(grid)),
+            dim3(P * kWave), 0, s, timer, q);
   return hipGetLastError();
 }
 
@@ -438,6 +490,27 @@ hipError_t launch_mc_shape(const McParams& p, int P, int D, int NC, int max_item
     return launch_mc_t<kGated, p_, d_, nc_, false, 0>(p, max_items, num_cus, s, timer);
   GX_MC_GENERIC(GX_MC_GO)
 #undef GX_MC_GO
+  return hipErrorInvalidValue;
+}
+
+// Shapes compiled with the routing prologue: those pick_shape chooses for
+// up to kSmallTopkMaxT tokens.
+bool route_shape(int nb, int P, int D, int NC) {
+  if (NC != 1) return false;
+  if (nb == kNbGptOss) return (P == 3 && D == 5) || (P == 2 && D == 9);
+  return P == 1 && D >= 1 && D <= 4 && nb % D == 0;
+}
+
+hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int num_cus, hipStream_t s,
+                           const KernelTimer& timer) {
+  if (p.g.nb == kNbGptOss) {
+    if (P == 3 && D == 5) return launch_mc_t<true, 3, 5, 1, false, kNbGptOss / 3, true>(p, max_items, num_cus, s, timer);
+    if (P == 2 && D == 9) return launch_mc_t<true, 2, 9, 1, false, kNbGptOss / 2, true>(p, max_items, num_cus, s, timer);
+  }
+  if (P == 1 && D == 4) return launch_mc_t<true, 1, 4, 1, false, 0, true>(p, max_items, num_cus, s, timer);
+  if (P == 1 && D == 3) return launch_mc_t<true, 1, 3, 1, false, 0, true>(p, max_items, num_cus, s, timer);
+  if (P == 1 && D == 2) return launch_mc_t<true, 1, 2, 1, false, 0, true>(p, max_items, num_cus, s, timer);
+  if (P == 1 && D == 1) return launch_mc_t<true, 1, 1, 1, false, 0, true>(p, max_items, num_cus, s, timer);
   return hipErrorInvalidValue;
 }
 
@@ -492,6 +565,20 @@ hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
     NC = a.mc_shape[2];
   }
   const int max_items = a.max_active * (g.N / kTileRows);
+  if (gated && a.route_logits != nullptr) {  // routing in the prologue (decode_route_in_w1 said yes)
+    if (a.special_any1 || NC != 1 || a.T > kSmallTopkMaxT || !route_shape(g.nb, P, D, NC))
+      return hipErrorInvalidValue;
+    p.r_logits = a.route_logits;
+    p.r_fp32 = a.route_fp32;
+    p.r_T = a.T;
+    p.r_E = a.E;
+    p.r_k = a.k;
+    p.r_variant = a.route_variant;
+    p.r_idx = a.route_idx;
+    p.r_w = a.route_w;
+    p.r_plan = a.plan;
+    return launch_mc_route(p, P, D, max_items, a.num_cus, s, a.timer);
+  }
   if (gated ? a.special_any1 : a.special_any2)  // weights with e8m0 code 0 or 255: the checking variant
     return gated ? launch_mc_t<true, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s, a.timer)
                  : launch_mc_t<false, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s, a.timer);
@@ -505,6 +592,25 @@ hipError_t launch_w1_mc(const ExpertArgs& a, hipStream_t s) { return launch_mc(a
 hipError_t launch_w2_mc(const ExpertArgs& a, hipStream_t s) { return launch_mc(a, false, s); }
 
 bool decode_shape_valid(int nb, int P, int D, int NC) { return shape_compiled(nb, P, D, NC); }
+
+// Measured on MI355X (GPT-OSS-120B, graph-replayed steps): at one token the
+// prologue's top-k and plan cost less than the launch they replace (28.4 vs
+// 29.5 us per layer); from two tokens the waves' serial selections before
+// the first weight load cost more (B=8: 81.7 vs 77.3 us).
+constexpr int kRouteInW1MaxT = 1;
+
+bool decode_route_in_w1(int T, int k, int E, int H, int I, const int* mc_shape) {
+  if (T < 1 || T > kRouteInW1MaxT || T * k > kWave || E > kMaxExperts) return false;
+  const TiledGeom g = tiled_geom(2 * I, H);
+  int P, D, NC;
+  pick_shape(g.nb, T * k, P, D, NC);
+  if (mc_shape && mc_shape[0] > 0 && shape_compiled(g.nb, mc_shape[0], mc_shape[1], mc_shape[2])) {
+    P = mc_shape[0];
+    D = mc_shape[1];
+    NC = mc_shape[2];
+  }
+  return route_shape(g.nb, P, D, NC);
+}
 
 bool decode_mc_supported(int T, int k, int E, int H, int I) {
   const TiledGeom g1 = tiled_geom(2 * I, H), g2 = tiled_geom(H, I);

@@ -110,6 +110,7 @@ struct RouteArgs {
   uint16_t* normed;
   uint16_t* sum_out;
   KernelTimer timer;       // from the first launch's start to the last one's stop
+  int logits_only;         // 1: the logits (and norm) only; top-k and plan are the caller's
 };
 
 // Bytes of route scratch (reserved: the launches need none).
@@ -149,6 +150,12 @@ struct ExpertArgs {
   int num_cus;                // compute units of the device (persistent grid size)
   int mc_shape[3];            // {P, D, NC} launch shape override, {0,0,0} = automatic
   KernelTimer timer;          // of the next launch_w1* / launch_w2* / launch_combine_slots
+  // launch_w1_mc with the routing in its prologue (decode_route_in_w1): the
+  // router's logits; idx, w and plan are written by the launch.
+  const void* route_logits;   // [T][E] bf16 or fp32, or null (plan from a plan launch)
+  int route_fp32, route_variant;
+  int32_t* route_idx;
+  float* route_w;
 };
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
 // The two launches of launch_experts, for callers that time them separately.
@@ -165,6 +172,10 @@ hipError_t launch_w2_mc(const ExpertArgs& a, hipStream_t s);
 bool decode_mc_supported(int T, int k, int E, int H, int I);
 // Is {P, D, NC} a compiled matrix-core decode shape that fits nb blocks?
 bool decode_shape_valid(int nb, int P, int D, int NC);
+// Does the matrix-core gate_up launch for T tokens (shape override mc_shape,
+// may be null) route in its prologue, so the router's top-k launch can be
+// left out?  (T <= 8 tokens, regular scale codes checked by the caller.)
+bool decode_route_in_w1(int T, int k, int E, int H, int I, const int* mc_shape);
 // flags[e] = 1 if expert e's slot-order scales (tiled_geom(N, K)) hold an
 // e8m0 code 0 or 255, else 0.
 hipError_t launch_special_scan(const uint8_t* ws, int N, int K, int E, int32_t* flags, hipStream_t s);

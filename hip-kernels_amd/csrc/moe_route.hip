@@ -27,6 +27,7 @@
 #include "moe_device.h"
 #include "moe_kernels.h"
 #include "moe_stages.h"
+#include "moe_topk.h"
 
 namespace gxmoe {
 
@@ -35,210 +36,6 @@ namespace {
 constexpr int kRouteThreads = 256;
 constexpr int kPlanThreads = 1024;
 constexpr int kTopkPlanMaxT = 256;  // tokens of the single-work-group top-k + plan
-
-__device__ __forceinline__ float sanitize_logit(float v) {
-  // topk_softmax.cu:47-52: NaN and +-Inf become -FLT_MAX.
-  return ((__float_as_uint(v) & 0x7f800000u) == 0x7f800000u) ? -FLT_MAX : v;
-}
-
-__device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
-  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = __uint_as_float(d[i] << 16);
-    f[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
-  }
-}
-
-// Lane l + 16 / l + 32 values into lane l (for l below 16 / 32), and DPP
-// row_shl:m (lane l reads lane l + m of its 16-lane row).
-__device__ __forceinline__ uint32_t from_plus32(uint32_t x) {
-  return __builtin_amdgcn_permlane32_swap(x, x, false, false)[1];
-}
-__device__ __forceinline__ uint32_t from_plus16(uint32_t x) {
-  return __builtin_amdgcn_permlane16_swap(x, x, false, false)[1];
-}
-template <int M>
-__device__ __forceinline__ uint32_t from_plus_row(uint32_t x) {
-  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x100 | M, 0xf, 0xf, true));
-}
-
-// The sum of the 64 lanes' values in the order of the xor butterfly of
-// gemv_bf16.cu:95-100 (lanes 32 apart added first, then 16, 8, 4, 2, 1):
-// lane 0 adds exactly the same pairs in the same order.  Valid in lane 0.
-__device__ __forceinline__ float tree_sum_lane0(float v) {
-  v = v + __uint_as_float(from_plus32(__float_as_uint(v)));
-  v = v + __uint_as_float(from_plus16(__float_as_uint(v)));
-  v = v + __uint_as_float(from_plus_row<8>(__float_as_uint(v)));
-  v = v + __uint_as_float(from_plus_row<4>(__float_as_uint(v)));
-  v = v + __uint_as_float(from_plus_row<2>(__float_as_uint(v)));
-  v = v + __uint_as_float(from_plus_row<1>(__float_as_uint(v)));
-  return v;
-}
-
-// Wave-uniform max / min of a per-lane u32.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
-  x = max(x, from_plus32(x));
-  x = max(x, from_plus16(x));
-  x = max(x, from_plus_row<8>(x));
-  x = max(x, from_plus_row<4>(x));
-  x = max(x, from_plus_row<2>(x));
-  x = max(x, from_plus_row<1>(x));
-  return __builtin_amdgcn_readfirstlane(x);
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
-  x = min(x, from_plus32(x));
-  x = min(x, from_plus16(x));
-  x = min(x, from_plus_row<8>(x));
-  x = min(x, from_plus_row<4>(x));
-  x = min(x, from_plus_row<2>(x));
-  x = min(x, from_plus_row<1>(x));
-  return __builtin_amdgcn_readfirstlane(x);
-}
-
-// Selection key of a logit: larger key = earlier in the reference's order
-// (value descending; -0 and +0 equal).  After sanitizing, -FLT_MAX is never
-// selected (the reference compares strictly against -FLT_MAX,
-// topk_softmax.cu:133-159) and gets key 0.
-__device__ __forceinline__ uint32_t select_key(float v) {
-  if (v == -FLT_MAX) return 0u;
-  if (v == 0.0f) v = 0.0f;
-  const uint32_t u = __float_as_uint(v);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Logits of one token as the lanes of a wave hold them: expert lane + 64 j
-// (NV = ceil(E / 64) values per lane).
-template <bool F32, int NV>
-__device__ __forceinline__ void load_token_logits(const void* logits, int t, int E, int lane, float (&v)[NV]) {
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int e = lane + kWave * j;
-    const size_t o = static_cast<size_t>(t) * E + e;
-    v[j] = e >= E ? -FLT_MAX
-           : F32  ? reinterpret_cast<const float*>(logits)[o]
-                  : bf16_to_f32(reinterpret_cast<const uint16_t*>(logits)[o]);
-  }
-}
-
-// Sum of the k selected exponentials in the reference's order: v1
-// (topk_softmax.cu:199-204) adds them in slot order; v2 (topk_softmax.cu:
-// 358-362) ends every lane of its butterfly with the tree t[s] + t[s ^ m],
-// m = k/2 .. 1, whose value in slot 0 this returns.
-template <int K>
-__device__ __forceinline__ float slot_sum(const float* ex, int variant) {
-  if (variant == 1) {
-    float sum = 0.0f;
-#pragma unroll
-    for (int s = 0; s < K; ++s) sum = sum + ex[s];
-    return sum;
-  }
-  float t[K];
-#pragma unroll
-  for (int s = 0; s < K; ++s) t[s] = ex[s];
-#pragma unroll
-  for (int m = K >> 1; m > 0; m >>= 1) {
-    float u[K];
-#pragma unroll
-    for (int s = 0; s < K; ++s) u[s] = t[s] + t[s ^ m];
-#pragma unroll
-    for (int s = 0; s < K; ++s) t[s] = u[s];
-  }
-  return t[0];
-}
-
-__device__ __forceinline__ float slot_sum_k(const float* ex, int k, int variant) {
-  switch (k) {
-    case 1: return slot_sum<1>(ex, variant);
-    case 2: return slot_sum<2>(ex, variant);
-    case 4: return slot_sum<4>(ex, variant);
-    default: return slot_sum<8>(ex, variant);
-  }
-}
-
-// Softmax over the selected slots and the slot outputs (topk_softmax.cu:
-// 160-215, 339-375): sel_i[0] == -1 means no finite logit at all (experts
-// 0..k-1, weight 1/k); padded slots (index -1) get weight 0.
-__device__ __forceinline__ void write_slots(const float* sel_v, const int* sel_i, int k, int variant, int32_t* out_idx,
-                                            float* out_w, int32_t* tokens_per_expert) {
-  if (sel_i[0] == -1) {
-#pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) {
-        out_idx[s] = s;
-        out_w[s] = 1.0f / static_cast<float>(k);
-      }
-    if (tokens_per_expert)
-      for (int s = 0; s < k; ++s) atomicAdd(&tokens_per_expert[s], 1);
-    return;
-  }
-  float mx = -FLT_MAX;
-  float ex[kMaxTopK];
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s)
-    if (s < k && sel_v[s] > mx) mx = sel_v[s];
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) ex[s] = (s < k) ? gx_expf(sel_v[s] - mx) : 0.0f;
-  const float inv = 1.0f / slot_sum_k(ex, k, variant);
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) {
-    if (s < k) {
-      out_idx[s] = sel_i[s];
-      out_w[s] = (sel_i[s] < 0) ? 0.0f : ex[s] * inv;
-      if (tokens_per_expert && sel_i[s] >= 0) atomicAdd(&tokens_per_expert[sel_i[s]], 1);
-    }
-  }
-}
-
-// Top-k of one token and the softmax over the selected k (topk_softmax.cu:
-// 77-375), from the lanes' logits v.  Round s takes the largest visible key
-// (value desc) and, among equal keys, the smallest expert index; a round with
-// nothing visible yields (-FLT_MAX, -1), the reference's padding.  Lane 0
-// writes the slot outputs (v1 sequential sum for variant 1, v2 butterfly tree
-// otherwise).  Control flow is wave-uniform.
-template <int NV>
-__device__ __forceinline__ void topk_token(float (&v)[NV], int k, int variant, int32_t* out_idx, float* out_w,
-                                           int32_t* tokens_per_expert, int lane) {
-  uint32_t key[NV];
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    v[j] = sanitize_logit(v[j]);
-    key[j] = select_key(v[j]);
-  }
-  float sel_v[kMaxTopK];
-  int sel_i[kMaxTopK];
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) {
-    sel_v[s] = -FLT_MAX;
-    sel_i[s] = -1;
-    if (s < k) {
-      uint32_t best = key[0];
-#pragma unroll
-      for (int j = 1; j < NV; ++j) best = max(best, key[j]);
-      const uint32_t K = wave_max_u32(best);
-      if (K != 0u) {
-        uint32_t cand = 0xffffffffu;
-#pragma unroll
-        for (int j = NV - 1; j >= 0; --j)
-          if (key[j] == K) cand = static_cast<uint32_t>(lane + kWave * j);
-        const int I = static_cast<int>(wave_min_u32(cand));
-        const int jj = I >> 6, ll = I & 63;
-        float val = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-          if (j == jj) {
-            val = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v[j])), ll)));
-            if (lane == ll) key[j] = 0u;
-          }
-        }
-        sel_v[s] = val;
-        sel_i[s] = I;
-      }
-    }
-  }
-  if (lane != 0) return;
-  write_slots(sel_v, sel_i, k, variant, out_idx, out_w, tokens_per_expert);
-}
 
 // Dispatch plan over the T*k slots of `idx` with NT threads: counts,
 // exclusive offsets, a gather map that is stable in slot order (the counting
@@ -822,89 +619,8 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_lanes_kernel(const voi
   build_plan<kPlanThreads>([&](int s2) { return s_idx[s2]; }, T, K, E, p);
 }
 
-// The plan of S <= 64 slots (values from LDS) built by one wave with no
-// barrier: lane s holds slot s; its rank among equal experts comes from
-// ballots over the expert bits; the counts go through LDS to the lanes that
-// own the experts (expert lane + 64 j), which scan them into offsets and the
-// ascending active list.  Same outputs as build_plan.  LDS accesses of one
-// wave execute in order, so values written are read back without a wait.
-template <int NV>
-__device__ __forceinline__ void plan_one_wave(const int32_t* s_idx, int S, int k, int E, PlanBufs p, int lane,
-                                              int32_t* s_cnt, int32_t* s_off, int32_t* s_aidx) {
-  const int e = lane < S ? s_idx[lane] : -1;
-  const bool valid = e >= 0 && e < E;
-  unsigned long long peers = __ballot(valid);
-#pragma unroll
-  for (int b = 0; b < 8; ++b) {  // E <= 256
-    const bool bit = valid && ((e >> b) & 1);
-    const unsigned long long mb = __ballot(bit);
-    peers &= bit ? mb : ~mb;
-  }
-  const int rank = __popcll(peers & ((1ull << lane) - 1ull));
-#pragma unroll
-  for (int j = 0; j < NV; ++j) s_cnt[lane + kWave * j] = 0;
-  __builtin_amdgcn_wave_barrier();
-  if (valid && rank == 0) s_cnt[e] = __popcll(peers);
-  __builtin_amdgcn_wave_barrier();
-  // experts lane + 64 j: counts, exclusive offsets (scan over j-major order)
-  int base = 0, abase = 0;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int ex = lane + kWave * j;
-    const int c = ex < E ? s_cnt[ex] : 0;
-    int incl = c;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int o = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += o;
-    }
-    const int excl = base + incl - c;
-    const bool act = c > 0;
-    const unsigned long long am = __ballot(act);
-    const int aidx = abase + __popcll(am & ((1ull << lane) - 1ull));
-    if (ex < E) {
-      p.counts[ex] = c;
-      p.offsets[ex] = excl;
-      s_off[ex] = excl;
-      if (ex == E - 1) p.offsets[E] = excl + c;
-    }
-    if (act) {
-      p.active[aidx] = ex;
-      s_aidx[ex] = aidx;
-      if (p.tasks) {
-        int32_t* t = p.tasks + static_cast<size_t>(aidx) * kTaskInts;
-        t[0] = ex;
-        t[1] = excl;
-        t[2] = c;
-        t[3] = 0;
-      }
-    }
-    base += __shfl(incl, kWave - 1, kWave);
-    abase += __popcll(am);
-  }
-  const int nact = abase;
-  if (lane == 0) *p.n_active = nact;
-  if (p.tasks) {
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int r = lane + kWave * j;
-      if (r < E && r >= nact) p.tasks[static_cast<size_t>(r) * kTaskInts] = -1;
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  if (valid) {
-    const int pos = s_off[e] + rank;
-    p.gather_map[lane] = pos;
-    p.perm_token[pos] = lane / k;
-    if (p.tasks && rank < kTaskTokens) p.tasks[static_cast<size_t>(s_aidx[e]) * kTaskInts + 4 + rank] = lane / k;
-  } else if (lane < S) {
-    p.gather_map[lane] = -1;
-  }
-}
-
 // Top-k of T <= kSmallTopkMaxT tokens (wave t: token t, topk_token) and the
 // plan of their T k <= 64 slots by wave 0 after one barrier.
-constexpr int kSmallTopkMaxT = 8;
 template <bool F32, int NV>
 __global__ __launch_bounds__(kSmallTopkMaxT * kWave) void topk_plan_small_kernel(const void* logits, int T, int E,
                                                                                  int k, int variant, int32_t* idx,
@@ -1011,6 +727,7 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
   const int variant = (a.T <= 8) ? 1 : 2;  // topk_softmax.cu:399
   const bool plan = a.plan.counts != nullptr;
   const bool fused = plan && a.T <= kTopkPlanMaxT;
+  if (a.logits_only) return a.logits_fp32 ? launch_logits<true>(a, s, a.timer) : launch_logits<false>(a, s, a.timer);
   const KernelTimer first{a.timer.start, nullptr}, last{nullptr, a.timer.stop};
   hipError_t err = a.logits_fp32 ? launch_logits<true>(a, s, first) : launch_logits<false>(a, s, first);
   if (err != hipSuccess) return err;
