@@ -178,4 +178,13 @@ __device__ __forceinline__ float wave_butterfly_sum(float v) {
   return v;
 }
 
+// LDS-only work-group barrier: orders the LDS traffic of the waves without
+// waiting for their global memory operations (a weight stream stays in
+// flight; stores that no other wave of the launch reads need not complete).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace gxmoe

@@ -42,38 +42,68 @@ constexpr int kTopkPlanMaxT = 256;  // tokens of the single-work-group top-k + p
 // sort of moe_permute.cu:184-236), the permuted token list, the ascending
 // list of experts with at least one slot and the task records.  Slots with an
 // index outside [0, E) get gather_map = -1 and are not dispatched.
+//
+// Wave w owns the contiguous slots [w C, (w + 1) C).  Pass 1 counts its
+// slots per expert 64 at a time: lanes with equal experts find each other by
+// ballots over the expert bits and the lowest adds the group's size (LDS
+// operations of one wave execute in order, so no atomics and no barrier).
+// A scan over the waves then gives each (wave, expert) its base, and pass 2
+// walks the chunk again: position = offset[e] + base[w][e] + rank.  The
+// barriers order LDS only: no wave reads another's global stores.
 template <int NT, typename IdxFn>
 __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
   constexpr int NW = NT / kWave;
   static_assert(NT >= kMaxExperts, "one thread per expert in the scan");
   __shared__ int s_off[kMaxExperts + 1];
-  __shared__ int s_cnt[kMaxExperts];
-  __shared__ int s_run[kMaxExperts];
-  __shared__ int s_wc[NW][kMaxExperts];
+  __shared__ int s_wc[NW][kMaxExperts];  // pass 1: per-wave counts; then per-wave bases
   __shared__ int s_aidx[kMaxExperts];
   __shared__ unsigned long long s_mask[kMaxExperts / kWave];
   __shared__ int s_wsum[kMaxExperts / kWave];
   const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
   const int S = T * k;
+  const int C = ((S + NW - 1) / NW + kWave - 1) / kWave * kWave;  // slots per wave, a multiple of 64
+  const int s0 = min(S, warp * C), s1 = min(S, s0 + C);
 
-  if (tid < kMaxExperts) {
-    s_cnt[tid] = 0;
-    s_run[tid] = 0;
-  }
+  // rank of this lane's slot among the 64 slots' equal experts and the
+  // group mask (wave-uniform control flow)
+  auto group = [&](int e, bool valid, unsigned long long& peers) -> int {
+    peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {  // E <= 256
+      const bool bit = valid && ((e >> b) & 1);
+      const unsigned long long mb = __ballot(bit);
+      peers &= bit ? mb : ~mb;
+    }
+    return __popcll(peers & ((1ull << lane) - 1ull));
+  };
+
   for (int i = tid; i < NW * kMaxExperts; i += NT) (&s_wc[0][0])[i] = 0;
-  __syncthreads();
-  for (int s = tid; s < S; s += NT) {
-    const int e = idx(s);
-    if (e >= 0 && e < E) atomicAdd(&s_cnt[e], 1);
+  lds_barrier();
+  for (int b = s0; b < s1; b += kWave) {
+    const int s = b + lane;
+    const int e = s < s1 ? idx(s) : -1;
+    const bool valid = e >= 0 && e < E;
+    unsigned long long peers;
+    const int rank = group(e, valid, peers);
+    if (valid && rank == 0) s_wc[warp][e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
   }
-  __syncthreads();
+  lds_barrier();
 
-  // exclusive scan of the counts (E <= 256: one value per thread of waves 0..3)
+  // per-wave bases within each expert, then the exclusive scan over experts
+  // (E <= 256: one value per thread of waves 0..3)
   int c = 0, incl = 0;
   bool act = false;
   unsigned long long am = 0ull;
   if (tid < kMaxExperts) {  // wave-uniform
-    c = (tid < E) ? s_cnt[tid] : 0;
+    if (tid < E) {
+#pragma unroll 4
+      for (int w = 0; w < NW; ++w) {
+        const int v = s_wc[w][tid];
+        s_wc[w][tid] = c;
+        c += v;
+      }
+    }
     incl = c;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -85,7 +115,7 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
     am = __ballot(act);
     if (lane == 0) s_mask[warp] = am;
   }
-  __syncthreads();
+  lds_barrier();
   int nact = 0;
 #pragma unroll
   for (int w = 0; w < kMaxExperts / kWave; ++w) nact += __popcll(s_mask[w]);
@@ -120,45 +150,27 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
     if (p.tasks && tid < E && tid >= nact) p.tasks[static_cast<size_t>(tid) * kTaskInts] = -1;
   }
   if (tid == 0) *p.n_active = nact;
-  __syncthreads();
+  lds_barrier();
 
-  // stable positions, NT slots per round: rank among equal experts of the
-  // wave by ballots, then the counts of earlier waves and rounds
-  for (int r0 = 0; r0 < S; r0 += NT) {
-    const int s = r0 + tid;
-    const int e = (s < S) ? idx(s) : -1;
-    const bool valid = (e >= 0 && e < E);
-    unsigned long long peers = __ballot(valid);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const bool bit = valid && ((e >> b) & 1);
-      const unsigned long long mb = __ballot(bit);
-      peers &= bit ? mb : ~mb;
-    }
-    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
-    if (valid && rank == 0) s_wc[warp][e] = __popcll(peers);
-    __syncthreads();
+  // pass 2: stable positions
+  for (int b = s0; b < s1; b += kWave) {
+    const int s = b + lane;
+    const int e = s < s1 ? idx(s) : -1;
+    const bool valid = e >= 0 && e < E;
+    unsigned long long peers;
+    const int rank = group(e, valid, peers);
     if (valid) {
-      int pos = s_off[e] + s_run[e] + rank;
-      for (int w = 0; w < warp; ++w) pos += s_wc[w][e];
+      const int pos = s_off[e] + s_wc[warp][e] + rank;
       p.gather_map[s] = pos;
       p.perm_token[pos] = s / k;
       if (p.tasks && pos - s_off[e] < kTaskTokens)
         p.tasks[static_cast<size_t>(s_aidx[e]) * kTaskInts + 4 + (pos - s_off[e])] = s / k;
-    } else if (s < S) {
+    } else if (s < s1) {
       p.gather_map[s] = -1;
     }
-    __syncthreads();
-    if (tid < E) {
-      int add = 0;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        add += s_wc[w][tid];
-        s_wc[w][tid] = 0;
-      }
-      s_run[tid] += add;
-    }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
+    if (valid && rank == 0) s_wc[warp][e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -644,8 +656,50 @@ __global__ __launch_bounds__(kSmallTopkMaxT * kWave) void topk_plan_small_kernel
   plan_one_wave<NV>(s_idx, S, k, E, p, lane, s_cnt, s_off, s_aidx);
 }
 
-__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* idx, int T, int k, int E, PlanBufs p) {
-  build_plan<kPlanThreads>([&](int s) { return idx[s]; }, T, k, E, p);
+// staged: the T k indices are copied to (dynamic) LDS first, so the ranking
+// rounds of build_plan, separated by barriers, read LDS instead of waiting
+// on global loads one round at a time.
+constexpr int kPlanStageMaxSlots = 24 * 1024;  // 96 KiB of LDS
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* idx, int T, int k, int E, PlanBufs p,
+                                                            int staged) {
+  extern __shared__ int32_t d_idx[];
+  if (staged) {
+    // 16 loads in flight per thread before the first store (a plain loop
+    // waits for each load in turn)
+    constexpr int kBatch = 16;
+    const int S = T * k;
+    for (int s0 = threadIdx.x; s0 < S; s0 += kBatch * kPlanThreads) {
+      int v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int s = s0 + u * kPlanThreads;
+        v[u] = s < S ? idx[s] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int s = s0 + u * kPlanThreads;
+        if (s < S) d_idx[s] = v[u];
+      }
+    }
+    lds_barrier();
+    build_plan<kPlanThreads>([&](int s) { return d_idx[s]; }, T, k, E, p);
+  } else {
+    build_plan<kPlanThreads>([&](int s) { return idx[s]; }, T, k, E, p);
+  }
+}
+
+hipError_t launch_plan_kernel(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s,
+                              const KernelTimer& timer) {
+  const int S = T * k;
+  const int staged = S <= kPlanStageMaxSlots ? 1 : 0;
+  const size_t lds = staged ? static_cast<size_t>(S) * 4 : 0;
+  if (lds > 0) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(plan_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+  }
+  gx_launch(plan_kernel, dim3(1), dim3(kPlanThreads), lds, s, timer, idx, T, k, E, plan, staged);
+  return hipGetLastError();
 }
 
 constexpr int kNormFusedMaxT = 4;  // tokens up to which the residual RMSNorm runs inside the router
@@ -778,9 +832,7 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
   else launch_topk_t<false>(a.logits, a.T, a.E, a.k, variant, a.idx, a.w, nullptr, s, mid);
   err = hipGetLastError();
   if (err != hipSuccess || !plan) return err;
-  gx_launch(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, last, static_cast<const int32_t*>(a.idx), a.T, a.k, a.E,
-            a.plan);
-  return hipGetLastError();
+  return launch_plan_kernel(static_cast<const int32_t*>(a.idx), a.T, a.k, a.E, a.plan, s, last);
 }
 
 hipError_t launch_topk(const void* logits, int logits_fp32, int T, int E, int k,
@@ -795,8 +847,7 @@ hipError_t launch_topk(const void* logits, int logits_fp32, int T, int E, int k,
 hipError_t launch_plan(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s,
                        const KernelTimer& timer) {
   if (T <= 0) return hipSuccess;
-  gx_launch(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, timer, idx, T, k, E, plan);
-  return hipGetLastError();
+  return launch_plan_kernel(idx, T, k, E, plan, s, timer);
 }
 
 }  // namespace gxmoe

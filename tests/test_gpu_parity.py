@@ -163,7 +163,10 @@ def test_route_router_topk(gpu, orc, torch_mod, T, fp32, E, H):
     assert np.array_equal(host(idx2), ridx)
 
 
-@pytest.mark.parametrize("T,k,E", [(1, 4, 128), (64, 4, 128), (4096, 4, 128), (33, 2, 8), (7, 8, 32)])
+# 6144 x 4 slots: the largest plan whose indices are staged in LDS; 8192 x 4:
+# the plan reads them from global memory
+@pytest.mark.parametrize("T,k,E", [(1, 4, 128), (64, 4, 128), (4096, 4, 128), (6144, 4, 128), (8192, 4, 128),
+                                   (33, 2, 8), (7, 8, 32)])
 def test_permute_plan(gpu, orc, torch_mod, T, k, E):
     torch = torch_mod
     rng = np.random.default_rng(T + E)
