@@ -294,3 +294,26 @@ def test_layer_profiling_events(gpu, torch_mod):
     r, a, b, c, n = L.layer.profile_read()
     assert n == 1 and min(r, a, b, c) > 0.0
     L.layer.set_profiling(0)
+
+
+def test_mc_one_token_dropped_slots(gpu, orc, torch_mod):
+    """One token on the matrix-core path with routed slots dropped (-1,
+    >= E), every slot dropped (output = the residual, bit for bit) and a null
+    residual."""
+    torch = torch_mod
+    E, k, H, I = 8, 4, 128, 128
+    w = moe_data.make_layer(31, E, H, I, bias="random")
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=4, exact=False)
+    x, res = moe_data.make_tokens(31, 1, H)
+    wt = np.array([[0.4, 0.3, 0.2, 0.1]], np.float32)
+    for case in ([[3, -1, 5, 1]], [[-1, -1, -1, -1]], [[2, 9, 0, 7]]):
+        idx = np.array(case, np.int32)
+        for r in (res, None):
+            out = host(L.layer.forward_routed(dev(x, torch), dev(idx, torch), dev(wt, torch),
+                                              residual=dev(r, torch) if r is not None else None))
+            torch.cuda.synchronize()
+            ref = orc.moe_forward_routed(w, x, r, idx, wt, E, k, H, I)
+            if (idx < 0).all():
+                assert np.array_equal(out, r if r is not None else np.zeros_like(out)), case
+            else:
+                check_layer_out(out, ref, f"one token {case} residual={r is not None}")
