@@ -141,6 +141,7 @@ struct gptoss_moe_layer {
   int32_t* special1 = nullptr;  // [E] W1 / W2 scales hold e8m0 code 0 or 255
   int32_t* special2 = nullptr;
   int32_t* gqueue = nullptr;    // tile queue of the persistent grouped kernel (zeroed; left zeroed)
+  int32_t* pchunk = nullptr;    // scratch of the multi-launch plan (many tokens)
   int special_any1 = 0, special_any2 = 0;
   int num_cus = 0;
   int mc_shape[3] = {0, 0, 0};  // matrix-core decode launch shape override
@@ -325,6 +326,7 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   ALLOC(special1, int32_t*, E * 4)
   ALLOC(special2, int32_t*, E * 4)
   ALLOC(gqueue, int32_t*, grouped_queue_ints() * 4)
+  ALLOC(pchunk, int32_t*, plan_chunk_ints(static_cast<int>(S), E) * 4)
   if (L->norm_w != nullptr) {
     ALLOC(normed, uint16_t*, T * H * 2)
     ALLOC(sumres, uint16_t*, T * H * 2)
@@ -533,7 +535,7 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ra.logits = L->logits;
   ra.idx = L->idx;
   ra.w = L->w;
-  ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks};
+  ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks, L->pchunk};
   // Up to 8 tokens on the matrix-core decode path, the gate_up launch makes
   // the top-k and plan itself: the router launch computes the logits only.
   const bool prefill = c.prefill_min_tokens > 0 && T >= c.prefill_min_tokens;
@@ -609,7 +611,7 @@ int gptoss_moe_layer_forward_routed(gptoss_moe_layer* L, const uint16_t* normed,
   const gptoss_moe_config& c = L->cfg;
   const ProfForward pf = next_prof(L, s);
   HIP_TRY(launch_plan(idx, T, c.top_k, c.num_experts,
-                      PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks}, s,
+                      PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks, L->pchunk}, s,
                       pf.timer(0)),
           "plan launch");
   return layer_experts(L, normed, residual, w, out, T, s, pf);

@@ -88,7 +88,17 @@ struct PlanBufs {
   // records j >= n_active hold expert -1.  One load gives an expert kernel
   // everything it needs to start streaming weights and activations.
   int32_t* tasks;
+  // Scratch of the multi-launch plan for many slots (plan_chunk_ints(S, E)
+  // ints), or null: one work-group builds the plan.
+  int32_t* chunk;
 };
+
+// Ints of PlanBufs::chunk for S slots and E experts: per 1024-slot chunk
+// and expert a count (then a base), and each expert's active index.
+constexpr int kPlanChunkSlots = 1024;
+inline size_t plan_chunk_ints(int S, int E) {
+  return (static_cast<size_t>((S + kPlanChunkSlots - 1) / kPlanChunkSlots) + 1) * static_cast<size_t>(E);
+}
 
 struct RouteArgs {
   const uint16_t* x;       // [T][H] bf16

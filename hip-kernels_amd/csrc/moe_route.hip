@@ -656,6 +656,185 @@ __global__ __launch_bounds__(kSmallTopkMaxT * kWave) void topk_plan_small_kernel
   plan_one_wave<NV>(s_idx, S, k, E, p, lane, s_cnt, s_off, s_aidx);
 }
 
+// The plan of many slots in three launches that use the whole device (the
+// single work-group's plan_kernel is bound by one CU's throughput).  Slots
+// are cut into chunks of kPlanChunkSlots; work-group b owns chunk b, its
+// wave w the 256 slots from 1024 b + 256 w, ranked 64 at a time as
+// build_plan does (ballots over the expert bits, no atomics).
+//   plan_count_kernel  per (chunk, expert) counts
+//   plan_scan_kernel   per expert: exclusive scan over the chunks (counts
+//                      become chunk bases), then the scan over experts:
+//                      counts, offsets, active list, task records
+//   plan_place_kernel  per chunk: wave bases, stable positions, gather map,
+//                      permuted tokens, task token lists
+// Stable in slot order: position = offset[e] + (slots of e in earlier
+// chunks) + (in earlier waves of the chunk) + (earlier in the wave).
+constexpr int kChunkThreads = 256;
+constexpr int kChunkWaves = kChunkThreads / kWave;
+constexpr int kChunkWaveSlots = kPlanChunkSlots / kChunkWaves;
+
+__device__ __forceinline__ int slot_group(int e, bool valid, int lane, unsigned long long& peers) {
+  peers = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {  // E <= 256
+    const bool bit = valid && ((e >> b) & 1);
+    const unsigned long long mb = __ballot(bit);
+    peers &= bit ? mb : ~mb;
+  }
+  return __popcll(peers & ((1ull << lane) - 1ull));
+}
+
+// s_wc[w][e] += slots of expert e in wave w's part of chunk b
+__device__ __forceinline__ void chunk_wave_counts(const int32_t* __restrict__ idx, int S, int E, int b, int w,
+                                                  int lane, int (*s_wc)[kMaxExperts]) {
+  const int s0 = b * kPlanChunkSlots + w * kChunkWaveSlots;
+  const int s1 = min(S, s0 + kChunkWaveSlots);
+  int ev[kChunkWaveSlots / kWave];
+#pragma unroll
+  for (int i = 0; i < kChunkWaveSlots / kWave; ++i) {  // all loads in flight first
+    const int s = s0 + kWave * i + lane;
+    ev[i] = s < s1 ? idx[s] : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < kChunkWaveSlots / kWave; ++i) {
+    const bool valid = ev[i] >= 0 && ev[i] < E;
+    unsigned long long peers;
+    const int rank = slot_group(ev[i], valid, lane, peers);
+    if (valid && rank == 0) s_wc[w][ev[i]] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+__global__ __launch_bounds__(kChunkThreads) void plan_count_kernel(const int32_t* __restrict__ idx, int S, int E,
+                                                                   int32_t* __restrict__ chunk) {
+  __shared__ int s_wc[kChunkWaves][kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, b = blockIdx.x;
+  for (int i = tid; i < kChunkWaves * kMaxExperts; i += kChunkThreads) (&s_wc[0][0])[i] = 0;
+  lds_barrier();
+  chunk_wave_counts(idx, S, E, b, w, lane, s_wc);
+  lds_barrier();
+  for (int e = tid; e < E; e += kChunkThreads) {
+    int c = 0;
+#pragma unroll
+    for (int ww = 0; ww < kChunkWaves; ++ww) c += s_wc[ww][e];
+    chunk[static_cast<size_t>(b) * E + e] = c;
+  }
+}
+
+__global__ __launch_bounds__(kMaxExperts) void plan_scan_kernel(int NB, int E, int32_t* __restrict__ chunk,
+                                                                PlanBufs p) {
+  __shared__ unsigned long long s_mask[kMaxExperts / kWave];
+  __shared__ int s_wsum[kMaxExperts / kWave];
+  const int tid = threadIdx.x, lane = tid & 63, warp = tid >> 6;
+  int c = 0;
+  if (tid < E) {
+    int v[8];
+    for (int b0 = 0; b0 < NB; b0 += 8) {  // eight chunk counts in flight at a time
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = b0 + u < NB ? chunk[static_cast<size_t>(b0 + u) * E + tid] : 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (b0 + u < NB) {
+          chunk[static_cast<size_t>(b0 + u) * E + tid] = c;
+          c += v[u];
+        }
+    }
+  }
+  int incl = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) s_wsum[warp] = incl;
+  const bool act = tid < E && c > 0;
+  const unsigned long long am = __ballot(act);
+  if (lane == 0) s_mask[warp] = am;
+  __syncthreads();
+  int nact = 0, base = 0, abase = 0;
+#pragma unroll
+  for (int w = 0; w < kMaxExperts / kWave; ++w) {
+    nact += __popcll(s_mask[w]);
+    if (w < warp) {
+      base += s_wsum[w];
+      abase += __popcll(s_mask[w]);
+    }
+  }
+  const int excl = base + incl - c;
+  if (tid < E) {
+    p.counts[tid] = c;
+    p.offsets[tid] = excl;
+    if (tid == E - 1) p.offsets[E] = excl + c;
+  }
+  const int aidx = abase + __popcll(am & ((1ull << lane) - 1ull));
+  if (tid < E) chunk[static_cast<size_t>(NB) * E + tid] = act ? aidx : -1;
+  if (act) {
+    p.active[aidx] = tid;
+    if (p.tasks) {
+      int32_t* t = p.tasks + static_cast<size_t>(aidx) * kTaskInts;
+      t[0] = tid;
+      t[1] = excl;
+      t[2] = c;
+      t[3] = 0;
+    }
+  }
+  if (p.tasks && tid < E && tid >= nact) p.tasks[static_cast<size_t>(tid) * kTaskInts] = -1;
+  if (tid == 0) *p.n_active = nact;
+}
+
+__global__ __launch_bounds__(kChunkThreads) void plan_place_kernel(const int32_t* __restrict__ idx, int S, int k,
+                                                                   int E, const int32_t* __restrict__ chunk,
+                                                                   PlanBufs p) {
+  __shared__ int s_wc[kChunkWaves][kMaxExperts];  // counts, then the waves' bases
+  __shared__ int s_off[kMaxExperts], s_aidx[kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, b = blockIdx.x;
+  const int NB = (S + kPlanChunkSlots - 1) / kPlanChunkSlots;
+  for (int i = tid; i < kChunkWaves * kMaxExperts; i += kChunkThreads) (&s_wc[0][0])[i] = 0;
+  lds_barrier();
+  chunk_wave_counts(idx, S, E, b, w, lane, s_wc);
+  lds_barrier();
+  for (int e = tid; e < E; e += kChunkThreads) {
+    int base = chunk[static_cast<size_t>(b) * E + e];
+#pragma unroll
+    for (int ww = 0; ww < kChunkWaves; ++ww) {
+      const int v = s_wc[ww][e];
+      s_wc[ww][e] = base;
+      base += v;
+    }
+    s_off[e] = p.offsets[e];
+    s_aidx[e] = chunk[static_cast<size_t>(NB) * E + e];
+  }
+  lds_barrier();
+  const int s0 = b * kPlanChunkSlots + w * kChunkWaveSlots;
+  const int s1 = min(S, s0 + kChunkWaveSlots);
+  int ev[kChunkWaveSlots / kWave];
+#pragma unroll
+  for (int i = 0; i < kChunkWaveSlots / kWave; ++i) {
+    const int s = s0 + kWave * i + lane;
+    ev[i] = s < s1 ? idx[s] : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < kChunkWaveSlots / kWave; ++i) {
+    const int s = s0 + kWave * i + lane;
+    const int e = ev[i];
+    const bool valid = e >= 0 && e < E;
+    unsigned long long peers;
+    const int rank = slot_group(e, valid, lane, peers);
+    if (valid) {
+      const int r = s_wc[w][e] + rank;  // rank of the slot within its expert
+      const int pos = s_off[e] + r;
+      p.gather_map[s] = pos;
+      p.perm_token[pos] = s / k;
+      if (p.tasks && r < kTaskTokens) p.tasks[static_cast<size_t>(s_aidx[e]) * kTaskInts + 4 + r] = s / k;
+    } else if (s < s1) {
+      p.gather_map[s] = -1;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (valid && rank == 0) s_wc[w][e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // staged: the T k indices are copied to (dynamic) LDS first, so the ranking
 // rounds of build_plan, separated by barriers, read LDS instead of waiting
 // on global loads one round at a time.
@@ -691,6 +870,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* idx, 
 hipError_t launch_plan_kernel(const int32_t* idx, int T, int k, int E, PlanBufs plan, hipStream_t s,
                               const KernelTimer& timer) {
   const int S = T * k;
+  if (plan.chunk != nullptr && S > kPlanChunkSlots) {  // three launches over the device
+    const int NB = (S + kPlanChunkSlots - 1) / kPlanChunkSlots;
+    gx_launch(plan_count_kernel, dim3(NB), dim3(kChunkThreads), 0, s, KernelTimer{timer.start, nullptr}, idx, S, E,
+              plan.chunk);
+    gx_launch(plan_scan_kernel, dim3(1), dim3(kMaxExperts), 0, s, KernelTimer{}, NB, E, plan.chunk, plan);
+    gx_launch(plan_place_kernel, dim3(NB), dim3(kChunkThreads), 0, s, KernelTimer{nullptr, timer.stop}, idx, S, k,
+              E, static_cast<const int32_t*>(plan.chunk), plan);
+    return hipGetLastError();
+  }
   const int staged = S <= kPlanStageMaxSlots ? 1 : 0;
   const size_t lds = staged ? static_cast<size_t>(S) * 4 : 0;
   if (lds > 0) {

@@ -284,3 +284,37 @@ def test_gptoss120b_prefill_zipf_4096(gpu, orc, torch_mod, zipf120):
     check_layer_out(out_mc[sel], ref, "zipf T=4096 matrix core vs oracle (32 tokens)")
     out_mc2 = host(pre.layer.forward_routed(dx, di, dw, residual=dr))
     assert np.array_equal(out_mc, out_mc2)  # run-to-run deterministic
+
+
+@pytest.mark.parametrize("T", [300, 2000])
+def test_layer_plan_many_slots(gpu, orc, torch_mod, T):
+    """The layer's plan for more than 1024 slots (three launches over the
+    device: per-chunk counts, scan, placement) against the oracle's counting
+    sort, array by array: counts, offsets, stable gather map, permuted tokens
+    and the active list, with dropped slots (-1 and >= E)."""
+    torch = torch_mod
+    E, k, H, I = 128, 4, 128, 128
+    w = moe_data.make_layer(70 + T, E, H, I)
+    rng = np.random.default_rng(T)
+    z = rng.zipf(1.3, size=(T, 64)) % E  # skewed, with repeats removed per token below
+    idx = np.empty((T, k), np.int32)
+    for t in range(T):
+        u = list(dict.fromkeys(z[t].tolist()))
+        idx[t] = (u + [e for e in range(E) if e not in u])[:k]
+    idx[::7, 1] = -1
+    idx[::11, 3] = E + 5
+    wt = np.full((T, k), 0.25, np.float32)
+    x, res = moe_data.make_tokens(70 + T, T, H)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T, exact=False)
+    L.layer.forward_routed(dev(x, torch), dev(idx, torch), dev(wt, torch), residual=dev(res, torch))
+    torch.cuda.synchronize()
+    tr = L.layer.trace()
+    rd = lambda ptr, n: gpu.copy_device_to_tensor(ptr, n * 4, torch.int32).cpu().numpy()  # noqa: E731
+    r = orc.plan(idx, E)
+    assert np.array_equal(rd(tr.expert_counts, E), r["counts"])
+    assert np.array_equal(rd(tr.expert_offsets, E + 1), r["offsets"])
+    assert np.array_equal(rd(tr.gather_map, T * k), r["gather_map"])
+    nv = int(((idx >= 0) & (idx < E)).sum())
+    assert np.array_equal(rd(tr.perm_token, T * k)[:nv], r["perm_token"][:nv])
+    n = int(rd(tr.n_active, 1)[0])
+    assert n == r["n_active"] and np.array_equal(rd(tr.active_experts, E)[:n], r["active"])
