@@ -215,24 +215,37 @@ def zipf_routing(seed: int, T: int, k: int, s: float = 1.1):
     return idx, (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
 
 
-def timed_events(torch, fn, reps: int):
-    """Mean ms of fn() over reps on the current stream (HIP events)."""
+def timed_graph(torch, fn, per_graph: int = 5, replays: int = 4):
+    """Mean ms of fn() from replays of a hipGraph holding per_graph calls,
+    after one untimed replay: steady state, without the clock ramp of the
+    first calls after the device idles."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
     fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for _ in range(per_graph):
+            fn()
+    graph.replay()
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(reps):
-        fn()
-    t1.record()
+    with torch.cuda.stream(s):
+        t0.record(s)
+        for _ in range(replays):
+            graph.replay()
+        t1.record(s)
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / reps
+    del graph
+    return t0.elapsed_time(t1) / (per_graph * replays)
 
 
 def bench_prefill(g, torch, wc, T: int = 4096, reps: int = 5):
     """one GPT-OSS-120B layer forward at T tokens with
     Zipf(1.1) routing injected (forward_routed: plan, grouped gate_up + SwiGLU
-    and grouped down on the matrix cores, combine)."""
+    and grouped down on the matrix cores, combine), timed by graph replay;
+    per-launch times from HIP events on eager forwards."""
     idx, wt = zipf_routing(4096, T, K_TOP)
     cfg = g.default_config(E, T)
     L = g.MoELayer().init(cfg, 0, wc["router_w"], wc["router_b"], wc["b1"], wc["b2"], tiled=wc["tiled"])
@@ -243,7 +256,9 @@ def bench_prefill(g, torch, wc, T: int = 4096, reps: int = 5):
     di = torch.from_numpy(idx).cuda()
     dw = torch.from_numpy(wt).cuda()
     out = torch.empty_like(x)
-    ms = timed_events(torch, lambda: L.forward_routed(x, di, dw, residual=r, out=out), reps)
+    ms = timed_graph(torch, lambda: L.forward_routed(x, di, dw, residual=r, out=out), per_graph=reps)
+    for _ in range(reps):  # warm, then the per-launch events of `reps` eager forwards
+        L.forward_routed(x, di, dw, residual=r, out=out)
     L.set_profiling(reps)
     for _ in range(reps):
         L.forward_routed(x, di, dw, residual=r, out=out)
@@ -274,8 +289,8 @@ def bench_router(g, torch, T: int = 4096, reps: int = 20):
     logits = torch.empty((T, E), dtype=torch.float32, device="cuda")
     idx = torch.empty((T, K_TOP), dtype=torch.int32, device="cuda")
     w = torch.empty((T, K_TOP), dtype=torch.float32, device="cuda")
-    ms = timed_events(torch, lambda: g.route(x, W, b, K_TOP, logits_fp32=True, out=(logits, idx, w),
-                                             scratch=scratch), reps)
+    ms = timed_graph(torch, lambda: g.route(x, W, b, K_TOP, logits_fp32=True, out=(logits, idx, w),
+                                            scratch=scratch), per_graph=10, replays=reps // 10 or 1)
     nbytes = T * H * 2 + E * H * 2 + E * 2 + T * E * 4 + 2 * T * K_TOP * 4
     return dict(tokens=T, logits="fp32", us=ms * 1e3, tokens_per_s=T / (ms / 1e3), algorithmic_bytes=nbytes,
                 gbs=nbytes / (ms / 1e3) / 1e9)
