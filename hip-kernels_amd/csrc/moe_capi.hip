@@ -370,7 +370,7 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
 // One allocation with every weight of the layer (the checkpoint reader
 // fills it and tiles the experts), then the borrowed-tiled init over it; the
 // layer takes the allocation over.
-int gptoss_moe_layer_init_from_checkpoint(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
+static int gptoss_moe_layer_init_from_checkpoint_impl(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
                                           const gptoss_checkpoint* ckpt, int layer_index) {
   if (L == nullptr || cfg == nullptr || ckpt == nullptr) return fail(GPTOSS_ERR_INVALID, "null argument");
   if (L->initialized) return fail(GPTOSS_ERR_STATE, "layer already initialised");
@@ -398,6 +398,11 @@ int gptoss_moe_layer_init_from_checkpoint(gptoss_moe_layer* L, const gptoss_moe_
   }
   L->owned.push_back(blob);
   return ok();
+}
+
+int gptoss_moe_layer_init_from_checkpoint(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
+                                          const gptoss_checkpoint* ckpt, int layer_index) {
+  return guarded([&] { return gptoss_moe_layer_init_from_checkpoint_impl(L, cfg, device_id, ckpt, layer_index); });
 }
 
 // Timing of one profiled forward (gptoss_moe_layer_set_profiling): launch i

@@ -392,7 +392,14 @@ void copy_pieces(const std::vector<Piece>& pieces) {
     return;
   }
   std::vector<std::thread> th;
-  for (size_t t = 0; t < nt; ++t) th.emplace_back(run, total * t / nt, total * (t + 1) / nt);
+  size_t started = 0;
+  try {
+    th.reserve(nt);
+    for (; started < nt; ++started) th.emplace_back(run, total * started / nt, total * (started + 1) / nt);
+  } catch (...) {
+    // fewer threads than asked for: this thread copies the ranges not handed out
+  }
+  for (size_t t = started; t < nt; ++t) run(total * t / nt, total * (t + 1) / nt);
   for (std::thread& t : th) t.join();
 }
 
@@ -717,7 +724,7 @@ int upload_experts(Staging& st, const ExpertSource& src, int E, int N, int K, ui
 
 extern "C" {
 
-int gptoss_checkpoint_open(const char* path, gptoss_checkpoint** out) {
+static int gptoss_checkpoint_open_impl(const char* path, gptoss_checkpoint** out) {
   if (path == nullptr || out == nullptr) return set_error(GPTOSS_ERR_INVALID, "null argument");
   *out = nullptr;
   struct stat st;
@@ -736,20 +743,20 @@ int gptoss_checkpoint_open(const char* path, gptoss_checkpoint** out) {
   } else {
     files.push_back(path);
   }
-  gptoss_checkpoint* ck = new (std::nothrow) gptoss_checkpoint();
-  if (!ck) return set_error(GPTOSS_ERR_OOM, "out of host memory");
+  std::unique_ptr<gptoss_checkpoint> ck(new gptoss_checkpoint());
   for (const std::string& f : files) {
-    const int rc = open_shard(ck, f);
-    if (rc != GPTOSS_OK) {
-      delete ck;
-      return rc;
-    }
+    const int rc = open_shard(ck.get(), f);
+    if (rc != GPTOSS_OK) return rc;
   }
   // name -> tensor; a later shard's entry replaces an earlier one
   for (size_t i = 0; i < ck->tensors.size(); ++i) ck->index[ck->tensors[i].name] = static_cast<int>(i);
-  *out = ck;
+  *out = ck.release();
   clear_error();
   return GPTOSS_OK;
+}
+
+int gptoss_checkpoint_open(const char* path, gptoss_checkpoint** out) {
+  return guarded([&] { return gptoss_checkpoint_open_impl(path, out); });
 }
 
 void gptoss_checkpoint_close(gptoss_checkpoint* ckpt) { delete ckpt; }
@@ -777,13 +784,18 @@ int gptoss_checkpoint_tensor_at(const gptoss_checkpoint* ckpt, int i, gptoss_ten
   return GPTOSS_OK;
 }
 
-int gptoss_checkpoint_find(const gptoss_checkpoint* ckpt, const char* name, gptoss_tensor_info* info) {
+static int gptoss_checkpoint_find_impl(const gptoss_checkpoint* ckpt, const char* name,
+                                       gptoss_tensor_info* info) {
   if (!ckpt || !name) return set_error(GPTOSS_ERR_INVALID, "null argument");
   const Tensor* t = ckpt->find(name);
   if (!t) return set_error(GPTOSS_ERR_NOT_FOUND, "tensor '%s' not found", name);
   if (info) fill_info(ckpt, *t, info);
   clear_error();
   return GPTOSS_OK;
+}
+
+int gptoss_checkpoint_find(const gptoss_checkpoint* ckpt, const char* name, gptoss_tensor_info* info) {
+  return guarded([&] { return gptoss_checkpoint_find_impl(ckpt, name, info); });
 }
 
 int gptoss_checkpoint_set_staging_bytes(gptoss_checkpoint* ckpt, size_t bytes) {
@@ -894,24 +906,30 @@ int ckpt_upload_layer(const LayerSource* src, void** blob, gptoss_moe_weights* w
   const size_t o_w2n = take(g2.nib_bytes * E), o_w2s = take(g2.scale_bytes * E);
   const size_t o_rw = take(v_rw.size() * 2), o_rb = take(v_rb.size() * 2), o_nw = take(v_nw.size() * 2);
   const size_t o_b1 = take(v_b1.size() * 2), o_b2 = take(v_b2.size() * 2);
-  uint8_t* base = nullptr;
-  hipError_t e = hipMalloc(reinterpret_cast<void**>(&base), off);
-  if (e != hipSuccess) return set_error(GPTOSS_ERR_OOM, "hipMalloc(%zu) for the layer weights: %s", off, hipGetErrorString(e));
+  struct DeviceBlob {  // freed unless handed to the caller (error returns, exceptions)
+    uint8_t* p = nullptr;
+    ~DeviceBlob() {
+      if (p) (void)hipFree(p);
+    }
+  } blob_guard;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&blob_guard.p), off);
+  if (e != hipSuccess)
+    return set_error(GPTOSS_ERR_OOM, "hipMalloc(%zu) for the layer weights: %s", off, hipGetErrorString(e));
+  uint8_t* const base = blob_guard.p;
 
   struct Small {
     size_t off;
     const std::vector<uint16_t>* v;
   } smalls[] = {{o_rw, &v_rw}, {o_rb, &v_rb}, {o_nw, &v_nw}, {o_b1, &v_b1}, {o_b2, &v_b2}};
   for (const Small& s : smalls)
-    if (e == hipSuccess && !s.v->empty()) e = hipMemcpy(base + s.off, s.v->data(), s.v->size() * 2, hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    (void)hipFree(base);
-    return set_error(GPTOSS_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
-  }
+    if (e == hipSuccess && !s.v->empty())
+      e = hipMemcpy(base + s.off, s.v->data(), s.v->size() * 2, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return set_error(GPTOSS_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
 
   {
-    const size_t per1 = align_up(static_cast<size_t>(2 * I) * H / 2, 256) + align_up(static_cast<size_t>(2 * I) * H / 32, 256);
-    const size_t per2 = align_up(static_cast<size_t>(H) * I / 2, 256) + align_up(static_cast<size_t>(H) * I / 32, 256);
+    const size_t n1 = static_cast<size_t>(2 * I) * H, n2 = static_cast<size_t>(H) * I;
+    const size_t per1 = align_up(n1 / 2, 256) + align_up(n1 / 32, 256);
+    const size_t per2 = align_up(n2 / 2, 256) + align_up(n2 / 32, 256);
     const gptoss_checkpoint* ck = src->ck;
     const size_t want = std::max({ck->staging, per1, per2});
     // slots hold whole experts: no more than the larger matrix's experts need
@@ -920,19 +938,18 @@ int ckpt_upload_layer(const LayerSource* src, void** blob, gptoss_moe_weights* w
     int device = 0;
     e = hipGetDevice(&device);
     Staging* st = e == hipSuccess ? ck->staging_for(device, slot, &e) : nullptr;
-    if (st == nullptr) {
-      (void)hipFree(base);
+    if (st == nullptr)
       return set_error(GPTOSS_ERR_OOM, "staging buffers (2 x %zu bytes): %s", slot, hipGetErrorString(e));
-    }
     st->pending[0] = st->pending[1] = false;  // the previous load ended with a stream sync
+    struct StreamSync {  // the repack launches end before the blob can be freed on any way out
+      hipStream_t s;
+      ~StreamSync() { (void)hipStreamSynchronize(s); }
+    } drain{st->stream};
     rc = upload_experts(*st, src->s1, E, 2 * I, H, base + o_w1n, base + o_w1s);
     if (rc == GPTOSS_OK) rc = upload_experts(*st, src->s2, E, H, I, base + o_w2n, base + o_w2s);
     e = hipStreamSynchronize(st->stream);
     if (rc == GPTOSS_OK && e != hipSuccess) rc = set_error(GPTOSS_ERR_HIP, "expert upload: %s", hipGetErrorString(e));
-    if (rc != GPTOSS_OK) {
-      (void)hipFree(base);
-      return rc;
-    }
+    if (rc != GPTOSS_OK) return rc;
   }
 
   *wt = gptoss_moe_weights{};
@@ -945,7 +962,8 @@ int ckpt_upload_layer(const LayerSource* src, void** blob, gptoss_moe_weights* w
   wt->mlp1_tiled_scales = base + o_w1s;
   wt->mlp2_tiled_nibbles = base + o_w2n;
   wt->mlp2_tiled_scales = base + o_w2s;
-  *blob = base;
+  *blob = blob_guard.p;
+  blob_guard.p = nullptr;
   return GPTOSS_OK;
 }
 

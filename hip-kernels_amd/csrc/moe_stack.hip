@@ -14,6 +14,7 @@
 
 #include <cstdint>
 #include <map>
+#include <memory>
 #include <new>
 #include <vector>
 
@@ -133,60 +134,53 @@ int finish_create(gptoss_moe_stack* st) {
 
 extern "C" {
 
-int gptoss_moe_stack_create(const gptoss_moe_config* cfg, int device_id, const gptoss_checkpoint* ckpt,
-                            int first_layer, int num_layers, gptoss_moe_stack** out) {
+static int gptoss_moe_stack_create_impl(const gptoss_moe_config* cfg, int device_id, const gptoss_checkpoint* ckpt,
+                                        int first_layer, int num_layers, gptoss_moe_stack** out) {
   if (!cfg || !ckpt || !out) return set_error(GPTOSS_ERR_INVALID, "null argument");
   *out = nullptr;
   if (num_layers < 1 || first_layer < 0)
     return set_error(GPTOSS_ERR_INVALID, "layers [%d, %d + %d) is empty or negative", first_layer, first_layer,
                      num_layers);
-  gptoss_moe_stack* st = new (std::nothrow) gptoss_moe_stack();
-  if (!st) return set_error(GPTOSS_ERR_OOM, "out of host memory");
+  std::unique_ptr<gptoss_moe_stack> st(new gptoss_moe_stack());
   st->owns_layers = true;
   for (int l = 0; l < num_layers; ++l) {
     gptoss_moe_layer* L = gptoss_moe_layer_create();
-    if (!L) {
-      delete st;
-      return set_error(GPTOSS_ERR_OOM, "out of host memory");
-    }
+    if (!L) return set_error(GPTOSS_ERR_OOM, "out of host memory");
     st->layers.push_back(L);
     const int rc = gptoss_moe_layer_init_from_checkpoint(L, cfg, device_id, ckpt, first_layer + l);
-    if (rc != GPTOSS_OK) {
-      delete st;
-      return rc;  // the message names the layer's tensor
-    }
+    if (rc != GPTOSS_OK) return rc;  // the message names the layer's tensor
   }
-  const int rc = finish_create(st);
-  if (rc != GPTOSS_OK) {
-    delete st;
-    return rc;
+  const int rc = finish_create(st.get());
+  if (rc != GPTOSS_OK) return rc;
+  *out = st.release();
+  clear_error();
+  return GPTOSS_OK;
+}
+
+int gptoss_moe_stack_create(const gptoss_moe_config* cfg, int device_id, const gptoss_checkpoint* ckpt,
+                            int first_layer, int num_layers, gptoss_moe_stack** out) {
+  return guarded([&] { return gptoss_moe_stack_create_impl(cfg, device_id, ckpt, first_layer, num_layers, out); });
+}
+
+static int gptoss_moe_stack_create_from_layers_impl(gptoss_moe_layer* const* layers, int num_layers,
+                                                    gptoss_moe_stack** out) {
+  if (!layers || !out) return set_error(GPTOSS_ERR_INVALID, "null argument");
+  *out = nullptr;
+  if (num_layers < 1) return set_error(GPTOSS_ERR_INVALID, "num_layers=%d must be >= 1", num_layers);
+  std::unique_ptr<gptoss_moe_stack> st(new gptoss_moe_stack());
+  for (int l = 0; l < num_layers; ++l) {
+    if (!layers[l]) return set_error(GPTOSS_ERR_INVALID, "layer %d is NULL", l);
+    st->layers.push_back(layers[l]);
   }
-  *out = st;
+  const int rc = finish_create(st.get());
+  if (rc != GPTOSS_OK) return rc;
+  *out = st.release();
   clear_error();
   return GPTOSS_OK;
 }
 
 int gptoss_moe_stack_create_from_layers(gptoss_moe_layer* const* layers, int num_layers, gptoss_moe_stack** out) {
-  if (!layers || !out) return set_error(GPTOSS_ERR_INVALID, "null argument");
-  *out = nullptr;
-  if (num_layers < 1) return set_error(GPTOSS_ERR_INVALID, "num_layers=%d must be >= 1", num_layers);
-  gptoss_moe_stack* st = new (std::nothrow) gptoss_moe_stack();
-  if (!st) return set_error(GPTOSS_ERR_OOM, "out of host memory");
-  for (int l = 0; l < num_layers; ++l) {
-    if (!layers[l]) {
-      delete st;
-      return set_error(GPTOSS_ERR_INVALID, "layer %d is NULL", l);
-    }
-    st->layers.push_back(layers[l]);
-  }
-  const int rc = finish_create(st);
-  if (rc != GPTOSS_OK) {
-    delete st;
-    return rc;
-  }
-  *out = st;
-  clear_error();
-  return GPTOSS_OK;
+  return guarded([&] { return gptoss_moe_stack_create_from_layers_impl(layers, num_layers, out); });
 }
 
 int gptoss_moe_stack_io(gptoss_moe_stack* st, uint16_t** residual, uint16_t** deltas, int* max_tokens,
@@ -225,8 +219,8 @@ int gptoss_moe_stack_layer(gptoss_moe_stack* st, int index, gptoss_moe_layer** l
   return GPTOSS_OK;
 }
 
-int gptoss_moe_stack_decode_step(gptoss_moe_stack* st, int T, gptoss_layer_hook hook, void* user, int use_graph,
-                                 void* stream) {
+static int gptoss_moe_stack_decode_step_impl(gptoss_moe_stack* st, int T, gptoss_layer_hook hook, void* user,
+                                             int use_graph, void* stream) {
   if (!st) return set_error(GPTOSS_ERR_INVALID, "stack is NULL");
   if (T < 0 || T > st->max_tokens)
     return set_error(GPTOSS_ERR_INVALID, "num_tokens=%d outside [0, max_tokens=%d]", T, st->max_tokens);
@@ -275,6 +269,11 @@ int gptoss_moe_stack_decode_step(gptoss_moe_stack* st, int T, gptoss_layer_hook 
   if (e != hipSuccess) return set_error(GPTOSS_ERR_HIP, "hipGraphLaunch: %s", hipGetErrorString(e));
   clear_error();
   return GPTOSS_OK;
+}
+
+int gptoss_moe_stack_decode_step(gptoss_moe_stack* st, int T, gptoss_layer_hook hook, void* user, int use_graph,
+                                 void* stream) {
+  return guarded([&] { return gptoss_moe_stack_decode_step_impl(st, T, hook, user, use_graph, stream); });
 }
 
 void gptoss_moe_stack_destroy(gptoss_moe_stack* st) { delete st; }
