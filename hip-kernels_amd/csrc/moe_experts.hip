@@ -495,16 +495,28 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* __restric
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int s = 0; s < k; ++s) {
-    const int gm = gather_map[t * k + s];
-    if (gm < 0) continue;
-    const float ws = w[t * k + s];
-    const uint4 v = *reinterpret_cast<const uint4*>(y + static_cast<size_t>(gm) * H + c * 8);
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+  // every slot's map entry and weight, then every expert row, in flight at
+  // once (two dependent round trips in all, not two per slot)
+  int gm[kMaxTopK];
+  float ws[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    gm[s] = s < k ? gather_map[t * k + s] : -1;
+    ws[s] = s < k ? w[t * k + s] : 0.0f;
+  }
+  uint4 v[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s)
+    v[s] = gm[s] >= 0 ? *reinterpret_cast<const uint4*>(y + static_cast<size_t>(gm[s]) * H + c * 8)
+                      : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    if (gm[s] < 0) continue;  // dropped slot (or s >= k): nothing added, as the reference skips it
+    const uint32_t d[4] = {v[s].x, v[s].y, v[s].z, v[s].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = __builtin_fmaf(ws, __uint_as_float(d[i] << 16), acc[2 * i]);
-      acc[2 * i + 1] = __builtin_fmaf(ws, __uint_as_float(d[i] & 0xffff0000u), acc[2 * i + 1]);
+      acc[2 * i] = __builtin_fmaf(ws[s], __uint_as_float(d[i] << 16), acc[2 * i]);
+      acc[2 * i + 1] = __builtin_fmaf(ws[s], __uint_as_float(d[i] & 0xffff0000u), acc[2 * i + 1]);
     }
   }
   if (residual != nullptr) {
