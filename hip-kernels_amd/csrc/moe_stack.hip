@@ -70,7 +70,7 @@ struct gptoss_moe_stack {
   }
   ~gptoss_moe_stack() {
     DeviceScope ds(device);
-    if (capture) (void)hipStreamSynchronize(capture);
+    (void)hipDeviceSynchronize();  // replays still running on the callers' streams end first
     for (auto& kv : graphs) drop(kv.second);
     if (capture) (void)hipStreamDestroy(capture);
     if (own_residual) (void)hipFree(own_residual);
@@ -200,7 +200,7 @@ int gptoss_moe_stack_bind(gptoss_moe_stack* st, uint16_t* residual, uint16_t* de
     return set_error(GPTOSS_ERR_INVALID, "residual and deltas must be 16-byte aligned");
   {
     DeviceScope ds(st->device);
-    if (st->capture) (void)hipStreamSynchronize(st->capture);
+    (void)hipDeviceSynchronize();  // replays still running end before their graphs go
     for (auto& kv : st->graphs) gptoss_moe_stack::drop(kv.second);  // they hold the old pointers
     st->graphs.clear();
   }

@@ -227,7 +227,8 @@ int gptoss_moe_stack_create_from_layers(gptoss_moe_layer* const* layers, int num
 int gptoss_moe_stack_io(gptoss_moe_stack* stack, uint16_t** residual, uint16_t** deltas, int* max_tokens,
                         int* num_layers);
 /* Step on caller-owned buffers of the same shapes instead (NULL: back to the
- * stack's own); drops the captured graphs, which hold the old pointers. */
+ * stack's own); waits for the device, then drops the captured graphs, which
+ * hold the old pointers. */
 int gptoss_moe_stack_bind(gptoss_moe_stack* stack, uint16_t* residual, uint16_t* deltas);
 int gptoss_moe_stack_layer(gptoss_moe_stack* stack, int index, gptoss_moe_layer** layer);
 /* One step over every layer, ordered on `stream`.  use_graph = 1: replay
