@@ -317,3 +317,31 @@ def test_mc_one_token_dropped_slots(gpu, orc, torch_mod):
                 assert np.array_equal(out, r if r is not None else np.zeros_like(out)), case
             else:
                 check_layer_out(out, ref, f"one token {case} residual={r is not None}")
+
+
+@pytest.mark.parametrize("T", [127, 128])
+def test_mc_decode_prefill_boundary(gpu, orc, torch_mod, pair120, T):
+    """Either side of prefill_min_tokens at the GPT-OSS-120B shape: 127
+    tokens (508 slots, the largest matrix-core decode step; experts with
+    several 16-token chunks) and 128 (the grouped prefill GEMMs), against the
+    exact decode kernels on the same weights: expert indices bit-exact,
+    outputs within the tolerance, run-to-run deterministic."""
+    torch = torch_mod
+    w, ex, mc = pair120
+    layer = DeviceLayer(gpu, torch, w, E120, K120, H120, I120, max_tokens=128, exact=False, tiled=ex.tiled, t=ex.t)
+    assert layer.layer.cfg.prefill_min_tokens == 128
+    cfg = gpu.default_config(E120, 128, prefill_min_tokens=0, decode_exact=True)
+    exact = gpu.MoELayer().init(cfg, 0, ex.t["router_w"], ex.t.get("router_b"), ex.t.get("w1_bias"),
+                                ex.t.get("w2_bias"), tiled=ex.tiled)
+    x, res = moe_data.make_tokens(900 + T, T, H120)
+    dx, dr = dev(x, torch), dev(res, torch)
+    say("120B boundary T", T)
+    out = host(layer.layer.forward_prenormed(dx, dr))
+    idx = gpu.copy_device_to_tensor(layer.layer.trace().expert_indices, T * K120 * 4, torch.int32).cpu().numpy()
+    out_ex = host(exact.forward_prenormed(dx, dr))
+    idx_ex = gpu.copy_device_to_tensor(exact.trace().expert_indices, T * K120 * 4, torch.int32).cpu().numpy()
+    torch.cuda.synchronize()
+    assert np.array_equal(idx, idx_ex)
+    check_layer_out(out, out_ex, f"120B T={T} vs exact")
+    assert np.array_equal(out, host(layer.layer.forward_prenormed(dx, dr)))
+    exact.destroy()
