@@ -345,3 +345,31 @@ def test_mc_decode_prefill_boundary(gpu, orc, torch_mod, pair120, T):
     check_layer_out(out, out_ex, f"120B T={T} vs exact")
     assert np.array_equal(out, host(layer.layer.forward_prenormed(dx, dr)))
     exact.destroy()
+
+
+@pytest.mark.parametrize("k", [1, 2, 8])
+@pytest.mark.parametrize("T", [1, 8])
+def test_mc_top_k_variants_gptoss20b(gpu, orc, torch_mod, k, T):
+    """Top-k other than 4 at the GPT-OSS-20B shape (E=32, H=I=2880) on the
+    matrix-core decode path (one token: top-k and plan inside the gate_up
+    launch) against the exact path: indices and weights bit-exact, outputs
+    within the tolerance; token 0 against the oracle."""
+    torch = torch_mod
+    E, H, I = 32, 2880, 2880
+    w = moe_data.make_layer(950 + k, E, H, I, bias="random")
+    ex = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=8, via_tables=False, exact=True)
+    mc = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=8, exact=False, tiled=ex.tiled, t=ex.t)
+    x, res = moe_data.make_tokens(960 + 10 * k + T, T, H)
+    dx, dr = dev(x, torch), dev(res, torch)
+    say("20B top-k", k, "T", T)
+    out_mc = host(mc.layer.forward_prenormed(dx, dr))
+    rd = lambda L, p, n, dt: gpu.copy_device_to_tensor(p, n * 4).cpu().numpy().view(dt)  # noqa: E731
+    tr_mc = mc.layer.trace()
+    idx_mc, w_mc = rd(mc, tr_mc.expert_indices, T * k, np.int32), rd(mc, tr_mc.expert_weights, T * k, np.float32)
+    out_ex = host(ex.layer.forward_prenormed(dx, dr))
+    tr_ex = ex.layer.trace()
+    torch.cuda.synchronize()
+    assert np.array_equal(idx_mc, rd(ex, tr_ex.expert_indices, T * k, np.int32))
+    assert np.array_equal(w_mc.view(np.uint32), rd(ex, tr_ex.expert_weights, T * k, np.float32).view(np.uint32))
+    check_layer_out(out_mc, out_ex, f"20B k={k} T={T} vs exact")
+    assert np.array_equal(out_ex[:1], orc.moe_forward(w, x[:1], res[:1], E, k, H, I))
