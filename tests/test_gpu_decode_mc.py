@@ -373,3 +373,37 @@ def test_mc_top_k_variants_gptoss20b(gpu, orc, torch_mod, k, T):
     assert np.array_equal(w_mc.view(np.uint32), rd(ex, tr_ex.expert_weights, T * k, np.float32).view(np.uint32))
     check_layer_out(out_mc, out_ex, f"20B k={k} T={T} vs exact")
     assert np.array_equal(out_ex[:1], orc.moe_forward(w, x[:1], res[:1], E, k, H, I))
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_mc_fp32_logits(gpu, orc, torch_mod, pair120, T):
+    """fp32 router logits (logits_fp32 = 1) on the matrix-core decode path
+    (one token: the gate_up launch selects from fp32 logits) against the
+    oracle's fp32 routing: logits and indices bit-exact, weights bit-exact,
+    outputs within the tolerance of the exact path."""
+    torch = torch_mod
+    w, ex, _ = pair120
+    cfg = gpu.default_config(E120, 8, logits_fp32=True)
+    cfg.top_k = K120
+    mc = gpu.MoELayer().init(cfg, 0, ex.t["router_w"], ex.t.get("router_b"), ex.t.get("w1_bias"),
+                             ex.t.get("w2_bias"), tiled=ex.tiled)
+    cfg_ex = gpu.default_config(E120, 8, logits_fp32=True, decode_exact=True)
+    exl = gpu.MoELayer().init(cfg_ex, 0, ex.t["router_w"], ex.t.get("router_b"), ex.t.get("w1_bias"),
+                              ex.t.get("w2_bias"), tiled=ex.tiled)
+    x, res = moe_data.make_tokens(980 + T, T, H120)
+    dx, dr = dev(x, torch), dev(res, torch)
+    out = host(mc.forward_prenormed(dx, dr))
+    tr = mc.trace()
+    rd = lambda p, n, dt: gpu.copy_device_to_tensor(p, n * 4).cpu().numpy().view(dt)  # noqa: E731
+    logits = rd(tr.logits, T * E120, np.float32).reshape(T, E120)
+    idx = rd(tr.expert_indices, T * K120, np.int32).reshape(T, K120)
+    wts = rd(tr.expert_weights, T * K120, np.float32).reshape(T, K120)
+    out_ex = host(exl.forward_prenormed(dx, dr))
+    torch.cuda.synchronize()
+    ref_logits = orc.router(x, w["router_w"], w["router_b"], logits_fp32=True)
+    assert np.array_equal(logits.view(np.uint32), ref_logits.view(np.uint32))
+    ridx, rw = orc.topk_softmax(ref_logits, K120)
+    assert np.array_equal(idx, ridx) and np.array_equal(wts.view(np.uint32), rw.view(np.uint32))
+    check_layer_out(out, out_ex, f"120B fp32 logits T={T} vs exact")
+    mc.destroy()
+    exl.destroy()
