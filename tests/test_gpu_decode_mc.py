@@ -407,3 +407,36 @@ def test_mc_fp32_logits(gpu, orc, torch_mod, pair120, T):
     check_layer_out(out, out_ex, f"120B fp32 logits T={T} vs exact")
     mc.destroy()
     exl.destroy()
+
+
+@pytest.mark.parametrize("T", [1, 2, 6])
+def test_mc_forward_residual(gpu, orc, torch_mod, pair120, T):
+    """The decode step's residual add + RMSNorm + MoE (forward_residual) on
+    the matrix-core path: one and two tokens with the norm inside the
+    router's launch (one token also routed inside gate_up), six with the
+    norm in its own launch; the new residual bit-exact with the oracle, the
+    expert indices with the exact path, outputs within the tolerance."""
+    torch = torch_mod
+    w, ex, _ = pair120
+    norm_w = moe_data.bf16(np.random.default_rng(990).normal(1.0, 0.1, H120))
+    dn = dev(norm_w, torch)
+    layers = []
+    for exact in (False, True):
+        cfg = gpu.default_config(E120, 8, decode_exact=exact)
+        cfg.top_k = K120
+        layers.append(gpu.MoELayer().init(cfg, 0, ex.t["router_w"], ex.t.get("router_b"), ex.t.get("w1_bias"),
+                                          ex.t.get("w2_bias"), moe_norm_weight=dn, tiled=ex.tiled))
+    r, d = moe_data.make_tokens(995 + T, T, H120)
+    outs, sums, idxs = [], [], []
+    for L in layers:
+        s_out = torch.empty((T, H120), dtype=torch.bfloat16, device="cuda")
+        outs.append(host(L.forward_residual(dev(r, torch), dev(d, torch), residual_out=s_out)))
+        sums.append(host(s_out))
+        idxs.append(gpu.copy_device_to_tensor(L.trace().expert_indices, T * K120 * 4, torch.int32).cpu().numpy())
+    torch.cuda.synchronize()
+    _, ref_sum = orc.residual_rmsnorm(r, d, norm_w)
+    assert np.array_equal(sums[0], ref_sum) and np.array_equal(sums[1], ref_sum)
+    assert np.array_equal(idxs[0], idxs[1])
+    check_layer_out(outs[0], outs[1], f"120B forward_residual T={T} mc vs exact")
+    for L in layers:
+        L.destroy()
