@@ -170,3 +170,22 @@ def test_stack_graph_prefill_path(gpu, torch_mod, model):
             torch.cuda.synchronize()
         assert np.array_equal(outs[0], outs[1]), i
     st.destroy()
+
+
+def test_engine_one_token_graph(gpu, orc, torch_mod, model):
+    """A one-token engine step on matrix-core layers (norm inside the
+    router's launch, routing inside gate_up) replayed from its graph: bit
+    for bit the eager step, and within the tolerance of the oracle."""
+    torch = torch_mod
+    eng = gpu.MoEEngine().init(model["path"], max_tokens=4)
+    res, deltas = _inputs(1200, 1)
+    dr = dev(res, torch)
+    dd = torch.stack([dev(d, torch) for d in deltas])
+    eager = host(eng.decode_step(dr, deltas=dd, use_graph=False))
+    for rep in range(3):
+        got = host(eng.decode_step(dr, deltas=dd, use_graph=True))
+        torch.cuda.synchronize()
+        assert np.array_equal(got, eager), rep
+    c = moe_data.compare_bf16(eager, _oracle_step(orc, model, res, deltas))
+    assert c["max_abs"] <= 2e-2 and c["mean_rel"] <= 1e-3, c
+    eng.shutdown()
