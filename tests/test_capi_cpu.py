@@ -146,3 +146,12 @@ def test_cpp_operator_shim_exports_reference_signatures():
                                    text=True).stdout.split("\n")) - {""}
     missing = REFERENCE_OPERATOR_SIGNATURES - demangled
     assert not missing, missing
+
+
+def test_bench_rejects_several_gpus():
+    """bench.py measures one GPU: --gpus above 1 exits with status 2 and says so."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "one GPU only" in r.stderr and r.stdout == ""
