@@ -155,3 +155,16 @@ def test_bench_rejects_several_gpus():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=60)
     assert r.returncode == 2 and "one GPU only" in r.stderr and r.stdout == ""
+
+
+def test_binding_fails_loudly_without_library(tmp_path):
+    """The Python binding has no CPU fallback: imported from a directory that
+    holds no built libgptoss_moe.so, it raises ImportError naming the library."""
+    import importlib.util
+    import shutil
+    src = os.path.join(ROOT, "hip-kernels_amd", "gptoss_moe.py")
+    shutil.copy(src, tmp_path / "gptoss_moe_nolib.py")
+    spec = importlib.util.spec_from_file_location("gptoss_moe_nolib", tmp_path / "gptoss_moe_nolib.py")
+    mod = importlib.util.module_from_spec(spec)
+    with pytest.raises(ImportError, match="libgptoss_moe.so is not built"):
+        spec.loader.exec_module(mod)
