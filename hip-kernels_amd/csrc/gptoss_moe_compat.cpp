@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <map>
+#include <mutex>
 #include <vector>
 
 #include "gptoss_moe.h"
@@ -15,12 +17,27 @@ namespace gptoss {
 class MoELayer {
  public:
   gptoss_moe_layer* impl = nullptr;
+  int device = -1;  // device whose shared workspace this layer holds a reference on
 };
 
 namespace {
 
 constexpr int kExperts = 128;  // ModelConfig::experts_per_gpu with ep_size 1 (config.h:20,63)
-constexpr int kDefaultMaxTokens = 256;  // ModelConfig::max_batch_size (config.h:57)
+// The engine's MoE scratch capacity (MAX_TOKENS, engine.cu:860): its prefill
+// passes up to this many tokens to moe_layer_forward (transformer.cu:494-499).
+constexpr int kDefaultMaxTokens = 8192;
+
+// One forward workspace per device, shared by every layer on it, as the
+// engine hands all its layers one set of scratch buffers (engine.cu:975-1000);
+// the engine runs a device's layers one after another on one stream.  Freed
+// with the last layer on the device.
+struct SharedWorkspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  int users = 0;
+};
+std::mutex g_ws_mu;
+std::map<int, SharedWorkspace> g_ws;
 
 [[noreturn]] void die(const char* what) {
   fprintf(stderr, "gptoss MoE: %s failed: %s\n", what, gptoss_last_error());
@@ -54,6 +71,20 @@ MoELayer* moe_layer_create() {
 void moe_layer_destroy(MoELayer* l) {
   if (l == nullptr) return;
   gptoss_moe_layer_destroy(l->impl);
+  if (l->device >= 0) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    SharedWorkspace& ws = g_ws[l->device];
+    if (--ws.users == 0) {
+      int prev = -1;
+      const bool have_prev = hipGetDevice(&prev) == hipSuccess;
+      if (hipSetDevice(l->device) == hipSuccess) {
+        (void)hipDeviceSynchronize();  // no forward on any stream may still use it
+        (void)hipFree(ws.ptr);
+      }
+      if (have_prev) (void)hipSetDevice(prev);
+      g_ws.erase(l->device);
+    }
+  }
   delete l;
 }
 
@@ -88,7 +119,38 @@ void moe_layer_init(MoELayer* layer, int, int device_id, int, EPComm*, const Cub
   w.mlp1_scales = s1.data();
   w.mlp2_packed = p2.data();
   w.mlp2_scales = s2.data();
-  check(gptoss_moe_layer_init(layer->impl, &cfg, device_id, &w), "moe_layer_init");
+  // the device's shared workspace, grown when this config needs more
+  void* ws_ptr = nullptr;
+  size_t ws_bytes = 0;
+  {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    SharedWorkspace& ws = g_ws[device_id];
+    const size_t need = gptoss_moe_layer_workspace_bytes(&cfg);
+    if (need == 0) {
+      fprintf(stderr, "gptoss MoE: moe_layer_init: invalid configuration\n");
+      abort();
+    }
+    if (ws.bytes < need) {
+      if (ws.users > 0) {
+        fprintf(stderr, "gptoss MoE: moe_layer_init: layers on device %d need %zu workspace bytes, the shared "
+                        "workspace holds %zu\n", device_id, need, ws.bytes);
+        abort();
+      }
+      int prev = -1;
+      if (hipGetDevice(&prev) != hipSuccess || hipSetDevice(device_id) != hipSuccess ||
+          hipMalloc(&ws.ptr, need) != hipSuccess) {
+        fprintf(stderr, "gptoss MoE: moe_layer_init: hipMalloc(%zu) of the shared workspace failed\n", need);
+        abort();
+      }
+      (void)hipSetDevice(prev);
+      ws.bytes = need;
+    }
+    ws.users++;
+    layer->device = device_id;
+    ws_ptr = ws.ptr;
+    ws_bytes = ws.bytes;
+  }
+  check(gptoss_moe_layer_init_with_workspace(layer->impl, &cfg, device_id, &w, ws_ptr, ws_bytes), "moe_layer_init");
 }
 
 void moe_layer_forward(MoELayer* layer, const __hip_bfloat16* input, __hip_bfloat16* output, int num_tokens,

@@ -75,6 +75,13 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// [a, a + bytes) and [b, b + bytes) share at least one byte.
+bool overlaps(const void* a, const void* b, size_t bytes) {
+  if (a == nullptr || b == nullptr || bytes == 0) return false;
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + bytes && y < x + bytes;
+}
+
 bool valid_topk(int k) { return k == 1 || k == 2 || k == 4 || k == 8; }
 
 // Shape limits of the tiled expert kernels: K a multiple of 32 with at most 16
@@ -104,6 +111,45 @@ struct ScopedDevice {
     if (changed) (void)hipSetDevice(prev);
   }
 };
+
+// The layer's per-forward scratch, carved from one workspace.  The grouped
+// kernel's tile queue sits first at a fixed offset, so layers of any shape
+// that share a workspace share one queue; it must read zero when a grouped
+// launch starts, and every launch leaves it zero.
+struct WsLayout {
+  size_t queue, logits, idx, w, counts, offsets, gmap, ptok, active, n_active, tasks, act, y, pchunk, normed,
+      sumres, total;
+};
+
+WsLayout ws_layout(const gptoss_moe_config& c) {
+  const size_t T = static_cast<size_t>(c.max_tokens), S = T * c.top_k, E = c.num_experts;
+  const size_t H = c.hidden_size, I = c.intermediate_size;
+  WsLayout l{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) & ~static_cast<size_t>(255);
+    return at;
+  };
+  l.queue = take(grouped_queue_ints() * 4);
+  l.logits = take(T * E * 4);
+  l.idx = take(S * 4);
+  l.w = take(S * 4);
+  l.counts = take(E * 4);
+  l.offsets = take((E + 1) * 4);
+  l.gmap = take(S * 4);
+  l.ptok = take(S * 4);
+  l.active = take(E * 4);
+  l.n_active = take(4);
+  l.tasks = take(E * kTaskInts * 4);
+  l.act = take(S * I * 2);
+  l.y = take(S * H * 2);
+  l.pchunk = take(plan_chunk_ints(static_cast<int>(S), static_cast<int>(E)) * 4);
+  l.normed = take(T * H * 2);
+  l.sumres = take(T * H * 2);
+  l.total = off;
+  return l;
+}
 
 }  // namespace
 
@@ -137,7 +183,7 @@ struct gptoss_moe_layer {
   uint16_t* gate_up = nullptr;
   uint16_t* normed = nullptr;
   uint16_t* sumres = nullptr;   // residual + delta of forward_residual when the caller keeps no copy
-  void* route_scratch = nullptr;
+  void* workspace = nullptr;   // per-forward scratch (owned, or borrowed and shared)
   int32_t* special1 = nullptr;  // [E] W1 / W2 scales hold e8m0 code 0 or 255
   int32_t* special2 = nullptr;
   int32_t* gqueue = nullptr;    // tile queue of the persistent grouped kernel (zeroed; left zeroed)
@@ -145,7 +191,6 @@ struct gptoss_moe_layer {
   int special_any1 = 0, special_any2 = 0;
   int num_cus = 0;
   int mc_shape[3] = {0, 0, 0};  // matrix-core decode launch shape override
-  int n_groups = 0;
   bool trace_gu = false;
   // per-launch timing (gptoss_moe_layer_set_profiling): 4 events per recorded forward
   std::vector<hipEvent_t> prof_events;
@@ -223,8 +268,8 @@ void gptoss_moe_layer_destroy(gptoss_moe_layer* layer) {
   delete layer;
 }
 
-int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
-                          const gptoss_moe_weights* wt) {
+static int layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
+                      const gptoss_moe_weights* wt, void* workspace, size_t workspace_bytes) {
   if (L == nullptr || cfg == nullptr || wt == nullptr) return fail(GPTOSS_ERR_INVALID, "null argument");
   if (L->initialized) return fail(GPTOSS_ERR_STATE, "layer already initialised");
   const int H = cfg->hidden_size, E = cfg->num_experts, k = cfg->top_k, I = cfg->intermediate_size;
@@ -248,6 +293,14 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
       return fail(GPTOSS_ERR_INVALID, "tiled weights: all four tiled buffers are required");
   } else if (!wt->mlp1_packed || !wt->mlp1_scales || !wt->mlp2_packed || !wt->mlp2_scales) {
     return fail(GPTOSS_ERR_INVALID, "expert weights missing (neither reference-layout tables nor tiled buffers)");
+  }
+
+  const WsLayout lay = ws_layout(*cfg);
+  if (workspace != nullptr) {
+    if (workspace_bytes < lay.total)
+      return fail(GPTOSS_ERR_INVALID, "workspace of %zu bytes, this config needs %zu", workspace_bytes, lay.total);
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+      return fail(GPTOSS_ERR_INVALID, "workspace must be 256-byte aligned");
   }
 
   ScopedDevice sd(device_id);
@@ -300,40 +353,35 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
     }
   }
 
-  const size_t T = static_cast<size_t>(cfg->max_tokens), S = T * k;
-  L->n_groups = static_cast<int>((T + kRouteTokensPerGroup - 1) / kRouteTokensPerGroup);
-  const size_t route_bytes = route_scratch_bytes(static_cast<int>(T), E, k);
-  void* p;
-#define ALLOC(field, type, bytes)                          \
-  if ((rc = L->alloc(&p, (bytes), #field)) != GPTOSS_OK) { \
-    L->release();                                          \
-    return rc;                                             \
-  }                                                        \
-  L->field = static_cast<type>(p);
-  ALLOC(logits, void*, T * E * 4)
-  ALLOC(idx, int32_t*, S * 4)
-  ALLOC(w, float*, S * 4)
-  ALLOC(counts, int32_t*, E * 4)
-  ALLOC(offsets, int32_t*, (E + 1) * 4)
-  ALLOC(gmap, int32_t*, S * 4)
-  ALLOC(ptok, int32_t*, S * 4)
-  ALLOC(active, int32_t*, E * 4)
-  ALLOC(n_active, int32_t*, 4)
-  ALLOC(tasks, int32_t*, static_cast<size_t>(E) * kTaskInts * 4)
-  ALLOC(act, uint16_t*, S * I * 2)
-  ALLOC(y, uint16_t*, S * H * 2)
-  ALLOC(route_scratch, void*, route_bytes)
-  ALLOC(special1, int32_t*, E * 4)
-  ALLOC(special2, int32_t*, E * 4)
-  ALLOC(gqueue, int32_t*, grouped_queue_ints() * 4)
-  ALLOC(pchunk, int32_t*, plan_chunk_ints(static_cast<int>(S), E) * 4)
-  if (L->norm_w != nullptr) {
-    ALLOC(normed, uint16_t*, T * H * 2)
-    ALLOC(sumres, uint16_t*, T * H * 2)
+  if (workspace != nullptr) {
+    L->workspace = workspace;
+  } else if ((rc = L->alloc(&L->workspace, lay.total, "forward scratch")) != GPTOSS_OK) {
+    L->release();
+    return rc;
   }
-#undef ALLOC
-  hipError_t err = hipMemset(L->route_scratch, 0, route_bytes);
-  if (err == hipSuccess) err = hipMemset(L->gqueue, 0, grouped_queue_ints() * 4);
+  char* ws = static_cast<char*>(L->workspace);
+  L->gqueue = reinterpret_cast<int32_t*>(ws + lay.queue);
+  L->logits = ws + lay.logits;
+  L->idx = reinterpret_cast<int32_t*>(ws + lay.idx);
+  L->w = reinterpret_cast<float*>(ws + lay.w);
+  L->counts = reinterpret_cast<int32_t*>(ws + lay.counts);
+  L->offsets = reinterpret_cast<int32_t*>(ws + lay.offsets);
+  L->gmap = reinterpret_cast<int32_t*>(ws + lay.gmap);
+  L->ptok = reinterpret_cast<int32_t*>(ws + lay.ptok);
+  L->active = reinterpret_cast<int32_t*>(ws + lay.active);
+  L->n_active = reinterpret_cast<int32_t*>(ws + lay.n_active);
+  L->tasks = reinterpret_cast<int32_t*>(ws + lay.tasks);
+  L->act = reinterpret_cast<uint16_t*>(ws + lay.act);
+  L->y = reinterpret_cast<uint16_t*>(ws + lay.y);
+  L->pchunk = reinterpret_cast<int32_t*>(ws + lay.pchunk);
+  L->normed = reinterpret_cast<uint16_t*>(ws + lay.normed);
+  L->sumres = reinterpret_cast<uint16_t*>(ws + lay.sumres);
+  void* p;
+  if ((rc = L->alloc(&p, E * 4, "special1")) != GPTOSS_OK) return (L->release(), rc);
+  L->special1 = static_cast<int32_t*>(p);
+  if ((rc = L->alloc(&p, E * 4, "special2")) != GPTOSS_OK) return (L->release(), rc);
+  L->special2 = static_cast<int32_t*>(p);
+  hipError_t err = hipMemset(L->gqueue, 0, grouped_queue_ints() * 4);
   if (err == hipSuccess) err = launch_special_scan(L->w1s, 2 * I, H, E, L->special1, nullptr);
   if (err == hipSuccess) err = launch_special_scan(L->w2s, H, I, E, L->special2, nullptr);
   if (err == hipSuccess) err = hipDeviceGetAttribute(&L->num_cus, hipDeviceAttributeMultiprocessorCount, device_id);
@@ -365,6 +413,24 @@ int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int
   }
   L->initialized = true;
   return ok();
+}
+
+int gptoss_moe_layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
+                          const gptoss_moe_weights* wt) {
+  return layer_init(L, cfg, device_id, wt, nullptr, 0);
+}
+
+size_t gptoss_moe_layer_workspace_bytes(const gptoss_moe_config* cfg) {
+  if (cfg == nullptr || cfg->max_tokens < 1 || cfg->num_experts < 1 || cfg->top_k < 1 || cfg->hidden_size < 1 ||
+      cfg->intermediate_size < 1)
+    return 0;
+  return ws_layout(*cfg).total;
+}
+
+int gptoss_moe_layer_init_with_workspace(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int device_id,
+                                         const gptoss_moe_weights* wt, void* workspace, size_t workspace_bytes) {
+  if (workspace == nullptr) return fail(GPTOSS_ERR_INVALID, "workspace is NULL");
+  return layer_init(L, cfg, device_id, wt, workspace, workspace_bytes);
 }
 
 // One allocation with every weight of the layer (the checkpoint reader
@@ -598,6 +664,15 @@ int gptoss_moe_layer_forward_residual(gptoss_moe_layer* L, const uint16_t* resid
   if (delta == nullptr) return fail(GPTOSS_ERR_INVALID, "null delta");
   if (!aligned16(delta) || (residual_out && !aligned16(residual_out)))
     return fail(GPTOSS_ERR_INVALID, "delta and residual_out must be 16-byte aligned");
+  // Every work-group of the router launch reads residual and delta while one
+  // of them writes residual_out, and the combine reads residual_out while it
+  // writes out: residual_out must not share memory with residual or delta,
+  // and out is either residual_out itself or apart from it.
+  const size_t rows = static_cast<size_t>(T) * L->cfg.hidden_size * sizeof(uint16_t);
+  if (overlaps(residual_out, residual, rows) || overlaps(residual_out, delta, rows))
+    return fail(GPTOSS_ERR_INVALID, "residual_out overlaps residual or delta (the sum needs its own buffer)");
+  if (out != residual_out && overlaps(out, residual_out, rows))
+    return fail(GPTOSS_ERR_INVALID, "out partially overlaps residual_out");
   ScopedDevice sd(L->device);
   if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
   return layer_forward_core(L, residual, nullptr, out, T, static_cast<hipStream_t>(stream), delta,

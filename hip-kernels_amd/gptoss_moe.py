@@ -91,6 +91,9 @@ _sig("gptoss_mxfp4_tiled_size", [_I, _I, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ
 _sig("gptoss_mxfp4_pack_tiled", [_P, _P, _I, _I, _P, _P, _P])
 _sig("gptoss_moe_layer_create", [], _P)
 _sig("gptoss_moe_layer_init", [_P, ctypes.POINTER(MoeConfig), _I, ctypes.POINTER(MoeWeights)])
+_sig("gptoss_moe_layer_workspace_bytes", [ctypes.POINTER(MoeConfig)], _SZ)
+_sig("gptoss_moe_layer_init_with_workspace", [_P, ctypes.POINTER(MoeConfig), _I, ctypes.POINTER(MoeWeights), _P,
+                                               _SZ])
 _sig("gptoss_moe_layer_forward", [_P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_prenormed", [_P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_residual", [_P, _P, _P, _P, _P, _I, _P])
@@ -149,6 +152,36 @@ def _ptr(t):
     return t.data_ptr()
 
 
+def _bad(msg: str):
+    raise ValueErrorG(GPTOSS_ERR_INVALID, msg)
+
+
+def _check_tensor(name: str, t, device: int, dtype_size: int, cols: int, rows: int | None = None,
+                  dtypes=None) -> None:
+    """A contiguous 2-D tensor on cuda:`device` with `cols` columns (and
+    `rows` rows when given) of `dtype_size`-byte elements; dtypes, when given,
+    is the set of accepted torch dtypes.  The kernels read and write raw rows
+    of that shape, so anything else is refused before the library sees it."""
+    if not isinstance(t, torch.Tensor):
+        _bad(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.dim() != 2:
+        _bad(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.shape[1] != cols or (rows is not None and t.shape[0] != rows):
+        want = f"[{rows if rows is not None else 'T'}, {cols}]"
+        _bad(f"{name} has shape {tuple(t.shape)}, expected {want}")
+    if dtypes is not None and t.dtype not in dtypes:
+        _bad(f"{name} has dtype {t.dtype}, expected one of {sorted(str(d) for d in dtypes)}")
+    if t.element_size() != dtype_size:
+        _bad(f"{name} has {t.element_size()}-byte elements, expected {dtype_size}")
+    if not t.is_contiguous():
+        _bad(f"{name} must be contiguous")
+    if t.device.type != "cuda" or t.device.index != device:
+        _bad(f"{name} is on {t.device}, the layer is on cuda:{device}")
+
+
+_BF16 = (torch.bfloat16, torch.int16, torch.uint16)
+
+
 def _stream(stream):
     if stream is None:
         return torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else None
@@ -166,6 +199,11 @@ def default_config(num_experts: int = 128, max_tokens: int = 64, logits_fp32: bo
         cfg.prefill_min_tokens = prefill_min_tokens
     cfg.decode_exact = 1 if decode_exact else 0
     return cfg
+
+
+def workspace_bytes(cfg: MoeConfig) -> int:
+    """Bytes of forward scratch a layer of this config needs (0: invalid config)."""
+    return _lib.gptoss_moe_layer_workspace_bytes(ctypes.byref(cfg))
 
 
 def tiled_size(N: int, K: int):
@@ -217,6 +255,7 @@ class MoELayer:
         self._keep = []
         self._owned = True
         self.cfg = None
+        self.device = None
 
     @classmethod
     def _borrow(cls, handle: int) -> "MoELayer":
@@ -224,13 +263,19 @@ class MoELayer:
         self = cls.__new__(cls)
         self._h, self._keep, self._owned = handle, [], False
         self.cfg = MoeConfig()
-        check(_lib.gptoss_moe_layer_get_config(handle, ctypes.byref(self.cfg), None))
+        dev = _I()
+        check(_lib.gptoss_moe_layer_get_config(handle, ctypes.byref(self.cfg), ctypes.byref(dev)))
+        self.device = dev.value
         return self
 
     def init(self, cfg: MoeConfig, device_id: int, router_weight, router_bias=None, gate_up_bias=None,
-             down_bias=None, moe_norm_weight=None, mlp1=None, mlp2=None, tiled=None) -> "MoELayer":
+             down_bias=None, moe_norm_weight=None, mlp1=None, mlp2=None, tiled=None,
+             workspace=None) -> "MoELayer":
         """mlp1/mlp2: (list of packed tensors, list of scale tensors) per expert.
-        tiled: (w1_nibbles, w1_scales, w2_nibbles, w2_scales) expert-major buffers."""
+        tiled: (w1_nibbles, w1_scales, w2_nibbles, w2_scales) expert-major buffers.
+        workspace: a device tensor of at least workspace_bytes(cfg) bytes for
+        the forward scratch, shareable by layers run one after another on one
+        stream (None: the layer allocates its own)."""
         wt = MoeWeights()
         wt.moe_norm_weight = _ptr(moe_norm_weight)
         wt.router_weight = _ptr(router_weight)
@@ -250,8 +295,15 @@ class MoELayer:
             wt.mlp1_scales = ctypes.cast(arrs[1], ctypes.POINTER(_P))
             wt.mlp2_packed = ctypes.cast(arrs[2], ctypes.POINTER(_P))
             wt.mlp2_scales = ctypes.cast(arrs[3], ctypes.POINTER(_P))
-        check(_lib.gptoss_moe_layer_init(self._h, ctypes.byref(cfg), device_id, ctypes.byref(wt)))
+        if workspace is None:
+            check(_lib.gptoss_moe_layer_init(self._h, ctypes.byref(cfg), device_id, ctypes.byref(wt)))
+        else:
+            nbytes = workspace.numel() * workspace.element_size()
+            check(_lib.gptoss_moe_layer_init_with_workspace(self._h, ctypes.byref(cfg), device_id, ctypes.byref(wt),
+                                                            _ptr(workspace), nbytes))
+            self._keep.append(workspace)
         self.cfg = cfg
+        self.device = device_id
         return self
 
     def init_from_checkpoint(self, cfg: MoeConfig, device_id: int, ckpt: "Checkpoint",
@@ -262,21 +314,36 @@ class MoELayer:
         check(_lib.gptoss_moe_layer_init_from_checkpoint(self._h, ctypes.byref(cfg), device_id, ckpt._h,
                                                          layer_index))
         self.cfg = cfg
+        self.device = device_id
         return self
+
+    def _rows(self, name: str, t, T: int | None = None) -> int:
+        """Checks a bf16 [T, hidden_size] activation tensor on the layer's
+        device; returns T."""
+        if self.cfg is None:
+            raise GptossError(GPTOSS_ERR_STATE, "layer not initialised")
+        _check_tensor(name, t, self.device, 2, self.cfg.hidden_size, T, _BF16)
+        return t.shape[0]
+
+    def _out(self, out, like, T: int):
+        if out is None:
+            return torch.empty_like(like)
+        self._rows("out", out, T)
+        return out
 
     def forward(self, x, out=None, stream=None):
         """out = x + MoE(RMSNorm(x)) (moe_layer_forward)."""
-        T = x.shape[0]
-        if out is None:
-            out = torch.empty_like(x)
+        T = self._rows("x", x)
+        out = self._out(out, x, T)
         check(_lib.gptoss_moe_layer_forward(self._h, _ptr(x), _ptr(out), T, _stream(stream)))
         return out
 
     def forward_prenormed(self, normed, residual=None, out=None, stream=None):
         """out = residual + MoE(normed) (moe_layer_forward_prenormed)."""
-        T = normed.shape[0]
-        if out is None:
-            out = torch.empty_like(normed)
+        T = self._rows("normed", normed)
+        if residual is not None:
+            self._rows("residual", residual, T)
+        out = self._out(out, normed, T)
         check(_lib.gptoss_moe_layer_forward_prenormed(self._h, _ptr(normed), _ptr(residual), _ptr(out), T,
                                                       _stream(stream)))
         return out
@@ -284,10 +351,13 @@ class MoELayer:
     def forward_residual(self, residual, delta, residual_out=None, out=None, stream=None):
         """The decode step's residual add + RMSNorm + MoE in one call:
         s = residual + delta; residual_out (optional) = bf16(s);
-        out = bf16(s) + MoE(RMSNorm(s)).  Returns out."""
-        T = residual.shape[0]
-        if out is None:
-            out = torch.empty_like(residual)
+        out = bf16(s) + MoE(RMSNorm(s)).  residual_out must not share memory
+        with residual or delta.  Returns out."""
+        T = self._rows("residual", residual)
+        self._rows("delta", delta, T)
+        if residual_out is not None:
+            self._rows("residual_out", residual_out, T)
+        out = self._out(out, residual, T)
         check(_lib.gptoss_moe_layer_forward_residual(self._h, _ptr(residual), _ptr(delta), _ptr(residual_out),
                                                      _ptr(out), T, _stream(stream)))
         return out
@@ -295,9 +365,13 @@ class MoELayer:
     def forward_routed(self, normed, expert_indices, expert_weights, residual=None, out=None, stream=None):
         """out = residual + sum_k w * FFN_idx(normed) with the routing given
         (int32 [T][k] indices, fp32 [T][k] weights, on the device)."""
-        T = normed.shape[0]
-        if out is None:
-            out = torch.empty_like(normed)
+        T = self._rows("normed", normed)
+        if residual is not None:
+            self._rows("residual", residual, T)
+        k = self.cfg.top_k
+        _check_tensor("expert_indices", expert_indices, self.device, 4, k, T, (torch.int32,))
+        _check_tensor("expert_weights", expert_weights, self.device, 4, k, T, (torch.float32,))
+        out = self._out(out, normed, T)
         check(_lib.gptoss_moe_layer_forward_routed(self._h, _ptr(normed), _ptr(residual), _ptr(expert_indices),
                                                    _ptr(expert_weights), _ptr(out), T, _stream(stream)))
         return out

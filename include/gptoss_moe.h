@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GPTOSS_MOE_ABI_VERSION 4
+#define GPTOSS_MOE_ABI_VERSION 5
 
 enum {
   GPTOSS_OK = 0,
@@ -109,8 +109,28 @@ typedef struct gptoss_moe_weights {
 } gptoss_moe_weights;
 
 gptoss_moe_layer* gptoss_moe_layer_create(void);                    /* moe_layer_create */
+/* moe_layer_init: the layer allocates its per-forward scratch for
+ * cfg->max_tokens tokens (gptoss_moe_layer_workspace_bytes bytes). */
 int gptoss_moe_layer_init(gptoss_moe_layer* layer, const gptoss_moe_config* cfg, int device_id,
                           const gptoss_moe_weights* weights);       /* moe_layer_init */
+/* Bytes of per-forward scratch (routing plan, SwiGLU activations, expert
+ * outputs, norm output) of a layer of this config, sized for
+ * cfg->max_tokens; 0 for an invalid config. */
+size_t gptoss_moe_layer_workspace_bytes(const gptoss_moe_config* cfg);
+/* moe_layer_init with the per-forward scratch in a caller-owned device buffer
+ * of device_id (at least gptoss_moe_layer_workspace_bytes(cfg) bytes,
+ * 256-byte aligned), as the reference engine hands every layer the same
+ * scratch buffers (engine.cu:975-1000, moe_layer.cu:1585-1600).  Layers whose
+ * forwards are ordered on one stream may share one workspace, whatever their
+ * configs (each needs the bytes of its own); forwards that can overlap in time
+ * need separate workspaces.  The first 1152 bytes hold a work queue that must
+ * read zero whenever no forward is running: init zeroes it and every forward
+ * leaves it zero, so nothing else may write there.  The workspace must
+ * outlive the layer; a trace (gptoss_moe_layer_trace) then shows the last
+ * forward of any layer on it. */
+int gptoss_moe_layer_init_with_workspace(gptoss_moe_layer* layer, const gptoss_moe_config* cfg, int device_id,
+                                         const gptoss_moe_weights* weights, void* workspace,
+                                         size_t workspace_bytes);
 /* out = input + MoE(RMSNorm(input))  (moe_layer_forward, moe_layer.cu:982-1005) */
 int gptoss_moe_layer_forward(gptoss_moe_layer* layer, const uint16_t* input, uint16_t* output,
                              int num_tokens, void* stream);
@@ -121,7 +141,10 @@ int gptoss_moe_layer_forward(gptoss_moe_layer* layer, const uint16_t* input, uin
  * formed in fp32; residual_out (may be NULL) receives bf16(sum); out =
  * bf16(sum) + MoE(RMSNorm(sum)).  Up to 4 tokens the norm runs inside the
  * router's launch (one launch fewer), above in a launch of its own.  Needs
- * moe_norm_weight. */
+ * moe_norm_weight.  residual_out must not overlap residual or delta (the
+ * reference double-buffers the residual stream, transformer.cu:697-701;
+ * GPTOSS_ERR_INVALID otherwise); out may equal residual, residual_out or
+ * neither, but must not partially overlap residual_out. */
 int gptoss_moe_layer_forward_residual(gptoss_moe_layer* layer, const uint16_t* residual,
                                       const uint16_t* delta, uint16_t* residual_out, uint16_t* output,
                                       int num_tokens, void* stream);
@@ -279,9 +302,10 @@ int gptoss_moe_layer_profile_read(gptoss_moe_layer* layer, float* route_ms, floa
  * gemv_bf16.cu:236-247) / gemm_bf16_lt (T > 1, cuda_utils.h:226-308) plus
  * topk_softmax_forward (topk_softmax.cu:380).  logits: [T][E] bf16 if
  * logits_fp32 == 0 else fp32 (the router output, rounded as the reference's
- * bf16 logits or kept in fp32).  `scratch` (gptoss_moe_route_scratch_bytes
- * bytes of device memory) is reserved and not read or written by this
- * version. */
+ * bf16 logits or kept in fp32).  `scratch` is reserved: it must be non-NULL
+ * (gptoss_moe_route_scratch_bytes bytes of device memory, 256 today) and is
+ * neither read nor written; routing exchanges no values between
+ * work-groups, so no workspace is needed. */
 size_t gptoss_moe_route_scratch_bytes(int num_tokens, int num_experts, int top_k);
 int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
                      int num_tokens, int num_experts, int hidden, int top_k, int logits_fp32,

@@ -11,7 +11,11 @@
 // Arguments the single-GPU path does not use are accepted and ignored:
 // layer/gpu ids, the expert-parallel communicator, the BLAS handles, the
 // second stream, the NCCL communicator and the 19 caller-owned scratch
-// buffers (the layer owns its scratch, sized for max_tokens tokens).
+// buffers.  In their place every layer of a device shares one forward
+// workspace (gptoss_moe_layer_init_with_workspace), sized for
+// moe_layer_max_tokens() tokens and freed with the device's last layer, so
+// as in the reference a device's layers must run one after another (the
+// engine runs them in order on one stream).
 #pragma once
 
 #include <hip/hip_bf16.h>
@@ -41,8 +45,9 @@ void moe_layer_destroy(MoELayer* l);
 // moe_layer.cu:1585-1615.  expert_mlp1 / expert_mlp2 are host arrays of
 // ModelConfig::experts_per_gpu (128) descriptors; gate_up rows interleave
 // gate (even) and up (odd).  Tokens per forward: at most
-// moe_layer_max_tokens() (default 256, ModelConfig::max_batch_size; the
-// environment variable GPTOSS_MOE_MAX_TOKENS overrides it before init).
+// moe_layer_max_tokens() (default 8192, the engine's MAX_TOKENS, engine.cu:
+// 860; the environment variable GPTOSS_MOE_MAX_TOKENS overrides it before
+// the first init on a device).
 void moe_layer_init(
     MoELayer* layer, int layer_id, int device_id, int gpu_id, EPComm* ep_comm,
     const CublasHandle* cublas_compute, const CublasHandle* cublas_comm, hipStream_t compute_stream,

@@ -164,45 +164,53 @@ static float butterfly64(float* v) {
 /* Restatement of fused_mxfp4_gemv_kernel's per-row arithmetic
  * (fused_mxfp4_gemv.cu:93-183): thread tid takes uint32 chunks tid, tid+256,
  * ...; per chunk dot = 0 then per byte dot += (x0*w0 + x1*w1); acc += dot;
- * remainder bytes; butterfly per 64-lane warp; val = 0 + s0 + s1 + s2 + s3;
- * + bias; bf16.  The products are exact in fp32, so FMA contraction of the
- * pair sum cannot change the result. */
+ * remainder bytes; butterfly per 64-lane warp; val = 0 + s0 + s1 + s2 + s3.
+ * The products are exact in fp32, so FMA contraction of the pair sum cannot
+ * change the result.  xr holds the bf16 inputs as fp32 values. */
+static float mx_dot_refkernel(const float* xr, const uint8_t* packed, const uint8_t* scales,
+                              int K, int n) {
+  const int KH = K >> 1, KH4 = KH >> 2;
+  float part[256];
+  for (int tid = 0; tid < 256; ++tid) {
+    float acc = 0.0f;
+    for (int kb4 = tid; kb4 < KH4; kb4 += 256) {
+      int kb = kb4 << 2, k0 = kb << 1;
+      float dot = 0.0f;
+      for (int b = 0; b < 4; ++b) {
+        int k = k0 + 2 * b;
+        float w0 = mx_weight(packed, scales, K, n, k);
+        float w1 = mx_weight(packed, scales, K, n, k + 1);
+        float pair = xr[k] * w0 + xr[k + 1] * w1;
+        dot = dot + pair;
+      }
+      acc = acc + dot;
+    }
+    for (int kb = KH4 * 4 + tid; kb < KH; kb += 256) {
+      int k0 = kb << 1;
+      float pair = xr[k0] * mx_weight(packed, scales, K, n, k0) +
+                   xr[k0 + 1] * mx_weight(packed, scales, K, n, k0 + 1);
+      acc = acc + pair;
+    }
+    part[tid] = acc;
+  }
+  float val = 0.0f;
+  for (int w = 0; w < 4; ++w) val = val + butterfly64(part + 64 * w);
+  return val;
+}
+
 void orc_mxfp4_gemv_refkernel(const uint16_t* x, int M,
                               const uint8_t* packed, const uint8_t* scales,
                               const uint16_t* bias, int N, int K, uint16_t* y) {
-  const int KH = K >> 1, KH4 = KH >> 2;
+  float* xr = (float*)malloc(sizeof(float) * (size_t)K);
   for (int m = 0; m < M; ++m) {
-    const uint16_t* xr = x + (size_t)m * K;
+    for (int k = 0; k < K; ++k) xr[k] = bf(x[(size_t)m * K + k]);
     for (int n = 0; n < N; ++n) {
-      float part[256];
-      for (int tid = 0; tid < 256; ++tid) {
-        float acc = 0.0f;
-        for (int kb4 = tid; kb4 < KH4; kb4 += 256) {
-          int kb = kb4 << 2, k0 = kb << 1;
-          float dot = 0.0f;
-          for (int b = 0; b < 4; ++b) {
-            int k = k0 + 2 * b;
-            float w0 = mx_weight(packed, scales, K, n, k);
-            float w1 = mx_weight(packed, scales, K, n, k + 1);
-            float pair = bf(xr[k]) * w0 + bf(xr[k + 1]) * w1;
-            dot = dot + pair;
-          }
-          acc = acc + dot;
-        }
-        for (int kb = KH4 * 4 + tid; kb < KH; kb += 256) {
-          int k0 = kb << 1;
-          float pair = bf(xr[k0]) * mx_weight(packed, scales, K, n, k0) +
-                       bf(xr[k0 + 1]) * mx_weight(packed, scales, K, n, k0 + 1);
-          acc = acc + pair;
-        }
-        part[tid] = acc;
-      }
-      float val = 0.0f;
-      for (int w = 0; w < 4; ++w) val = val + butterfly64(part + 64 * w);
+      float val = mx_dot_refkernel(xr, packed, scales, K, n);
       if (bias) val = val + bf(bias[n]);
       y[(size_t)m * N + n] = orc_f32_to_bf16(val);
     }
   }
+  free(xr);
 }
 
 void orc_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, int N, int K,
@@ -229,6 +237,30 @@ static float gemv_tree(const uint16_t* a, const uint16_t* b, int K) {
         acc = fmaf(bf(a[k]), bf(b[k]), acc);
       }
     for (int k = (KV << 3) + tid; k < K; k += 256) acc = fmaf(bf(a[k]), bf(b[k]), acc);
+    part[tid] = acc;
+  }
+  float val = 0.0f;
+  for (int w = 0; w < 4; ++w) val = val + butterfly64(part + 64 * w);
+  return val;
+}
+
+/* gemv_bf16_kernel (gemv_bf16.cu:48-129) over the bf16 dequantisation of an
+ * MXFP4 row (mxfp4_dequant.cu:263-350, bf16(e2m1 * (code << 23))): the
+ * reference's product for an expert with one token inside a batch that also
+ * holds experts with several (moe_layer.cu:1409-1411, 1464-1466).  Products
+ * of bf16 values are exact in fp32, so the chains' fmaf equals the kernel's
+ * multiply-add however it is contracted. */
+static float mx_dot_gemv_tree(const float* xr, const uint8_t* packed, const uint8_t* scales, int K, int n) {
+  const int KV = K >> 3;
+  float part[256];
+  for (int tid = 0; tid < 256; ++tid) {
+    float acc = 0.0f;
+    for (int kv = tid; kv < KV; kv += 256)
+      for (int i = 0; i < 8; ++i) {
+        int k = (kv << 3) + i;
+        acc = fmaf(xr[k], rbf(mx_weight(packed, scales, K, n, k)), acc);
+      }
+    for (int k = (KV << 3) + tid; k < K; k += 256) acc = fmaf(xr[k], rbf(mx_weight(packed, scales, K, n, k)), acc);
     part[tid] = acc;
   }
   float val = 0.0f;
@@ -427,6 +459,55 @@ void orc_residual_rmsnorm(const uint16_t* r, const uint16_t* d, const uint16_t* 
 /* ------------------------------------------------------------------------ */
 /* Whole layer, multi-threaded over permuted slots.                          */
 /* ------------------------------------------------------------------------ */
+/* How the product of one active expert is computed (expert_order, see
+ * moe_oracle.h). */
+enum {
+  XP_CANONICAL = 0,   /* this build's order: K-part chains, bias before the rounding */
+  XP_FAST_ONE = 1,    /* T == 1 fast path: fused GEMV order, no bias inside the GEMV */
+  XP_FUSED_BATCH = 2, /* fused GEMV with the bias inside (a batch of one-token experts) */
+  XP_GEMV_DQ = 3,     /* gemv_bf16 over the dequantised weights, then bias_add_rows */
+  XP_MULTI = 4        /* several tokens: canonical order, bf16, then bias_add_rows */
+};
+
+/* The reference's choice per active expert j (ascending expert ids): one token
+ * takes the fast path (moe_layer.cu:1028); otherwise the active experts are
+ * cut into batches of 8 in ascending order (:1282-1304), a batch whose experts
+ * all hold one token runs the fused GEMV (:1319-1323), any other batch
+ * dequantises and runs gemv_bf16 for its one-token experts and hipBLASLt for
+ * the rest (:1409-1417). */
+static void classify_experts(int T, const int32_t* offsets, const int32_t* active, int n_active, int8_t* klass) {
+  enum { kBatch = 8 };
+  for (int j0 = 0; j0 < n_active; j0 += kBatch) {
+    const int j1 = j0 + kBatch < n_active ? j0 + kBatch : n_active;
+    int all_one = 1;
+    for (int j = j0; j < j1; ++j)
+      if (offsets[active[j] + 1] - offsets[active[j]] != 1) all_one = 0;
+    for (int j = j0; j < j1; ++j) {
+      const int m = offsets[active[j] + 1] - offsets[active[j]];
+      klass[j] = (int8_t)(T == 1 ? XP_FAST_ONE : all_one ? XP_FUSED_BATCH : m == 1 ? XP_GEMV_DQ : XP_MULTI);
+    }
+  }
+}
+
+/* One output of an expert matrix in the order its class uses; the bias goes
+ * where that path adds it (b = NULL: no bias). */
+static float expert_row(int klass, const float* xr, const uint8_t* P, const uint8_t* Sc, int K, int n,
+                        const uint16_t* b, int bias_inside) {
+  float v;
+  switch (klass) {
+    case XP_FAST_ONE:
+    case XP_FUSED_BATCH: v = mx_dot_refkernel(xr, P, Sc, K, n); break;
+    case XP_GEMV_DQ: v = mx_dot_gemv_tree(xr, P, Sc, K, n); break;
+    default: v = mx_dot_canonical(xr, P, Sc, K, n); break;
+  }
+  if (b == NULL) return v;
+  if (bias_inside) return v + bf(b[n]);   /* the GEMV's own epilogue (fused_mxfp4_gemv.cu:180) */
+  return rbf(v) + bf(b[n]);               /* a bias kernel over the bf16 product (moe_layer.cu:171-183, 442-463) */
+}
+
+/* ------------------------------------------------------------------------ */
+/* Whole layer, multi-threaded over permuted slots.                          */
+/* ------------------------------------------------------------------------ */
 typedef struct {
   const orc_cfg* cfg;
   const orc_weights* wt;
@@ -434,6 +515,7 @@ typedef struct {
   const int32_t* perm_token;
   const int32_t* offsets;
   const int32_t* active;
+  const int8_t* klass;      /* [n_active] dispatch class per active expert */
   int n_active;
   int next;                 /* work counter (guarded by mu) */
   pthread_mutex_t mu;
@@ -442,7 +524,7 @@ typedef struct {
   uint16_t* y;              /* [S][H] */
 } layer_job;
 
-/* One unit of work = one (active expert, row block) pair of either phase. */
+/* One unit of work = one active expert of either phase. */
 static void* layer_worker_w1(void* arg) {
   layer_job* J = (layer_job*)arg;
   const orc_cfg* c = J->cfg;
@@ -454,6 +536,7 @@ static void* layer_worker_w1(void* arg) {
     pthread_mutex_unlock(&J->mu);
     if (j >= J->n_active) break;
     int e = J->active[j];
+    const int kl = J->klass[j];
     const uint8_t* P = J->wt->w1_packed + (size_t)e * N1 * (H / 2);
     const uint8_t* Sc = J->wt->w1_scales + (size_t)e * N1 * (H / 32);
     const uint16_t* B = J->wt->w1_bias ? J->wt->w1_bias + (size_t)e * N1 : NULL;
@@ -461,14 +544,18 @@ static void* layer_worker_w1(void* arg) {
       const uint16_t* xt = J->x + (size_t)J->perm_token[pos] * H;
       for (int h = 0; h < H; ++h) xr[h] = bf(xt[h]);
       uint16_t* gu = J->gate_up + (size_t)pos * N1;
-      for (int n = 0; n < N1; ++n) {
-        float v = mx_dot_canonical(xr, P, Sc, H, n);
-        if (B) v = v + bf(B[n]);
-        gu[n] = orc_f32_to_bf16(v);
+      /* the fast path's GEMV has no bias: it is added inside the SwiGLU */
+      const uint16_t* Bg = kl == XP_FAST_ONE ? NULL : B;
+      const int inside = kl == XP_CANONICAL || kl == XP_FUSED_BATCH;
+      for (int n = 0; n < N1; ++n) gu[n] = orc_f32_to_bf16(expert_row(kl, xr, P, Sc, H, n, Bg, inside));
+      for (int i = 0; i < I; ++i) {
+        float g = bf(gu[2 * i]), u = bf(gu[2 * i + 1]);
+        if (kl == XP_FAST_ONE && B) {      /* moe_layer.cu:345-352: bias in fp32, no rounding before */
+          g = g + bf(B[2 * i]);
+          u = u + bf(B[2 * i + 1]);
+        }
+        J->act[(size_t)pos * I + i] = orc_f32_to_bf16(orc_swiglu(g, u, c->alpha, c->limit));
       }
-      for (int i = 0; i < I; ++i)
-        J->act[(size_t)pos * I + i] = orc_f32_to_bf16(
-            orc_swiglu(bf(gu[2 * i]), bf(gu[2 * i + 1]), c->alpha, c->limit));
     }
   }
   free(xr);
@@ -486,16 +573,15 @@ static void* layer_worker_w2(void* arg) {
     pthread_mutex_unlock(&J->mu);
     if (j >= J->n_active) break;
     int e = J->active[j];
+    const int kl = J->klass[j];
     const uint8_t* P = J->wt->w2_packed + (size_t)e * H * (I / 2);
     const uint8_t* Sc = J->wt->w2_scales + (size_t)e * H * (I / 32);
     const uint16_t* B = J->wt->w2_bias ? J->wt->w2_bias + (size_t)e * H : NULL;
+    const int inside = kl == XP_CANONICAL || kl == XP_FUSED_BATCH;
     for (int pos = J->offsets[e]; pos < J->offsets[e + 1]; ++pos) {
       for (int i = 0; i < I; ++i) ar[i] = bf(J->act[(size_t)pos * I + i]);
-      for (int n = 0; n < H; ++n) {
-        float v = mx_dot_canonical(ar, P, Sc, I, n);
-        if (B) v = v + bf(B[n]);
-        J->y[(size_t)pos * H + n] = orc_f32_to_bf16(v);
-      }
+      for (int n = 0; n < H; ++n)
+        J->y[(size_t)pos * H + n] = orc_f32_to_bf16(expert_row(kl, ar, P, Sc, I, n, B, inside));
     }
   }
   free(ar);
@@ -511,6 +597,22 @@ static void run_pool(void* (*fn)(void*), layer_job* J, int nthreads) {
   free(th);
 }
 
+/* The one-token fast path's combine (moe_layer.cu:479-497): from the
+ * residual, then w_k * y_k in slot order (compiled as fma), bf16.  Slots
+ * without an expert (index -1) are skipped. */
+static void combine_fast_one(const uint16_t* y, const int32_t* gather_map, const float* w, const uint16_t* residual,
+                             int k, int H, uint16_t* out) {
+  for (int h = 0; h < H; ++h) {
+    float acc = residual ? bf(residual[h]) : 0.0f;
+    for (int s = 0; s < k; ++s) {
+      int g = gather_map[s];
+      if (g < 0) continue;
+      acc = fmaf(w[s], bf(y[(size_t)g * H + h]), acc);
+    }
+    out[h] = orc_f32_to_bf16(acc);
+  }
+}
+
 /* The expert half of the layer with the routing given (moe_layer.cu:
  * 1196-1549: permute, experts, combine); idx/w are [T][k]. */
 static void moe_experts_combine(const orc_cfg* cfg, const orc_weights* wt, const uint16_t* x,
@@ -524,11 +626,13 @@ static void moe_experts_combine(const orc_cfg* cfg, const orc_weights* wt, const
   int32_t* ptok = (int32_t*)malloc(sizeof(int32_t) * (size_t)S);
   int32_t* active = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
   int n_active = orc_plan(idx, T, k, E, counts, offsets, gmap, ptok, active);
+  int8_t* klass = (int8_t*)calloc((size_t)E, 1);
+  if (cfg->expert_order == 1) classify_experts(T, offsets, active, n_active, klass);
 
   layer_job J;
   memset(&J, 0, sizeof(J));
   J.cfg = cfg; J.wt = wt; J.x = x; J.perm_token = ptok; J.offsets = offsets;
-  J.active = active; J.n_active = n_active;
+  J.active = active; J.n_active = n_active; J.klass = klass;
   pthread_mutex_init(&J.mu, NULL);
   J.gate_up = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)S * 2 * I);
   J.act = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)S * I);
@@ -537,7 +641,8 @@ static void moe_experts_combine(const orc_cfg* cfg, const orc_weights* wt, const
   run_pool(layer_worker_w2, &J, nthreads);
   pthread_mutex_destroy(&J.mu);
 
-  orc_combine(J.y, gmap, w, residual, T, k, H, out);
+  if (cfg->expert_order == 1 && T == 1) combine_fast_one(J.y, gmap, w, residual, k, H, out);
+  else orc_combine(J.y, gmap, w, residual, T, k, H, out);
 
   if (trace) {
     if (trace->gather_map) memcpy(trace->gather_map, gmap, sizeof(int32_t) * (size_t)S);
@@ -546,7 +651,7 @@ static void moe_experts_combine(const orc_cfg* cfg, const orc_weights* wt, const
     if (trace->y) memcpy(trace->y, J.y, sizeof(uint16_t) * (size_t)S * H);
   }
   free(J.gate_up); free(J.act); free(J.y);
-  free(counts); free(offsets); free(gmap); free(ptok); free(active);
+  free(counts); free(offsets); free(gmap); free(ptok); free(active); free(klass);
 }
 
 void orc_moe_forward(const orc_cfg* cfg, const orc_weights* wt,

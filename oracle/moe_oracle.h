@@ -109,6 +109,26 @@ typedef struct {
   float alpha, limit;
   int logits_fp32;        /* 0: bf16 logits (reference), 1: fp32 logits */
   int topk_variant;       /* 0 = launcher choice by T */
+  /* Expert products and combine:
+   *   0: this build's canonical order (K-part fmaf chains, bias before the
+   *      one bf16 rounding, combine from 0 with the residual last);
+   *   1: the reference's own dispatch, orders and rounding points, per
+   *      active expert as moe_layer.cu chooses them:
+   *      - one token (fast path, moe_layer.cu:1028-1098): fused_mxfp4_gemv
+   *        order with no bias (fused_mxfp4_gemv.cu:93-183), the gate_up bias
+   *        added in fp32 inside the SwiGLU (moe_layer.cu:303-362), the down
+   *        bias after the bf16 rounding (:442-463), the combine from the
+   *        residual (:479-497);
+   *      - several tokens, a batch of 8 active experts that all hold one
+   *        token (:1319-1368): fused_mxfp4_gemv with the bias inside;
+   *      - one token in a mixed batch (:1409-1411, :1464-1466): gemv_bf16 over
+   *        the dequantised weights (gemv_bf16.cu:40-130), then bias_add_rows
+   *        (moe_layer.cu:171-183);
+   *      - several tokens (hipBLASLt, :1413-1417): rounding points as the
+   *        reference (bf16 product, then bias_add_rows) with the canonical
+   *        order standing in for hipBLASLt's (not restated: not vendored);
+   *      - combine (T > 1): moe_combine.cu:69-115, the residual last. */
+  int expert_order;
 } orc_cfg;
 
 typedef struct {

@@ -25,7 +25,7 @@ _F = ctypes.c_float
 
 class OrcCfg(ctypes.Structure):
     _fields_ = [("H", _I), ("E", _I), ("k", _I), ("I", _I), ("alpha", _F), ("limit", _F),
-                ("logits_fp32", _I), ("topk_variant", _I)]
+                ("logits_fp32", _I), ("topk_variant", _I), ("expert_order", _I)]
 
 
 class OrcWeights(ctypes.Structure):
@@ -199,11 +199,13 @@ def set_exp_mode(mode: int) -> None:
 
 
 def moe_forward(weights: dict, x, residual, E, k, H, I, alpha=1.702, limit=7.0, logits_fp32=False,
-                topk_variant=0, nthreads=0, trace=False):
+                topk_variant=0, nthreads=0, trace=False, order=0):
     """Whole MoE layer.  weights: dict with router_w, router_b, w1_packed,
-    w1_scales, w1_bias, w2_packed, w2_scales, w2_bias (numpy, expert-major)."""
+    w1_scales, w1_bias, w2_packed, w2_scales, w2_bias (numpy, expert-major).
+    order 0: this build's canonical expert order; 1: the reference's own
+    dispatch, orders and rounding points (orc_cfg.expert_order)."""
     T = x.shape[0]
-    cfg = OrcCfg(H, E, k, I, alpha, limit, 1 if logits_fp32 else 0, topk_variant)
+    cfg = OrcCfg(H, E, k, I, alpha, limit, 1 if logits_fp32 else 0, topk_variant, order)
     wt = OrcWeights(*[_ptr(weights.get(n)) for n in
                       ("router_w", "router_b", "w1_packed", "w1_scales", "w1_bias",
                        "w2_packed", "w2_scales", "w2_bias")])
@@ -226,11 +228,11 @@ def moe_forward(weights: dict, x, residual, E, k, H, I, alpha=1.702, limit=7.0, 
 
 
 def moe_forward_routed(weights: dict, x, residual, idx, w, E, k, H, I, alpha=1.702, limit=7.0, nthreads=0,
-                       trace=False):
+                       trace=False, order=0):
     """The layer's expert half with the routing given (idx int32 [T][k],
     w float32 [T][k]); weights as moe_forward (router entries unused)."""
     T = x.shape[0]
-    cfg = OrcCfg(H, E, k, I, alpha, limit, 0, 0)
+    cfg = OrcCfg(H, E, k, I, alpha, limit, 0, 0, order)
     wt = OrcWeights(*[_ptr(weights.get(n)) for n in
                       ("router_w", "router_b", "w1_packed", "w1_scales", "w1_bias",
                        "w2_packed", "w2_scales", "w2_bias")])

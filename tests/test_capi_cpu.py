@@ -32,7 +32,7 @@ def test_exports_every_declared_symbol(g):
 
 
 def test_abi_version_and_defaults(g):
-    assert g.lib.gptoss_abi_version() == 4
+    assert g.lib.gptoss_abi_version() == 5
     cfg = g.default_config(128, 64)
     assert (cfg.hidden_size, cfg.num_experts, cfg.top_k, cfg.intermediate_size) == (2880, 128, 4, 2880)
     assert abs(cfg.swiglu_alpha - 1.702) < 1e-6 and cfg.swiglu_limit == 7.0
@@ -77,6 +77,44 @@ def test_layer_state_errors(g):
         L.init(cfg, 0, router_weight=None, mlp1=([], []), mlp2=([], []))
     with pytest.raises(ValueError, match="aligned"):
         L.init(cfg, 0, router_weight=_FakeT(2), mlp1=([], []), mlp2=([], []))
+    L.destroy()
+
+
+def test_layer_forward_argument_checks(g):
+    """The Python layer refuses tensors the kernels would misread before
+    anything reaches the library: wrong width, dtype, rank, a transposed
+    view, another device, mismatched rows, and routing tensors of the wrong
+    dtype or shape.  The layer is given a config without init (no GPU), so
+    every call here must fail in the host-side checks."""
+    import torch
+    L = g.MoELayer()
+    L.cfg, L.device = g.default_config(128, 8), 0
+    H = L.cfg.hidden_size
+
+    def bf(*shape):
+        return torch.zeros(shape, dtype=torch.bfloat16)
+
+    cases = [
+        (lambda: L.forward_prenormed(bf(2, H - 64)), "shape"),               # hidden width below H
+        (lambda: L.forward_prenormed(torch.zeros(2, H)), "dtype"),           # fp32 activations
+        (lambda: L.forward_prenormed(bf(2, 1, H)), "2-D"),
+        (lambda: L.forward_prenormed(bf(H, 2).t()), "contiguous"),            # transposed view
+        (lambda: L.forward_prenormed(bf(2, H)), "cuda:0"),                    # host tensor
+        (lambda: L.forward(bf(2, H)), "cuda:0"),
+        (lambda: L.forward_residual(bf(2, H), bf(2, H)), "cuda:0"),
+        (lambda: g._check_tensor("delta", bf(3, H), 0, 2, H, 2, g._BF16), "delta has shape"),  # rows != T
+        (lambda: L.forward_routed(bf(2, H), torch.zeros(2, 4, dtype=torch.int64),
+                                  torch.zeros(2, 4)), "cuda:0|dtype"),
+    ]
+    for call, msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            call()
+    # the routing tensors' own rules, on the helper the layer calls
+    with pytest.raises(ValueError, match="expert_indices has dtype"):
+        g._check_tensor("expert_indices", torch.zeros(2, 4, dtype=torch.int64), 0, 4, 4, 2, (torch.int32,))
+    with pytest.raises(ValueError, match="expert_weights has shape"):
+        g._check_tensor("expert_weights", torch.zeros(2, 8), 0, 4, 4, 2, (torch.float32,))
+    L.cfg = None
     L.destroy()
 
 

@@ -360,6 +360,22 @@ def test_layer_forward_residual(gpu, orc, torch_mod, T, E, H, I):
     # without residual_out the sum stays in the layer's scratch; same output
     out2 = host(L.layer.forward_residual(dev(res, torch), dev(delta, torch)))
     assert np.array_equal(out2, out)
+    if T == 1 and H == 192:
+        # residual_out on the residual or the delta (in place, or one row
+        # shifted) is refused before any launch; out in place on residual_out
+        # is fine and gives the same result
+        dr, dd = dev(res, torch), dev(delta, torch)
+        for alias in (dr, dd):
+            with pytest.raises(ValueError, match="residual_out overlaps"):
+                L.layer.forward_residual(dr, dd, residual_out=alias)
+        wide = torch.empty((T + 1, H), dtype=torch.bfloat16, device="cuda")
+        wide[:T].copy_(dr)
+        with pytest.raises(ValueError, match="residual_out overlaps"):
+            gpu.check(gpu.lib.gptoss_moe_layer_forward_residual(
+                L.layer._h, wide.data_ptr(), dd.data_ptr(), wide.data_ptr() + 2 * 8, res_out.data_ptr(), T,
+                torch.cuda.current_stream().cuda_stream))
+        same = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        assert np.array_equal(host(L.layer.forward_residual(dr, dd, residual_out=same, out=same)), out)
 
 
 def test_layer_edge_cases(gpu, orc, torch_mod):
@@ -464,17 +480,28 @@ _SHIM = {
     "init": "_ZN6gptoss14moe_layer_initEPNS_8MoELayerEiiiPNS_6EPCommEPKNS_12CublasHandleES6_P12ihipStream_tS8_"
             "PK14__hip_bfloat16SB_SB_SB_SB_PNS_11MXFP4WeightESD_PS9_SE_PiPfSF_SE_SF_SF_SF_SF_SE_SE_SE_SE_SE_SE_SE_"
             "SE_SE_P8ncclComm",
+    "forward": "_ZN6gptoss17moe_layer_forwardEPNS_8MoELayerEPK14__hip_bfloat16PS2_iP12ihipStream_t",
     "prenormed": "_ZN6gptoss27moe_layer_forward_prenormedEPNS_8MoELayerEPK14__hip_bfloat16S4_PS2_iP12ihipStream_t",
+    "max_tokens": "_ZN6gptoss20moe_layer_max_tokensEv",
 }
 
 
 def test_cpp_operator_shim_matches_c_abi(gpu, torch_mod, gptoss120):
+    """The reference engine's calls, by mangled name, at its token counts:
+    decode (1), a decode batch (64) and a prefill chunk (4096, above the
+    old 256-token default; the shim's layers share one per-device workspace
+    for the engine's 8192).  moe_layer_forward (RMSNorm inside) and
+    moe_layer_forward_prenormed, bit for bit against the C ABI with the
+    shim's configuration.  Two shim layers are created so that the second
+    shares the first's workspace."""
     import ctypes
     torch = torch_mod
     w, L = gptoss120
     E, H = 128, 2880
-    # the operator shim runs the default configuration (matrix-core decode)
-    Lmc = DeviceLayer(gpu, torch, w, E, 4, H, H, max_tokens=8, exact=False, t=L.t, via_tables=True)
+    norm_w = moe_data.bf16(np.random.default_rng(5).normal(1.0, 0.1, H))
+    # the operator shim runs the default configuration (matrix-core decode, grouped prefill)
+    Lmc = DeviceLayer(gpu, torch, w, E, 4, H, H, max_tokens=4096, exact=False, t=L.t, via_tables=True,
+                      norm_w=norm_w)
     lib = ctypes.CDLL(os.path.join(os.path.dirname(gpu.LIB_PATH), "libgptoss_moe_compat.so"))
     create = getattr(lib, _SHIM["create"])
     create.restype = ctypes.c_void_p
@@ -484,9 +511,13 @@ def test_cpp_operator_shim_matches_c_abi(gpu, torch_mod, gptoss120):
     init.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 12 + \
         [ctypes.c_void_p] * 19 + [ctypes.c_void_p]
     init.restype = None
-    fwd = getattr(lib, _SHIM["prenormed"])
-    fwd.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p]
+    fwd = getattr(lib, _SHIM["forward"])
+    fwd.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_void_p]
     fwd.restype = None
+    pre = getattr(lib, _SHIM["prenormed"])
+    pre.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p]
+    pre.restype = None
+    assert getattr(lib, _SHIM["max_tokens"])() == 8192
 
     class MXFP4Weight(ctypes.Structure):  # moe_layer.cu:585-589
         _fields_ = [("packed", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("num_elements", ctypes.c_int)]
@@ -497,21 +528,73 @@ def test_cpp_operator_shim_matches_c_abi(gpu, torch_mod, gptoss120):
         mlp1[e] = MXFP4Weight(L.t["w1_packed"][e].data_ptr(), L.t["w1_scales"][e].data_ptr(), 2 * H * H)
         mlp2[e] = MXFP4Weight(L.t["w2_packed"][e].data_ptr(), L.t["w2_scales"][e].data_ptr(), H * H)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-    layer = create()
-    assert layer
-    init(layer, 0, 0, 0, None, None, None, None, None, None, ptr(L.t["router_w"]), ptr(L.t.get("router_b")),
-         ptr(L.t.get("w1_bias")), ptr(L.t.get("w2_bias")), ctypes.cast(mlp1, ctypes.c_void_p),
-         ctypes.cast(mlp2, ctypes.c_void_p), *([None] * 19), None)
+    layers = []
     try:
-        for T in (1, 8):
-            say("C++ operator shim, T", T)
+        for _ in range(2):
+            layer = create()
+            assert layer
+            layers.append(layer)
+            init(layer, 0, 0, 0, None, None, None, None, None, None, ptr(Lmc.norm), ptr(L.t["router_w"]),
+                 ptr(L.t.get("router_b")), ptr(L.t.get("w1_bias")), ptr(L.t.get("w2_bias")),
+                 ctypes.cast(mlp1, ctypes.c_void_p), ctypes.cast(mlp2, ctypes.c_void_p), *([None] * 19), None)
+        stream = torch.cuda.current_stream().cuda_stream
+        for T in (1, 64, 4096):
             x, res = moe_data.make_tokens(900 + T, T, H)
             dx, dr = dev(x, torch), dev(res, torch)
-            out = torch.empty_like(dx)
-            fwd(layer, dx.data_ptr(), dr.data_ptr(), out.data_ptr(), T, torch.cuda.current_stream().cuda_stream)
-            torch.cuda.synchronize()
-            want = host(Lmc.layer.forward_prenormed(dx, dr))
-            assert np.array_equal(host(out), want), T
+            for li, layer in enumerate(layers):
+                say("C++ operator shim, layer", li, "T", T)
+                out = torch.empty_like(dx)
+                pre(layer, dx.data_ptr(), dr.data_ptr(), out.data_ptr(), T, stream)
+                torch.cuda.synchronize()
+                assert np.array_equal(host(out), host(Lmc.layer.forward_prenormed(dx, dr))), ("prenormed", T)
+                out2 = torch.empty_like(dx)
+                fwd(layer, dx.data_ptr(), out2.data_ptr(), T, stream)
+                torch.cuda.synchronize()
+                assert np.array_equal(host(out2), host(Lmc.layer.forward(dx))), ("forward", T)
     finally:
-        destroy(layer)
+        for layer in layers:
+            destroy(layer)
         Lmc.layer.destroy()
+
+
+def test_shared_workspace(gpu, orc, torch_mod):
+    """Layers of different shapes on one caller workspace, run one after
+    another on one stream (the reference engine's scratch sharing), give the
+    results of layers with their own scratch, at decode sizes and at a prefill
+    size whose grouped kernels use the workspace's tile queue; a workspace
+    that is too small or misaligned is refused."""
+    torch = torch_mod
+    shapes = [(16, 4, 128, 128), (8, 2, 192, 64)]
+    own, shared = [], []
+    need = 0
+    cfgs = []
+    for E, k, H, I in shapes:
+        cfg = gpu.default_config(E, 160)
+        cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, k
+        cfgs.append(cfg)
+        need = max(need, gpu.workspace_bytes(cfg))
+    ws = torch.empty(need + 256, dtype=torch.uint8, device="cuda")
+    for (E, k, H, I), cfg in zip(shapes, cfgs):
+        w = moe_data.make_layer(70 + E, E, H, I, bias="random")
+        a = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=160, exact=False, via_tables=False)
+        b = gpu.MoELayer().init(cfg, 0, a.t["router_w"], a.t.get("router_b"), a.t.get("w1_bias"),
+                                a.t.get("w2_bias"), tiled=a.tiled, workspace=ws[:need])
+        own.append((a, w, H))
+        shared.append(b)
+    bad = gpu.MoELayer()
+    with pytest.raises(ValueError, match="workspace of"):
+        bad.init(cfgs[0], 0, own[0][0].t["router_w"], tiled=own[0][0].tiled, workspace=ws[:64])
+    with pytest.raises(ValueError, match="aligned"):
+        bad.init(cfgs[0], 0, own[0][0].t["router_w"], tiled=own[0][0].tiled, workspace=ws[8:8 + need])
+    bad.destroy()
+    for T in (1, 8, 150, 3):
+        for (a, w, H), b in zip(own, shared):
+            say("shared workspace T", T, "H", H)
+            x, res = moe_data.make_tokens(80 + T, T, H)
+            dx, dr = dev(x, torch), dev(res, torch)
+            want = host(a.layer.forward_prenormed(dx, dr))
+            assert np.array_equal(host(b.forward_prenormed(dx, dr)), want), (T, H)
+    for b in shared:
+        b.destroy()
+    for a, _, _ in own:
+        a.layer.destroy()

@@ -360,6 +360,45 @@ def test_mxfp4_canonical_part_order(orc):
     assert np.all(y == 0.0)  # sequential part order: the two +1 are absorbed by 2^24
 
 
+def _unit_weights(N, K, ks):
+    """MXFP4 rows with weight 1.0 (code 2, scale 127) at the elements ks, 0 elsewhere."""
+    packed = np.zeros((N, K // 2), np.uint8)
+    for k_ in ks:
+        packed[:, k_ // 2] |= np.uint8(0x02 << (4 * (k_ & 1)))
+    return packed, np.full((N, K // 32), 127, np.uint8)
+
+
+@pytest.mark.parametrize("case", [
+    # (element: x value) -> expected output, derived by hand from
+    # fused_mxfp4_gemv.cu:93-183 at K = 2880 (360 uint32 chunks of 8 elements;
+    # thread tid takes chunks tid and tid + 256; warp = tid // 64).
+    # Warps are added in order from 0: ((2^24 + 1) + 1) - 2^24 = 0 (a pairwise
+    # tree over the warps would give 2).
+    ({0: 2.0 ** 24, 512: 1.0, 1024: 1.0, 1536: -(2.0 ** 24)}, 0.0),
+    # Inside a warp the xor butterfly pairs thread l with l + 32 first:
+    # (2^24 - 2^24) + (1 + 1) = 2 (an ascending sum over threads gives 1).
+    ({0: 2.0 ** 24, 8: 1.0, 256: -(2.0 ** 24), 264: 1.0}, 2.0),
+    # Thread 0 adds its chunks 0 and 256 first: (2^24 + 1) rounds to 2^24,
+    # then thread 32's -2^24 cancels it: 0 (a split of chunk 256 to another
+    # thread would leave the 1).
+    ({0: 2.0 ** 24, 2048: 1.0, 256: -(2.0 ** 24)}, 0.0),
+    # Inside a chunk, products are added in pairs before the chunk sum:
+    # (2^24 + 1) -> 2^24, (1 - 2^24) exact, sum 1 (an element chain gives 0).
+    ({0: 2.0 ** 24, 1: 1.0, 2: 1.0, 3: -(2.0 ** 24)}, 1.0),
+])
+def test_mxfp4_refkernel_order(orc, case):
+    """The restatement of the reference's fused MXFP4 GEMV order, pinned by
+    cancellation cases whose results a different order changes."""
+    vals, want = case
+    N, K = 64, 2880
+    x = np.zeros((1, K), np.float32)
+    for k_, v in vals.items():
+        x[0, k_] = v
+    packed, scales = _unit_weights(N, K, vals)
+    y = orc.bf16_to_f32(orc.mxfp4_gemv_refkernel(orc.f32_to_bf16(x), packed, scales, None, N, K))
+    assert np.all(y == want), (vals, y[:4])
+
+
 # ---------------------------------------------------------------------------
 # combine
 # ---------------------------------------------------------------------------
@@ -392,12 +431,19 @@ def test_combine_one_hot_and_linear(orc):
 # ---------------------------------------------------------------------------
 # whole layer against an fp64 restatement with the same rounding points
 # ---------------------------------------------------------------------------
-def _layer_fp64(w, x, res, E, k, H, I, orc):
+def _layer_fp64(w, x, res, E, k, H, I, orc, fast_one=False):
+    """The layer in fp64 with bf16 roundings at the reference's points.
+    fast_one: the one-token fast path's points (moe_layer.cu:1028-1098):
+    bf16 gate_up before its bias, bf16 down product before its bias."""
     xd = orc.bf16_to_f32(x).astype(np.float64)
     logits = xd @ orc.bf16_to_f32(w["router_w"]).astype(np.float64).T + orc.bf16_to_f32(w["router_b"])
     logits_b = orc.bf16_to_f32(orc.f32_to_bf16(logits.astype(np.float32))).astype(np.float64)
     T = x.shape[0]
     out = np.zeros((T, H))
+
+    def rnd(v):
+        return orc.bf16_to_f32(orc.f32_to_bf16(np.asarray(v, np.float32))).astype(np.float64)
+
     for t in range(T):
         order = sorted(range(E), key=lambda e: (-logits_b[t, e], e))[:k]
         v = logits_b[t, order]
@@ -406,15 +452,18 @@ def _layer_fp64(w, x, res, E, k, H, I, orc):
         acc = np.zeros(H)
         for s, e in enumerate(order):
             W1 = _dequant_f64(w["w1_packed"][e], w["w1_scales"][e], 2 * I, H, orc)
-            gu = xd[t] @ W1.T + orc.bf16_to_f32(w["w1_bias"][e])
-            gu = orc.bf16_to_f32(orc.f32_to_bf16(gu.astype(np.float32))).astype(np.float64)
+            b1 = orc.bf16_to_f32(w["w1_bias"][e]).astype(np.float64)
+            if fast_one:
+                gu = rnd(xd[t] @ W1.T) + b1
+            else:
+                gu = rnd(xd[t] @ W1.T + b1)
             g = np.minimum(gu[0::2], 7.0)
             u = np.clip(gu[1::2], -7.0, 7.0)
             a = (u + 1) * g / (1 + np.exp(-1.702 * g))
             a = orc.bf16_to_f32(orc.f32_to_bf16(a.astype(np.float32))).astype(np.float64)
             W2 = _dequant_f64(w["w2_packed"][e], w["w2_scales"][e], H, I, orc)
-            yy = a @ W2.T + orc.bf16_to_f32(w["w2_bias"][e])
-            yy = orc.bf16_to_f32(orc.f32_to_bf16(yy.astype(np.float32))).astype(np.float64)
+            b2 = orc.bf16_to_f32(w["w2_bias"][e]).astype(np.float64)
+            yy = rnd(rnd(a @ W2.T) + b2) if fast_one else rnd(a @ W2.T + b2)
             acc += p[s] * yy
         out[t] = acc + orc.bf16_to_f32(res[t])
     return orc.bf16_to_f32(orc.f32_to_bf16(out.astype(np.float32))).astype(np.float64)
@@ -430,6 +479,96 @@ def test_layer_tiny_vs_fp64(orc):
     assert rel.mean() <= 1e-3
     assert np.all(np.abs(out - ref) <= 2 * moe_data.ulp_bf16(ref) + 1e-6)
     assert (out == ref).mean() > 0.9
+
+
+@pytest.mark.parametrize("T", [1, 12])
+def test_layer_reference_order_vs_fp64(orc, T):
+    """order=1 (the reference's dispatch and rounding points) stays within two
+    bf16 steps of the fp64 layer, like the canonical order."""
+    E, k, H, I = 8, 2, 64, 64
+    # one token: random biases, at the fast path's rounding points; several
+    # tokens: zero biases, where every path's rounding points coincide
+    w = moe_data.make_layer(13 + T, E, H, I, bias="random" if T == 1 else "zero")
+    x, res = moe_data.make_tokens(13 + T, T, H)
+    out = orc.bf16_to_f32(orc.moe_forward(w, x, res, E, k, H, I, order=1)).astype(np.float64)
+    ref = _layer_fp64(w, x, res, E, k, H, I, orc, fast_one=T == 1)
+    rel = np.abs(out - ref) / np.maximum(np.abs(ref), 1e-3)
+    assert rel.mean() <= 1e-3
+    assert np.all(np.abs(out - ref) <= 2 * moe_data.ulp_bf16(ref) + 1e-6)
+
+
+def _f32(a):
+    return np.asarray(a, np.float32)
+
+
+def test_layer_reference_order_one_token(orc):
+    """The one-token fast path (moe_layer.cu:1028-1098) in order=1, checked
+    stage by stage against the oracle's single-matrix primitives: gate_up is
+    the fused GEMV with no bias; the SwiGLU takes bf16(gate_up) + bias in fp32;
+    the down output is bf16(bf16(GEMV) + bias); the combine starts from the
+    residual and adds w_k * y_k in slot order."""
+    E, k, H, I = 8, 4, 256, 128
+    w = moe_data.make_layer(21, E, H, I, bias="random")
+    x, res = moe_data.make_tokens(21, 1, H)
+    out, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True, order=1)
+    L = orc.lib()
+    gm = tr["gather_map"]
+    acc = orc.bf16_to_f32(res[0]).copy()
+    for s in range(k):
+        e, p = int(tr["idx"][0, s]), int(gm[s])
+        gu = orc.mxfp4_gemv_refkernel(x, w["w1_packed"][e], w["w1_scales"][e], None, 2 * I, H)[0]
+        assert np.array_equal(tr["gate_up"][p], gu)
+        gb = orc.bf16_to_f32(gu) + orc.bf16_to_f32(w["w1_bias"][e])      # fp32 sum, not rounded
+        act = np.array([L.orc_swiglu(float(gb[2 * i]), float(gb[2 * i + 1]), 1.702, 7.0) for i in range(I)],
+                       np.float32)
+        assert np.array_equal(tr["act"][p], orc.f32_to_bf16(act))
+        yd = orc.mxfp4_gemv_refkernel(tr["act"][p:p + 1], w["w2_packed"][e], w["w2_scales"][e], None, H, I)[0]
+        y = orc.f32_to_bf16(orc.bf16_to_f32(yd) + orc.bf16_to_f32(w["w2_bias"][e]))
+        assert np.array_equal(tr["y"][p], y)
+        # fma(w, y, acc): the product is exact in fp64 and so is its sum with acc here
+        acc = _f32(np.float64(tr["w"][0, s]) * orc.bf16_to_f32(y).astype(np.float64) + acc.astype(np.float64))
+    assert np.array_equal(out[0], orc.f32_to_bf16(acc))
+
+
+def test_layer_reference_order_dispatch(orc):
+    """order=1 with several tokens picks the reference's path per active
+    expert (moe_layer.cu:1282-1417).  Routing: experts 0-7 one token each
+    (batch 0: all one-token -> fused GEMV, bias inside), expert 8 four tokens
+    and 9-12 one each (batch 1, mixed -> hipBLASLt stand-in for 8, gemv_bf16
+    over the dequantised weights for 9-12, each then a separate bias add).
+    Every expert's rows are checked against the oracle's primitives."""
+    E, k, H, I, T = 16, 4, 256, 128, 4
+    w = moe_data.make_layer(22, E, H, I, bias="random")
+    x, res = moe_data.make_tokens(22, T, H)
+    idx = np.array([[0, 1, 8, 9], [2, 3, 8, 10], [4, 5, 8, 11], [6, 7, 8, 12]], np.int32)
+    wts = np.full((T, k), 0.25, np.float32)
+    out, tr = orc.moe_forward_routed(w, x, res, idx, wts, E, k, H, I, trace=True, order=1)
+    gm = tr["gather_map"]
+
+    def round_then_bias(prod_f32, b):
+        return orc.f32_to_bf16(orc.bf16_to_f32(orc.f32_to_bf16(prod_f32)) + orc.bf16_to_f32(b))
+
+    for t in range(T):
+        for s in range(k):
+            e, p = int(idx[t, s]), int(gm[t * k + s])
+            P1, S1, B1 = w["w1_packed"][e], w["w1_scales"][e], w["w1_bias"][e]
+            P2, S2, B2 = w["w2_packed"][e], w["w2_scales"][e], w["w2_bias"][e]
+            a = tr["act"][p:p + 1]
+            if e < 8:
+                gu = orc.mxfp4_gemv_refkernel(x[t:t + 1], P1, S1, B1, 2 * I, H)[0]
+                y = orc.mxfp4_gemv_refkernel(a, P2, S2, B2, H, I)[0]
+            elif e == 8:
+                gu = round_then_bias(orc.bf16_to_f32(orc.mxfp4_gemv(x[t:t + 1], P1, S1, None, 2 * I, H))[0], B1)
+                y = round_then_bias(orc.bf16_to_f32(orc.mxfp4_gemv(a, P2, S2, None, H, I))[0], B2)
+            else:
+                dq1 = orc.mxfp4_dequant(P1, S1, 2 * I, H)
+                dq2 = orc.mxfp4_dequant(P2, S2, H, I)
+                gu = round_then_bias(orc.router(x[t:t + 1], dq1, None, logits_fp32=True)[0], B1)
+                y = round_then_bias(orc.router(a, dq2, None, logits_fp32=True)[0], B2)
+            assert np.array_equal(tr["gate_up"][p], gu), (t, s, e)
+            assert np.array_equal(tr["act"][p], orc.swiglu_rows(gu[None], I)[0]), (t, s, e)
+            assert np.array_equal(tr["y"][p], y), (t, s, e)
+    assert np.array_equal(out, orc.combine(tr["y"], gm, wts, res, T, k, H))
 
 
 def test_layer_threads_deterministic(orc):
