@@ -534,7 +534,8 @@ def test_cpp_operator_shim_matches_c_abi(gpu, torch_mod, gptoss120):
             layer = create()
             assert layer
             layers.append(layer)
-            init(layer, 0, 0, 0, None, None, None, None, None, None, ptr(Lmc.norm), ptr(L.t["router_w"]),
+            # layer/device/gpu ids, EPComm, two BLAS handles, two streams, then the weights
+            init(layer, 0, 0, 0, None, None, None, None, None, ptr(Lmc.norm), ptr(L.t["router_w"]),
                  ptr(L.t.get("router_b")), ptr(L.t.get("w1_bias")), ptr(L.t.get("w2_bias")),
                  ctypes.cast(mlp1, ctypes.c_void_p), ctypes.cast(mlp2, ctypes.c_void_p), *([None] * 19), None)
         stream = torch.cuda.current_stream().cuda_stream
