@@ -151,6 +151,51 @@ WsLayout ws_layout(const gptoss_moe_config& c) {
   return l;
 }
 
+// Device pointers of one forward's scratch, carved from a workspace laid out
+// by ws_layout.
+struct Scratch {
+  void* logits = nullptr;
+  int32_t* idx = nullptr;
+  float* w = nullptr;
+  int32_t* counts = nullptr;
+  int32_t* offsets = nullptr;
+  int32_t* gmap = nullptr;
+  int32_t* ptok = nullptr;
+  int32_t* active = nullptr;
+  int32_t* n_active = nullptr;
+  int32_t* tasks = nullptr;
+  uint16_t* act = nullptr;
+  uint16_t* y = nullptr;
+  uint16_t* normed = nullptr;
+  uint16_t* sumres = nullptr;  // residual + delta of forward_residual when the caller keeps no copy
+  int32_t* gqueue = nullptr;   // tile queue of the persistent grouped kernel (zeroed; left zeroed)
+  int32_t* pchunk = nullptr;   // scratch of the multi-launch plan (many tokens)
+  uint16_t* gate_up = nullptr; // bf16 gate_up trace (layer-owned), or null
+  PlanBufs plan() const { return PlanBufs{counts, offsets, gmap, ptok, active, n_active, tasks, pchunk}; }
+};
+
+Scratch carve(void* base, const WsLayout& l) {
+  char* ws = static_cast<char*>(base);
+  Scratch c;
+  c.gqueue = reinterpret_cast<int32_t*>(ws + l.queue);
+  c.logits = ws + l.logits;
+  c.idx = reinterpret_cast<int32_t*>(ws + l.idx);
+  c.w = reinterpret_cast<float*>(ws + l.w);
+  c.counts = reinterpret_cast<int32_t*>(ws + l.counts);
+  c.offsets = reinterpret_cast<int32_t*>(ws + l.offsets);
+  c.gmap = reinterpret_cast<int32_t*>(ws + l.gmap);
+  c.ptok = reinterpret_cast<int32_t*>(ws + l.ptok);
+  c.active = reinterpret_cast<int32_t*>(ws + l.active);
+  c.n_active = reinterpret_cast<int32_t*>(ws + l.n_active);
+  c.tasks = reinterpret_cast<int32_t*>(ws + l.tasks);
+  c.act = reinterpret_cast<uint16_t*>(ws + l.act);
+  c.y = reinterpret_cast<uint16_t*>(ws + l.y);
+  c.pchunk = reinterpret_cast<int32_t*>(ws + l.pchunk);
+  c.normed = reinterpret_cast<uint16_t*>(ws + l.normed);
+  c.sumres = reinterpret_cast<uint16_t*>(ws + l.sumres);
+  return c;
+}
+
 }  // namespace
 
 struct gptoss_moe_layer {
@@ -167,27 +212,11 @@ struct gptoss_moe_layer {
   const uint8_t* w2n = nullptr;
   const uint8_t* w2s = nullptr;
   std::vector<void*> owned;
-  // scratch
-  void* logits = nullptr;
-  int32_t* idx = nullptr;
-  float* w = nullptr;
-  int32_t* counts = nullptr;
-  int32_t* offsets = nullptr;
-  int32_t* gmap = nullptr;
-  int32_t* ptok = nullptr;
-  int32_t* active = nullptr;
-  int32_t* n_active = nullptr;
-  int32_t* tasks = nullptr;
-  uint16_t* act = nullptr;
-  uint16_t* y = nullptr;
-  uint16_t* gate_up = nullptr;
-  uint16_t* normed = nullptr;
-  uint16_t* sumres = nullptr;   // residual + delta of forward_residual when the caller keeps no copy
-  void* workspace = nullptr;   // per-forward scratch (owned, or borrowed and shared)
+  Scratch sc;                   // this layer's forward scratch (in its workspace)
+  uint16_t* gate_up = nullptr;  // bf16 gate_up trace buffer (gptoss_moe_layer_set_trace_gate_up)
+  void* workspace = nullptr;    // per-forward scratch (owned, or borrowed and shared)
   int32_t* special1 = nullptr;  // [E] W1 / W2 scales hold e8m0 code 0 or 255
   int32_t* special2 = nullptr;
-  int32_t* gqueue = nullptr;    // tile queue of the persistent grouped kernel (zeroed; left zeroed)
-  int32_t* pchunk = nullptr;    // scratch of the multi-launch plan (many tokens)
   int special_any1 = 0, special_any2 = 0;
   int num_cus = 0;
   int mc_shape[3] = {0, 0, 0};  // matrix-core decode launch shape override
@@ -359,29 +388,13 @@ static int layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int dev
     L->release();
     return rc;
   }
-  char* ws = static_cast<char*>(L->workspace);
-  L->gqueue = reinterpret_cast<int32_t*>(ws + lay.queue);
-  L->logits = ws + lay.logits;
-  L->idx = reinterpret_cast<int32_t*>(ws + lay.idx);
-  L->w = reinterpret_cast<float*>(ws + lay.w);
-  L->counts = reinterpret_cast<int32_t*>(ws + lay.counts);
-  L->offsets = reinterpret_cast<int32_t*>(ws + lay.offsets);
-  L->gmap = reinterpret_cast<int32_t*>(ws + lay.gmap);
-  L->ptok = reinterpret_cast<int32_t*>(ws + lay.ptok);
-  L->active = reinterpret_cast<int32_t*>(ws + lay.active);
-  L->n_active = reinterpret_cast<int32_t*>(ws + lay.n_active);
-  L->tasks = reinterpret_cast<int32_t*>(ws + lay.tasks);
-  L->act = reinterpret_cast<uint16_t*>(ws + lay.act);
-  L->y = reinterpret_cast<uint16_t*>(ws + lay.y);
-  L->pchunk = reinterpret_cast<int32_t*>(ws + lay.pchunk);
-  L->normed = reinterpret_cast<uint16_t*>(ws + lay.normed);
-  L->sumres = reinterpret_cast<uint16_t*>(ws + lay.sumres);
+  L->sc = carve(L->workspace, lay);
   void* p;
   if ((rc = L->alloc(&p, E * 4, "special1")) != GPTOSS_OK) return (L->release(), rc);
   L->special1 = static_cast<int32_t*>(p);
   if ((rc = L->alloc(&p, E * 4, "special2")) != GPTOSS_OK) return (L->release(), rc);
   L->special2 = static_cast<int32_t*>(p);
-  hipError_t err = hipMemset(L->gqueue, 0, grouped_queue_ints() * 4);
+  hipError_t err = hipMemset(L->sc.gqueue, 0, grouped_queue_ints() * 4);
   if (err == hipSuccess) err = launch_special_scan(L->w1s, 2 * I, H, E, L->special1, nullptr);
   if (err == hipSuccess) err = launch_special_scan(L->w2s, H, I, E, L->special2, nullptr);
   if (err == hipSuccess) err = hipDeviceGetAttribute(&L->num_cus, hipDeviceAttributeMultiprocessorCount, device_id);
@@ -480,11 +493,20 @@ struct ProfForward {
 };
 constexpr int kProfEvents = 8;
 
+// The layer's own scratch for a forward, with its gate_up trace buffer when
+// tracing is on.
+static Scratch layer_scratch(const gptoss_moe_layer* L) {
+  Scratch S = L->sc;
+  S.gate_up = L->trace_gu ? L->gate_up : nullptr;
+  return S;
+}
+
 // Expert products and combine after the plan (decode: weight-streaming
 // kernels, on the matrix cores or exact; prefill: grouped matrix-core GEMMs).
 // w: routing weights [T][k].
-static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, const float* w,
-                         uint16_t* out, int T, hipStream_t s, const ProfForward& pf, bool route_in_w1 = false) {
+static int layer_experts(gptoss_moe_layer* L, const Scratch& S, const uint16_t* normed, const uint16_t* residual,
+                         const float* w, uint16_t* out, int T, hipStream_t s, const ProfForward& pf,
+                         bool route_in_w1 = false) {
   const gptoss_moe_config& c = L->cfg;
   ExpertArgs ea{};
   ea.x = normed;
@@ -501,11 +523,11 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
   ea.k = c.top_k;
   ea.alpha = c.swiglu_alpha;
   ea.limit = c.swiglu_limit;
-  ea.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks};
+  ea.plan = PlanBufs{S.counts, S.offsets, S.gmap, S.ptok, S.active, S.n_active, S.tasks};
   ea.w = w;
-  ea.act = L->act;
-  ea.gate_up = L->trace_gu ? L->gate_up : nullptr;
-  ea.y = L->y;
+  ea.act = S.act;
+  ea.gate_up = S.gate_up;
+  ea.y = S.y;
   ea.residual = residual;
   ea.out = out;
   ea.max_active = T * c.top_k < c.num_experts ? T * c.top_k : c.num_experts;
@@ -518,17 +540,17 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
   ea.mc_shape[1] = L->mc_shape[1];
   ea.mc_shape[2] = L->mc_shape[2];
   if (route_in_w1) {  // the gate_up launch selects the experts from the router's logits
-    ea.route_logits = L->logits;
+    ea.route_logits = S.logits;
     ea.route_fp32 = c.logits_fp32;
     ea.route_variant = 1;  // T <= 8 (topk_softmax.cu:399)
-    ea.route_idx = L->idx;
-    ea.route_w = L->w;
+    ea.route_idx = S.idx;
+    ea.route_w = S.w;
   }
   if (c.prefill_min_tokens > 0 && T >= c.prefill_min_tokens) {
     GroupedArgs g{};
     g.x = normed;
-    g.row_index = L->ptok;
-    g.offsets = L->offsets;
+    g.row_index = S.ptok;
+    g.offsets = S.offsets;
     g.E = c.num_experts;
     g.rows = T * c.top_k;
     g.wn = L->w1n;
@@ -536,23 +558,23 @@ static int layer_experts(gptoss_moe_layer* L, const uint16_t* normed, const uint
     g.N = 2 * c.intermediate_size;
     g.K = c.hidden_size;
     g.bias = L->b1;
-    g.out = L->act;
+    g.out = S.act;
     g.gate_up = ea.gate_up;
     g.gated = 1;
     g.alpha = c.swiglu_alpha;
     g.limit = c.swiglu_limit;
-    g.queue = L->gqueue;
+    g.queue = S.gqueue;
     g.num_cus = L->num_cus;
     g.timer = pf.timer(1);
     HIP_TRY(launch_grouped_mxfp4(g, s), "grouped gate_up launch");
-    g.x = L->act;
+    g.x = S.act;
     g.row_index = nullptr;
     g.wn = L->w2n;
     g.ws = L->w2s;
     g.N = c.hidden_size;
     g.K = c.intermediate_size;
     g.bias = L->b2;
-    g.out = L->y;
+    g.out = S.y;
     g.gate_up = nullptr;
     g.gated = 0;
     g.timer = pf.timer(2);
@@ -584,8 +606,9 @@ static ProfForward next_prof(gptoss_moe_layer* L, hipStream_t s) {
 
 // The router (optionally with the residual RMSNorm in front: delta != null)
 // then the experts and the combine.
-static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual, uint16_t* out,
-                              int T, hipStream_t s, const uint16_t* delta = nullptr, uint16_t* sum_out = nullptr) {
+static int layer_forward_core(gptoss_moe_layer* L, const Scratch& S, const uint16_t* normed, const uint16_t* residual,
+                              uint16_t* out, int T, hipStream_t s, const uint16_t* delta = nullptr,
+                              uint16_t* sum_out = nullptr) {
   const gptoss_moe_config& c = L->cfg;
   RouteArgs ra{};
   ra.x = normed;
@@ -593,7 +616,7 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
     ra.delta = delta;
     ra.norm_w = L->norm_w;
     ra.eps = c.rms_norm_eps;
-    ra.normed = L->normed;
+    ra.normed = S.normed;
     ra.sum_out = sum_out;
   }
   ra.W = L->router_w;
@@ -603,10 +626,10 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   ra.H = c.hidden_size;
   ra.k = c.top_k;
   ra.logits_fp32 = c.logits_fp32;
-  ra.logits = L->logits;
-  ra.idx = L->idx;
-  ra.w = L->w;
-  ra.plan = PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks, L->pchunk};
+  ra.logits = S.logits;
+  ra.idx = S.idx;
+  ra.w = S.w;
+  ra.plan = S.plan();
   // Up to 8 tokens on the matrix-core decode path, the gate_up launch makes
   // the top-k and plan itself: the router launch computes the logits only.
   const bool prefill = c.prefill_min_tokens > 0 && T >= c.prefill_min_tokens;
@@ -618,8 +641,8 @@ static int layer_forward_core(gptoss_moe_layer* L, const uint16_t* normed, const
   const ProfForward pf = next_prof(L, s);
   ra.timer = pf.timer(0);
   HIP_TRY(launch_route(ra, s), "route launch");
-  if (delta != nullptr) return layer_experts(L, L->normed, sum_out, L->w, out, T, s, pf, route_in_w1);
-  return layer_experts(L, normed, residual, L->w, out, T, s, pf, route_in_w1);
+  if (delta != nullptr) return layer_experts(L, S, S.normed, sum_out, S.w, out, T, s, pf, route_in_w1);
+  return layer_experts(L, S, normed, residual, S.w, out, T, s, pf, route_in_w1);
 }
 
 static int check_forward_args(gptoss_moe_layer* L, const void* in, const void* out, int T) {
@@ -639,7 +662,7 @@ int gptoss_moe_layer_forward_prenormed(gptoss_moe_layer* L, const uint16_t* norm
   if (T == 0) return ok();
   ScopedDevice sd(L->device);
   if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
-  return layer_forward_core(L, normed, residual, out, T, static_cast<hipStream_t>(stream));
+  return layer_forward_core(L, layer_scratch(L), normed, residual, out, T, static_cast<hipStream_t>(stream));
 }
 
 int gptoss_moe_layer_forward(gptoss_moe_layer* L, const uint16_t* input, uint16_t* out, int T, void* stream) {
@@ -650,9 +673,10 @@ int gptoss_moe_layer_forward(gptoss_moe_layer* L, const uint16_t* input, uint16_
   ScopedDevice sd(L->device);
   if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  HIP_TRY(launch_rmsnorm(input, L->norm_w, L->normed, T, L->cfg.hidden_size, L->cfg.rms_norm_eps, s),
+  const Scratch S = layer_scratch(L);
+  HIP_TRY(launch_rmsnorm(input, L->norm_w, S.normed, T, L->cfg.hidden_size, L->cfg.rms_norm_eps, s),
           "rmsnorm launch");
-  return layer_forward_core(L, L->normed, input, out, T, s);
+  return layer_forward_core(L, S, S.normed, input, out, T, s);
 }
 
 int gptoss_moe_layer_forward_residual(gptoss_moe_layer* L, const uint16_t* residual, const uint16_t* delta,
@@ -675,8 +699,9 @@ int gptoss_moe_layer_forward_residual(gptoss_moe_layer* L, const uint16_t* resid
     return fail(GPTOSS_ERR_INVALID, "out partially overlaps residual_out");
   ScopedDevice sd(L->device);
   if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
-  return layer_forward_core(L, residual, nullptr, out, T, static_cast<hipStream_t>(stream), delta,
-                            residual_out ? residual_out : L->sumres);
+  const Scratch S = layer_scratch(L);
+  return layer_forward_core(L, S, residual, nullptr, out, T, static_cast<hipStream_t>(stream), delta,
+                            residual_out ? residual_out : S.sumres);
 }
 
 int gptoss_moe_layer_forward_routed(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual,
@@ -690,11 +715,9 @@ int gptoss_moe_layer_forward_routed(gptoss_moe_layer* L, const uint16_t* normed,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const gptoss_moe_config& c = L->cfg;
   const ProfForward pf = next_prof(L, s);
-  HIP_TRY(launch_plan(idx, T, c.top_k, c.num_experts,
-                      PlanBufs{L->counts, L->offsets, L->gmap, L->ptok, L->active, L->n_active, L->tasks, L->pchunk}, s,
-                      pf.timer(0)),
-          "plan launch");
-  return layer_experts(L, normed, residual, w, out, T, s, pf);
+  const Scratch S = layer_scratch(L);
+  HIP_TRY(launch_plan(idx, T, c.top_k, c.num_experts, S.plan(), s, pf.timer(0)), "plan launch");
+  return layer_experts(L, S, normed, residual, w, out, T, s, pf);
 }
 
 const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* L) {
@@ -724,18 +747,19 @@ int gptoss_moe_layer_set_trace_gate_up(gptoss_moe_layer* L, int enable) {
 
 int gptoss_moe_layer_trace(const gptoss_moe_layer* L, gptoss_moe_trace* t) {
   if (L == nullptr || t == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
-  t->logits = L->logits;
-  t->expert_indices = L->idx;
-  t->expert_weights = L->w;
-  t->expert_counts = L->counts;
-  t->expert_offsets = L->offsets;
-  t->gather_map = L->gmap;
-  t->perm_token = L->ptok;
-  t->active_experts = L->active;
-  t->n_active = L->n_active;
+  const Scratch& S = L->sc;
+  t->logits = S.logits;
+  t->expert_indices = S.idx;
+  t->expert_weights = S.w;
+  t->expert_counts = S.counts;
+  t->expert_offsets = S.offsets;
+  t->gather_map = S.gmap;
+  t->perm_token = S.ptok;
+  t->active_experts = S.active;
+  t->n_active = S.n_active;
   t->gate_up = L->trace_gu ? L->gate_up : nullptr;
-  t->act = L->act;
-  t->expert_out = L->y;
+  t->act = S.act;
+  t->expert_out = S.y;
   return ok();
 }
 
