@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -194,6 +195,44 @@ Scratch carve(void* base, const WsLayout& l) {
   c.normed = reinterpret_cast<uint16_t*>(ws + l.normed);
   c.sumres = reinterpret_cast<uint16_t*>(ws + l.sumres);
   return c;
+}
+
+// Forward scratch of gptoss_moe_layer_forward_prenormed_noalloc, for callers
+// that cannot allocate (graph capture, serving loops).  Every GPU that runs
+// the library holds its own copy of this array until the process ends; host
+// code reaches a GPU's copy only through the address hipGetSymbolAddress
+// returns with that GPU current (the array's name is a host-side stand-in).
+constexpr int kNoAllocMaxTokens = 64;
+constexpr size_t kNoAllocScratchBytes = static_cast<size_t>(8) << 20;
+constexpr int kNoAllocMaxDevices = 64;
+
+__global__ void zero_ints_kernel(int32_t* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+}
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kNoAllocMaxDevices] = {};  // per device: its copy of `scratch`, once resolved
+
+// The current device's copy of `scratch` (device is current).
+int noalloc_scratch(int device, void** out) {
+  if (device < 0 || device >= kNoAllocMaxDevices)
+    return fail(GPTOSS_ERR_UNSUPPORTED, "device %d outside the %d the static scratch covers", device,
+                kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[device] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_dev[device] = p;
+  }
+  *out = g_scratch_dev[device];
+  return GPTOSS_OK;
 }
 
 }  // namespace
@@ -718,6 +757,38 @@ int gptoss_moe_layer_forward_routed(gptoss_moe_layer* L, const uint16_t* normed,
   const Scratch S = layer_scratch(L);
   HIP_TRY(launch_plan(idx, T, c.top_k, c.num_experts, S.plan(), s, pf.timer(0)), "plan launch");
   return layer_experts(L, S, normed, residual, w, out, T, s, pf);
+}
+
+int gptoss_moe_layer_forward_prenormed_noalloc(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual,
+                                               uint16_t* out, int T, void* stream) {
+  if (L == nullptr) return fail(GPTOSS_ERR_INVALID, "layer is NULL");
+  if (!L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
+  if (T < 0 || T > kNoAllocMaxTokens)
+    return fail(GPTOSS_ERR_INVALID, "num_tokens=%d outside [0, %d] (the static forward scratch)", T,
+                kNoAllocMaxTokens);
+  if (T > 0 && (normed == nullptr || out == nullptr)) return fail(GPTOSS_ERR_INVALID, "null input/output");
+  if (T > 0 && !aligned16(normed)) return fail(GPTOSS_ERR_INVALID, "input must be 16-byte aligned");
+  if (T == 0) return ok();
+  gptoss_moe_config c = L->cfg;
+  c.max_tokens = T;
+  const WsLayout lay = ws_layout(c);
+  if (lay.total > kNoAllocScratchBytes)
+    return fail(GPTOSS_ERR_INVALID, "this layer needs %zu bytes of forward scratch at %d tokens, the static array "
+                "holds %zu", lay.total, T, kNoAllocScratchBytes);
+  ScopedDevice sd(L->device);
+  if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
+  void* base = nullptr;
+  const int rc = noalloc_scratch(L->device, &base);
+  if (rc != GPTOSS_OK) return rc;
+  const Scratch S = carve(base, lay);  // no gate_up trace: the layer's trace buffer is sized for its own tokens
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (c.prefill_min_tokens > 0 && T >= c.prefill_min_tokens) {
+    // the grouped kernels' tile queue must read zero: a fill kernel, since a
+    // caller may be capturing this stream
+    hipLaunchKernelGGL(zero_ints_kernel, dim3(1), dim3(256), 0, s, S.gqueue, grouped_queue_ints());
+    HIP_TRY(hipGetLastError(), "zero_ints launch");
+  }
+  return layer_forward_core(L, S, normed, residual, out, T, s);
 }
 
 const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* L) {

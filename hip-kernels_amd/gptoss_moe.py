@@ -98,6 +98,7 @@ _sig("gptoss_moe_layer_forward", [_P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_prenormed", [_P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_residual", [_P, _P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_forward_routed", [_P, _P, _P, _P, _P, _P, _I, _P])
+_sig("gptoss_moe_layer_forward_prenormed_noalloc", [_P, _P, _P, _P, _I, _P])
 _sig("gptoss_moe_layer_get_ffn_norm_weight", [_P], _P)
 _sig("gptoss_moe_layer_destroy", [_P], None)
 _sig("gptoss_moe_layer_init_from_checkpoint", [_P, ctypes.POINTER(MoeConfig), _I, _P, _I])
@@ -346,6 +347,20 @@ class MoELayer:
         out = self._out(out, normed, T)
         check(_lib.gptoss_moe_layer_forward_prenormed(self._h, _ptr(normed), _ptr(residual), _ptr(out), T,
                                                       _stream(stream)))
+        return out
+
+    def forward_prenormed_noalloc(self, normed, residual=None, out=None, stream=None):
+        """forward_prenormed with the forward scratch in the library's static
+        device array (no allocation; up to 64 tokens; calls overlapping on one
+        GPU race).  `out` must be given: this call allocates nothing."""
+        if out is None:
+            _bad("forward_prenormed_noalloc needs an output tensor (it allocates nothing)")
+        T = self._rows("normed", normed)
+        if residual is not None:
+            self._rows("residual", residual, T)
+        self._rows("out", out, T)
+        check(_lib.gptoss_moe_layer_forward_prenormed_noalloc(self._h, _ptr(normed), _ptr(residual), _ptr(out), T,
+                                                              _stream(stream)))
         return out
 
     def forward_residual(self, residual, delta, residual_out=None, out=None, stream=None):

@@ -163,6 +163,20 @@ int gptoss_moe_layer_forward_routed(gptoss_moe_layer* layer, const uint16_t* nor
                                     const uint16_t* residual, const int32_t* expert_indices,
                                     const float* expert_weights, uint16_t* output, int num_tokens,
                                     void* stream);
+/* forward_prenormed with no allocation and no use of the layer's own scratch:
+ * no counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the forward scratch is a static device array of 8 MiB
+ * that the library holds on every GPU it runs on until the process ends, so
+ * num_tokens is limited to 64 and to configs whose scratch fits (the
+ * GPT-OSS-120B layer at 64 tokens takes about 3.7 MiB); larger calls return
+ * GPTOSS_ERR_INVALID.  The layer's max_tokens does not bound it.  Calls on one
+ * GPU share that array: calls that overlap in time on one GPU (other streams,
+ * other threads) race, and the layer's trace does not show these calls.
+ * Results are those of gptoss_moe_layer_forward_prenormed. */
+int gptoss_moe_layer_forward_prenormed_noalloc(gptoss_moe_layer* layer, const uint16_t* normed,
+                                               const uint16_t* residual, uint16_t* output, int num_tokens,
+                                               void* stream);
 const uint16_t* gptoss_moe_layer_get_ffn_norm_weight(const gptoss_moe_layer* layer);
 /* The config and device the layer was initialised with. */
 int gptoss_moe_layer_get_config(const gptoss_moe_layer* layer, gptoss_moe_config* cfg, int* device_id);
