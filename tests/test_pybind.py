@@ -1,0 +1,160 @@
+"""The `gptoss` pybind module (hip-kernels_amd/csrc/gptoss_pybind.cpp), the
+reference's Python entry point (bindings.cpp:215-446) over the C ABI.
+
+CPU tests: the module imports without a GPU, carries the reference's module
+attributes and ModelConfig constants (include/config.h), and maps errors as
+the reference bindings do (argument errors -> ValueError, engine failures ->
+RuntimeError).  GPU tests: its MoELayer forwards and InferenceEngine decode
+step, loaded from a checkpoint, against the same weights through the C ABI
+(the ctypes binding), bit for bit.
+"""
+import numpy as np
+import pytest
+
+import ckpt_data
+import moe_data
+
+
+@pytest.fixture(scope="module")
+def gptoss():
+    import torch  # noqa: F401  (the module binds to torch's HIP runtime when torch is present)
+    import gptoss as m
+    return m
+
+
+def test_module_attributes_and_config(gptoss):
+    assert gptoss.__version__ == "0.1.0" and gptoss.MODEL_NAME == "gpt-oss-120b"
+    assert gptoss.ABI_VERSION == 5
+    assert gptoss.profiler_enabled() is True
+    C = gptoss.ModelConfig
+    assert (C.num_layers, C.hidden_size, C.num_q_heads, C.num_kv_heads, C.head_dim) == (36, 2880, 64, 8, 64)
+    assert (C.qkv_size, C.attn_out_size, C.vocab_size, C.gqa_ratio, C.kv_block_size) == (5120, 4096, 201088, 8, 16)
+    assert (C.num_experts, C.num_active_experts, C.expert_intermediate_size) == (128, 4, 2880)
+    assert (C.experts_per_gpu, C.world_size) == (128, 1)   # ep_size 1 (config.h:63-66)
+    assert C.rope_theta == 150000.0 and C.rope_max_pos == 131072 and abs(C.rms_norm_eps - 1e-5) < 1e-12
+    assert C.sliding_window_size == 128 and C.full_attention_interval == 2
+    # config.h:79-85: every second layer (odd index) attends fully
+    assert [C.is_full_attention(l) for l in range(4)] == [False, True, False, True]
+    assert [C.get_window_size(l) for l in range(4)] == [128, 0, 128, 0]
+    assert C().num_layers == 36 and "layers=36" in repr(C())
+    with pytest.raises(AttributeError):
+        C.num_layers = 3
+
+
+def test_engine_errors(gptoss, tmp_path):
+    e = gptoss.InferenceEngine()
+    assert e.is_initialized is False and "initialized=False" in repr(e)
+    for kw in (dict(prompt_tokens=[]), dict(prompt_tokens=[1], max_tokens=0),
+               dict(prompt_tokens=[1], temperature=-1.0), dict(prompt_tokens=[1], top_p=0.0),
+               dict(prompt_tokens=[1], top_p=1.5)):
+        with pytest.raises(ValueError):
+            e.generate(**kw)
+    with pytest.raises(ValueError, match="same length"):
+        e.generate_batch([[1, 2], [3]])
+    with pytest.raises(RuntimeError, match="MoE block only"):
+        e.generate([1, 2, 3])
+    with pytest.raises(RuntimeError, match="Engine init failed"):
+        e.init(str(tmp_path / "missing"))
+    with pytest.raises(RuntimeError, match="Not initialized"):
+        e.decode_step(None, None, 1)
+    e.shutdown()  # a no-op when not initialised
+    with pytest.raises(RuntimeError):
+        gptoss.MoELayer(str(tmp_path / "missing"), 0)
+    with pytest.raises(ValueError, match="max_tokens"):
+        gptoss.MoELayer(str(tmp_path), 0, max_tokens=0)
+
+
+# ---------------------------------------------------------------------------
+# GPU: against the C ABI
+# ---------------------------------------------------------------------------
+E, K, H, I, NL = 8, 4, 256, 128, 3
+
+
+@pytest.fixture(scope="module")
+def model(tmp_path_factory):
+    ws = [moe_data.make_layer(600 + l, E, H, I, bias="random") for l in range(NL)]
+    norms = [moe_data.bf16(np.random.default_rng(610 + l).normal(1.0, 0.1, H)) for l in range(NL)]
+    t = {}
+    for l in range(NL):
+        t.update(ckpt_data.layer_tensors(l, ws[l], E, H, I, norm_w=norms[l]))
+    d = tmp_path_factory.mktemp("pybind_ckpt")
+    ckpt_data.write_shards(str(d), t, n_shards=2)
+    return str(d)
+
+
+def _dev(a, torch):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def _host(t):
+    import torch
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.gpu
+def test_moe_layer_matches_c_abi(gptoss, gpu, model):
+    import torch
+    pl = gptoss.MoELayer(model, 1, max_tokens=160)
+    assert (pl.hidden_size, pl.num_experts, pl.top_k, pl.intermediate_size) == (H, E, K, I)
+    with gpu.Checkpoint(model) as ck:
+        cfg = gpu.default_config(E, 160)
+        cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, K
+        cl = gpu.MoELayer().init_from_checkpoint(cfg, 0, ck, 1)
+    for T in (1, 7, 150):   # decode, and a prefill size (grouped kernels)
+        x, r = moe_data.make_tokens(620 + T, T, H)
+        dx, dr = _dev(x, torch), _dev(r, torch)
+        assert np.array_equal(_host(pl.forward_prenormed(dx, dr)), _host(cl.forward_prenormed(dx, dr))), T
+        assert np.array_equal(_host(pl.forward(dx)), _host(cl.forward(dx))), T
+        s1, s2 = torch.empty_like(dx), torch.empty_like(dx)
+        o1 = pl.forward_residual(dx, dr, residual_out=s1)
+        o2 = cl.forward_residual(dx, dr, residual_out=s2)
+        assert np.array_equal(_host(o1), _host(o2)) and np.array_equal(_host(s1), _host(s2)), T
+        idx = torch.tensor(np.stack([np.random.default_rng(T + i).permutation(E)[:K] for i in range(T)]),
+                           dtype=torch.int32, device="cuda")
+        wts = torch.full((T, K), 0.25, dtype=torch.float32, device="cuda")
+        assert np.array_equal(_host(pl.forward_routed(dx, idx, wts, dr)), _host(cl.forward_routed(dx, idx, wts, dr)))
+    torch.cuda.synchronize()
+    # argument errors before the library: wrong width, host tensor, wrong routing dtype
+    with pytest.raises(ValueError, match="shape"):
+        pl.forward(torch.zeros((2, H - 8), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError, match="cuda:0"):
+        pl.forward(torch.zeros((2, H), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="dtype"):
+        pl.forward_routed(dx, idx.long(), wts)
+    # the library's own checks (more tokens than max_tokens) also arrive as ValueError
+    with pytest.raises(ValueError, match="max_tokens"):
+        pl.forward(torch.zeros((161, H), dtype=torch.bfloat16, device="cuda"))
+    pl.close()
+    cl.destroy()
+
+
+@pytest.mark.gpu
+def test_engine_decode_step_matches_c_abi(gptoss, gpu, model):
+    import torch
+    eng = gptoss.InferenceEngine()
+    eng.init(model, max_tokens=16)
+    assert eng.is_initialized and eng.num_layers == NL and eng.max_tokens == 16
+    with pytest.raises(RuntimeError, match="Already initialized"):
+        eng.init(model)
+    cfg = gpu.default_config(E, 16)
+    cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, K
+    with gpu.Checkpoint(model) as ck:
+        st = gpu.MoEStack.from_checkpoint(cfg, 0, ck)
+    residual = torch.zeros((16, H), dtype=torch.bfloat16, device="cuda")
+    deltas = torch.zeros((NL, 16, H), dtype=torch.bfloat16, device="cuda")
+    for i, (T, use_graph) in enumerate([(3, False), (3, True), (5, True), (3, True)]):
+        r, _ = moe_data.make_tokens(640 + i, T, H)
+        d = np.stack([moe_data.make_tokens(650 + 10 * i + l, T, H)[1] for l in range(NL)])
+        residual[:T].copy_(_dev(r, torch))
+        deltas[:, :T].copy_(_dev(d, torch))
+        st.residual[:T].copy_(_dev(r, torch))
+        st.deltas[:, :T].copy_(_dev(d, torch))
+        eng.decode_step(residual, deltas, T, use_graph=use_graph)
+        want = st.decode_step(T, use_graph=use_graph)
+        torch.cuda.synchronize()
+        assert np.array_equal(_host(residual[:T]), _host(want)), (i, T)
+    with pytest.raises(ValueError, match="num_tokens"):
+        eng.decode_step(residual, deltas, 17)
+    eng.shutdown()
+    assert not eng.is_initialized
+    st.destroy()
