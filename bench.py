@@ -241,13 +241,15 @@ def timed_graph(torch, fn, per_graph: int = 5, replays: int = 4):
     return t0.elapsed_time(t1) / (per_graph * replays)
 
 
-def bench_prefill(g, torch, wc, T: int = 4096, reps: int = 5):
+def bench_prefill(g, torch, wc, T: int = 4096, reps: int = 5, block_scaled: int = 0):
     """one GPT-OSS-120B layer forward at T tokens with
     Zipf(1.1) routing injected (forward_routed: plan, grouped gate_up + SwiGLU
     and grouped down on the matrix cores, combine), timed by graph replay;
-    per-launch times from HIP events on eager forwards."""
+    per-launch times from HIP events on eager forwards.  block_scaled: the
+    layer's prefill_block_scaled (0, the default: bf16 products; 1:
+    block-scaled fp4 x two e4m3 parts; 2: one e4m3 part)."""
     idx, wt = zipf_routing(4096, T, K_TOP)
-    cfg = g.default_config(E, T)
+    cfg = g.default_config(E, T, prefill_block_scaled=block_scaled)
     L = g.MoELayer().init(cfg, 0, wc["router_w"], wc["router_b"], wc["b1"], wc["b2"], tiled=wc["tiled"])
     gen = torch.Generator(device="cuda")
     gen.manual_seed(4096)
@@ -267,7 +269,8 @@ def bench_prefill(g, torch, wc, T: int = 4096, reps: int = 5):
     flops_w1 = 2.0 * T * K_TOP * (2 * I) * H
     flops_w2 = 2.0 * T * K_TOP * H * I
     w1 = w1_ms / n
-    res = dict(tokens=T, routing="zipf(1.1), top-4 distinct", ms_per_layer=ms, tokens_per_s=T / (ms / 1e3),
+    res = dict(tokens=T, routing="zipf(1.1), top-4 distinct", prefill_block_scaled=block_scaled,
+               ms_per_layer=ms, tokens_per_s=T / (ms / 1e3),
                tflops_layer=(flops_w1 + flops_w2) / (ms / 1e3) / 1e12,
                kernel_ms=dict(plan=plan_ms / n, gate_up=w1, down=w2_ms / n, combine=c_ms / n),
                gate_up_tflops=flops_w1 / (w1 / 1e3) / 1e12)
@@ -435,28 +438,145 @@ def bench_stack(g, torch, layers: int = 36, T: int = 32, steps: int = 256):
                 step="per layer: residual += delta, RMSNorm, MoE (gptoss_moe_stack_decode_step, one hipGraph)")
 
 
-def cpu_baseline(seconds: float, threads: int):
-    """The oracle (C, pthreads) on GPT-OSS-120B-shaped layers at batch 64,
-    repeated until `seconds` of wall time; returns tokens/s."""
+def _host_info(threads: int) -> dict:
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return dict(cpu_model=model, nproc=os.cpu_count(), usable_cpus=usable, threads_all_cores=threads)
+
+
+def _timed(fn, seconds: float):
+    """Repeat fn until `seconds` of wall time (at least once); (calls, s)."""
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return n, el
+
+
+def cpu_baseline(g, torch, seconds: float, threads: int):
+    """The C oracle (oracle/moe_oracle.c, pthreads) on this host, on bounded
+    samples of the BASELINE configurations, and the headline GPU path checked
+    against it on the same inputs.
+
+    Returns (cpu_baseline, accuracy).  cpu_baseline's `value` is config 2 at
+    batch 64 on `threads` threads for about `seconds`; `per_config` holds
+    one-shot figures for config 0 (E=32, T=1), config 2 at B=1/8/32, config 1
+    (router + top-k, fp32 logits, a 512-token sample of T=4096), config 3 (a
+    32-token sample of the T=4096 Zipf routing) and config 4 (one layer-step
+    at B=32, x36 layers), plus a 1-thread figure.  `accuracy`: the GPU
+    matrix-core decode path (the headline) and the exact path at B=64 on the
+    same weights and tokens, against the oracle in this build's canonical
+    order and (16 tokens) in the reference's own order."""
+    import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import moe_data
     import moe_oracle as orc
+    info = _host_info(threads)
+    log("cpu baseline: generating GPT-OSS-120B-shaped weights on the host")
     w = moe_data.make_layer(99, E, H, I, bias="zero")
     T = 64
     x, res = moe_data.make_tokens(99, T, H)
     orc.moe_forward(w, x[:1], res[:1], E, K_TOP, H, I, nthreads=threads)  # warm
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        orc.moe_forward(w, x, res, E, K_TOP, H, I, nthreads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return dict(value=n * T / el, unit="tokens/s", cores=threads, kind="port",
-                sample=f"{n} oracle forwards of a GPT-OSS-120B-shaped MoE layer (E=128, H=I=2880, top-4) at "
-                       f"batch 64, {el:.1f} s, {threads} threads")
+    ref = {}
+
+    def main_fwd():
+        ref["out"] = orc.moe_forward(w, x, res, E, K_TOP, H, I, nthreads=threads)
+    n, el = _timed(main_fwd, seconds)
+    value = n * T / el
+    per = {}
+    log("cpu baseline: per-config samples")
+    for B in (1, 8, 32):
+        n_b, el_b = _timed(lambda: orc.moe_forward(w, x[:B], res[:B], E, K_TOP, H, I, nthreads=threads), 0.0)
+        per[f"cfg2_b{B}"] = dict(tokens_per_s=n_b * B / el_b, seconds=el_b, sample=f"{n_b} forward(s) at batch {B}")
+    per["cfg2_b64"] = dict(tokens_per_s=value, sample=f"{n} forwards at batch 64")
+    per["cfg4_stack36_b32"] = dict(tokens_per_s=per["cfg2_b32"]["tokens_per_s"] / 36,
+                                   sample="one layer-step at batch 32 (cfg2_b32) x 36 layers")
+    n1, el1 = _timed(lambda: orc.moe_forward(w, x[:4], res[:4], E, K_TOP, H, I, nthreads=1), 0.0)
+    per["cfg2_b4_1thread"] = dict(tokens_per_s=n1 * 4 / el1, threads=1, seconds=el1,
+                                  sample=f"{n1} forward(s) at batch 4")
+    Tz = 32
+    idx, wt = zipf_routing(4096, 4096, K_TOP)
+    xz, rz = moe_data.make_tokens(4096, Tz, H)
+    n3, el3 = _timed(lambda: orc.moe_forward_routed(w, xz, rz, idx[:Tz], wt[:Tz], E, K_TOP, H, I,
+                                                     nthreads=threads), 0.0)
+    per["cfg3_prefill_zipf"] = dict(tokens_per_s=n3 * Tz / el3, seconds=el3,
+                                    sample=f"the first {Tz} tokens of the T=4096 Zipf(1.1) routing, expert half")
+    Tr = 512
+    xr, _ = moe_data.make_tokens(1, Tr, H)
+    rw, rb = w["router_w"], w["router_b"]
+
+    def route_fwd():
+        lg = orc.router(xr, rw, rb, logits_fp32=True)
+        orc.topk_softmax(lg, K_TOP)
+    nr, elr = _timed(route_fwd, 0.0)
+    per["cfg1_router_fp32"] = dict(tokens_per_s=nr * Tr / elr, threads=1, seconds=elr,
+                                   sample=f"router GEMV + top-4 softmax over {Tr} of T=4096 tokens")
+    w32 = moe_data.make_layer(7, 32, H, I, bias="zero")
+    x32, r32 = moe_data.make_tokens(7, 1, H)
+    n0, el0 = _timed(lambda: orc.moe_forward(w32, x32, r32, 32, K_TOP, H, I, nthreads=threads), 0.0)
+    per["cfg0_e32_t1"] = dict(tokens_per_s=n0 / el0, seconds=el0, sample=f"{n0} forward(s), E=32, T=1")
+    del w32
+    log(json.dumps(per))
+    cpu = dict(value=value, unit="tokens/s", cores=threads, kind="port",
+               sample=f"{n} oracle forwards of a GPT-OSS-120B-shaped MoE layer (E=128, H=I=2880, top-4) at "
+                      f"batch 64, {el:.1f} s, {threads} threads", per_config=per, **info)
+
+    # accuracy of the GPU paths on these weights and tokens
+    log("accuracy: GPU decode paths at batch 64 against the oracle")
+    acc = dict(batch=T, tolerance="max-abs 2e-2, mean-rel 1e-3 (north star)",
+               weights="make_layer(99): uniform e2m1 codes, e8m0 119..123, router N(0, 0.02), zero biases")
+    t = {nm: torch.from_numpy(np.ascontiguousarray(w[nm]).view(np.int16) if w[nm].dtype == np.uint16
+                              else np.ascontiguousarray(w[nm])).cuda()
+         for nm in ("router_w", "router_b", "w1_packed", "w1_scales", "w2_packed", "w2_scales", "w1_bias", "w2_bias")}
+    for nm in ("router_w", "router_b", "w1_bias", "w2_bias"):
+        t[nm] = t[nm].view(torch.bfloat16)
+    n1b, s1b = g.tiled_size(2 * I, H)
+    n2b, s2b = g.tiled_size(H, I)
+    tiled = [torch.empty(E * nb, dtype=torch.uint8, device="cuda") for nb in (n1b, s1b, n2b, s2b)]
+    for e in range(E):
+        g.pack_tiled(t["w1_packed"][e], t["w1_scales"][e], 2 * I, H, tiled[0][e * n1b:(e + 1) * n1b],
+                     tiled[1][e * s1b:(e + 1) * s1b])
+        g.pack_tiled(t["w2_packed"][e], t["w2_scales"][e], H, I, tiled[2][e * n2b:(e + 1) * n2b],
+                     tiled[3][e * s2b:(e + 1) * s2b])
+    dx = torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16)
+    dr = torch.from_numpy(res.view(np.int16)).cuda().view(torch.bfloat16)
+    outs = {}
+    for name, exact in (("matrix_core", False), ("exact", True)):
+        L = g.MoELayer().init(g.default_config(E, T, decode_exact=exact), 0, t["router_w"], t["router_b"],
+                              t["w1_bias"], t["w2_bias"], tiled=tiled)
+        outs[name] = L.forward_prenormed(dx, dr).cpu().view(torch.int16).numpy().view(np.uint16)
+        torch.cuda.synchronize()
+        L.destroy()
+    sel = slice(0, 16)
+    ref1 = orc.moe_forward(w, x[sel], res[sel], E, K_TOP, H, I, nthreads=threads, order=1)
+    keys = ("max_abs", "mean_rel", "norm_rel", "mismatch_frac", "over_abs_frac", "row_steps")
+
+    def stats(a, b):
+        c = moe_data.mfma_stats(a, b)
+        return {k: c[k] for k in keys}
+    acc["headline_matrix_core_vs_oracle_canonical"] = stats(outs["matrix_core"], ref["out"])
+    acc["headline_matrix_core_vs_oracle_reference_order_16_tokens"] = stats(outs["matrix_core"][sel], ref1)
+    acc["exact_vs_oracle_canonical"] = stats(outs["exact"], ref["out"])
+    acc["exact_vs_oracle_reference_order_16_tokens"] = stats(outs["exact"][sel], ref1)
+    acc["exact_bit_identical_to_canonical"] = bool(np.array_equal(outs["exact"], ref["out"]))
+    del tiled, t
+    torch.cuda.empty_cache()
+    return cpu, acc
 
 
 def main():
@@ -476,6 +596,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true",
                     help="decode sweep only (skip the exact-path, prefill, router and 36-layer stack legs)")
     ap.add_argument("--stack-layers", type=int, default=36)
+    ap.add_argument("--leg", choices=("prefill", "router", "stack"),
+                    help="only run this leg of the bench and print its JSON (profiler runs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -488,6 +610,17 @@ def main():
         copy_calibration(torch)
         return
     import gptoss_moe as g
+
+    if args.leg:
+        if args.leg == "prefill":
+            wc = make_copy(g, torch, 1000)
+            res = bench_prefill(g, torch, wc)
+        elif args.leg == "router":
+            res = bench_router(g, torch)
+        else:
+            res = bench_stack(g, torch, layers=args.stack_layers)
+        print(json.dumps({"leg": args.leg, **res}), flush=True)
+        return
 
     batches = [int(b) for b in args.batches.split(",")]
     headline_b = max(batches)
@@ -520,6 +653,13 @@ def main():
         log("prefill T=4096 (zipf routing)")
         extra["prefill"] = bench_prefill(g, torch, copies[0])
         log(json.dumps(extra["prefill"]))
+        # the block-scaled alternatives (not the default: outside the tolerance)
+        extra["prefill"]["block_scaled_variants"] = {}
+        for m in (1, 2):
+            v = bench_prefill(g, torch, copies[0], block_scaled=m)
+            extra["prefill"]["block_scaled_variants"][str(m)] = dict(
+                (key, v[key]) for key in ("ms_per_layer", "kernel_ms", "gate_up_tflops"))
+        log(json.dumps(extra["prefill"]["block_scaled_variants"]))
         log("router + top-k T=4096 fp32 logits")
         extra["router"] = bench_router(g, torch)
         log(json.dumps(extra["router"]))
@@ -534,11 +674,13 @@ def main():
         log(f"{args.stack_layers}-layer stack at batch 32")
         extra["stack"] = bench_stack(g, torch, layers=args.stack_layers)
         log(json.dumps(extra["stack"]))
-    cpu = None
+    cpu, accuracy = None, None
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         log(f"cpu baseline: oracle, {threads} threads, ~{args.cpu_seconds} s")
-        cpu = cpu_baseline(args.cpu_seconds, threads)
+        cpu, accuracy = cpu_baseline(g, torch, args.cpu_seconds, threads)
+        log(json.dumps(cpu))
+        log(json.dumps(accuracy))
     line = {
         "metric": "MoE-layer tokens/s (GPT-OSS-120B shape, decode)",
         "value": head["tokens_per_s"],
@@ -559,6 +701,7 @@ def main():
         "hbm_frac_of_peak": head["hbm_frac"],
         "roofline": rf,
         "cpu_baseline": cpu,
+        "accuracy": accuracy,
         "sweep": {str(k): v for k, v in sweep.items()},
     }
     line.update(extra)

@@ -119,7 +119,7 @@ struct ScopedDevice {
 // launch starts, and every launch leaves it zero.
 struct WsLayout {
   size_t queue, logits, idx, w, counts, offsets, gmap, ptok, active, n_active, tasks, act, y, pchunk, normed,
-      sumres, total;
+      sumres, xq, xqs, aq, aqs, total;
 };
 
 WsLayout ws_layout(const gptoss_moe_config& c) {
@@ -148,6 +148,13 @@ WsLayout ws_layout(const gptoss_moe_config& c) {
   l.pchunk = take(plan_chunk_ints(static_cast<int>(S), static_cast<int>(E)) * 4);
   l.normed = take(T * H * 2);
   l.sumres = take(T * H * 2);
+  // the block-scaled prefill's quantised inputs: e4m3 hi | lo per 32-element
+  // block (64 bytes) and a scale dword, for the tokens and for the activations
+  const bool mx = c.prefill_block_scaled && c.prefill_min_tokens > 0 && c.max_tokens >= c.prefill_min_tokens;
+  l.xq = take(mx ? T * H * 2 : 0);
+  l.xqs = take(mx ? T * (H / 32) * 4 : 0);
+  l.aq = take(mx ? S * I * 2 : 0);
+  l.aqs = take(mx ? S * (I / 32) * 4 : 0);
   l.total = off;
   return l;
 }
@@ -172,6 +179,10 @@ struct Scratch {
   int32_t* gqueue = nullptr;   // tile queue of the persistent grouped kernel (zeroed; left zeroed)
   int32_t* pchunk = nullptr;   // scratch of the multi-launch plan (many tokens)
   uint16_t* gate_up = nullptr; // bf16 gate_up trace (layer-owned), or null
+  uint8_t* xq = nullptr;       // block-scaled prefill: quantised tokens and activations
+  uint32_t* xqs = nullptr;
+  uint8_t* aq = nullptr;
+  uint32_t* aqs = nullptr;
   PlanBufs plan() const { return PlanBufs{counts, offsets, gmap, ptok, active, n_active, tasks, pchunk}; }
 };
 
@@ -194,6 +205,10 @@ Scratch carve(void* base, const WsLayout& l) {
   c.pchunk = reinterpret_cast<int32_t*>(ws + l.pchunk);
   c.normed = reinterpret_cast<uint16_t*>(ws + l.normed);
   c.sumres = reinterpret_cast<uint16_t*>(ws + l.sumres);
+  c.xq = reinterpret_cast<uint8_t*>(ws + l.xq);
+  c.xqs = reinterpret_cast<uint32_t*>(ws + l.xqs);
+  c.aq = reinterpret_cast<uint8_t*>(ws + l.aq);
+  c.aqs = reinterpret_cast<uint32_t*>(ws + l.aqs);
   return c;
 }
 
@@ -298,6 +313,7 @@ int gptoss_moe_config_default(gptoss_moe_config* cfg, int num_experts, int max_t
   cfg->max_tokens = max_tokens;
   cfg->prefill_min_tokens = 128;
   cfg->decode_exact = 0;
+  cfg->prefill_block_scaled = 0;
   return ok();
 }
 
@@ -348,6 +364,8 @@ static int layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int dev
     return fail(GPTOSS_ERR_INVALID, "prefill_min_tokens=%d must be >= 0", cfg->prefill_min_tokens);
   if (cfg->decode_exact != 0 && cfg->decode_exact != 1)
     return fail(GPTOSS_ERR_INVALID, "decode_exact=%d must be 0 or 1", cfg->decode_exact);
+  if (cfg->prefill_block_scaled < 0 || cfg->prefill_block_scaled > 2)
+    return fail(GPTOSS_ERR_INVALID, "prefill_block_scaled=%d must be 0, 1 or 2", cfg->prefill_block_scaled);
   if (H % kTileRows != 0) return fail(GPTOSS_ERR_UNSUPPORTED, "hidden_size=%d must be a multiple of 64", H);
   int rc = check_mxfp4_shape(2 * I, H);
   if (rc != GPTOSS_OK) return rc;
@@ -605,9 +623,26 @@ static int layer_experts(gptoss_moe_layer* L, const Scratch& S, const uint16_t* 
     g.queue = S.gqueue;
     g.num_cus = L->num_cus;
     g.timer = pf.timer(1);
+    if (c.prefill_block_scaled) {  // the tokens as e4m3 parts, then block-scaled products
+      const KernelTimer t1 = pf.timer(1);
+      HIP_TRY(launch_quant_fp8x2(normed, T, c.hidden_size, S.xq, S.xqs, s, KernelTimer{t1.start, nullptr}),
+              "quantise launch");
+      g.timer = KernelTimer{nullptr, t1.stop};
+      g.xq = S.xq;
+      g.xqs = S.xqs;
+      g.outq = S.aq;
+      g.outqs = S.aqs;
+      g.mx_single = c.prefill_block_scaled == 2;
+    }
     HIP_TRY(launch_grouped_mxfp4(g, s), "grouped gate_up launch");
     g.x = S.act;
     g.row_index = nullptr;
+    if (c.prefill_block_scaled) {
+      g.xq = S.aq;
+      g.xqs = S.aqs;
+      g.outq = nullptr;
+      g.outqs = nullptr;
+    }
     g.wn = L->w2n;
     g.ws = L->w2s;
     g.N = c.hidden_size;

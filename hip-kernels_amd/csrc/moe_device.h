@@ -64,6 +64,43 @@ __device__ __forceinline__ float gx_swiglu(float g, float u, float alpha, float 
   return (u + 1.0f) * glu;
 }
 
+// ---- activations as two e4m3 parts for the block-scaled products ----------
+// A 32-element block with largest magnitude m is split as v = (hi + lo/32) s,
+// s = 2^(e - 7), e = the exponent of m: |v / s| < 256 fits e4m3 (max 448),
+// hi = RNE(v / s) and lo = RNE((v / s - hi) * 32).  For |v| >= 2^-13 m, hi is
+// a normal e4m3 value (4 significant bits), so v / s - hi has at most four
+// significant bits and lies on lo's grid: the split is exact.  (gfx950's
+// v_cvt_pk_fp8_f32 encodes OCP e4m3 with round to nearest even.)
+
+// e8m0 codes of s and of s / 32, packed as code(s) | code(s / 32) << 8, and
+// 1 / s; m >= 0 (inf or NaN gives codes of 2^121 that fp8x2_quant4 pairs
+// with NaN parts).  Blocks below 2^-114 take s = 2^-121 (their parts
+// underflow, an error below 2^-120).
+__device__ __forceinline__ uint32_t fp8x2_codes(float m, float& inv_s) {
+  int e = static_cast<int>((__float_as_uint(m) >> 23) & 0xffu) - 127;
+  e = e < -114 ? -114 : e;
+  inv_s = __uint_as_float(static_cast<uint32_t>(127 + 7 - e) << 23);
+  return static_cast<uint32_t>(e + 120) | (static_cast<uint32_t>(e + 115) << 8);
+}
+
+// Four values of one block -> four hi bytes and four lo bytes (byte i =
+// element i).  finite = false (the block holds inf or NaN): NaN parts.
+__device__ __forceinline__ void fp8x2_quant4(float v0, float v1, float v2, float v3, float inv_s, bool finite,
+                                             uint32_t& hi, uint32_t& lo) {
+  const float a0 = v0 * inv_s, a1 = v1 * inv_s, a2 = v2 * inv_s, a3 = v3 * inv_s;  // exact: power-of-two scale
+  uint32_t h = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false));
+  h = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, static_cast<int>(h), true));
+  const int hs = static_cast<int>(h);
+  const float r0 = (a0 - __builtin_amdgcn_cvt_f32_fp8(hs, 0)) * 32.0f;  // exact residuals
+  const float r1 = (a1 - __builtin_amdgcn_cvt_f32_fp8(hs, 1)) * 32.0f;
+  const float r2 = (a2 - __builtin_amdgcn_cvt_f32_fp8(hs, 2)) * 32.0f;
+  const float r3 = (a3 - __builtin_amdgcn_cvt_f32_fp8(hs, 3)) * 32.0f;
+  uint32_t l = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false));
+  l = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(r2, r3, static_cast<int>(l), true));
+  hi = finite ? h : 0x7f7f7f7fu;
+  lo = finite ? l : 0u;
+}
+
 // e8m0 scale byte -> fp32 by placing the code in the exponent field
 // (code 0 -> +0, 255 -> +inf).
 __device__ __forceinline__ float e8m0_to_f32(uint32_t code) {

@@ -212,11 +212,33 @@ struct GroupedArgs {
   int32_t* queue;  // null, or grouped_queue_ints() zeroed ints (persistent grid; left zeroed)
   int num_cus;     // with a queue: compute units of the device
   KernelTimer timer;
+  // Block-scaled variant (v_mfma_scale_f32_16x16x128_f8f6f4, fp4 weights x
+  // fp8 activations): xq / xqs non-null select it.  xq, xqs: the rows of x
+  // quantised by launch_quant_fp8x2 (read through row_index like x; x itself
+  // is then read only for weights with e8m0 codes 0 or 255).  gated: outq /
+  // outqs (may be null) receive the activations quantised the same way, the
+  // down product's input.
+  const uint8_t* xq;
+  const uint32_t* xqs;
+  uint8_t* outq;
+  uint32_t* outqs;
+  int mx_single;  // block-scaled: the hi part alone (one product per block)
 };
 // Ints of the persistent grouped kernel's tile queue.
 constexpr int grouped_queue_ints() { return 9 * 32; }
 bool grouped_supported(int N, int K, int E);
 hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s);
+
+// Activations for the block-scaled products: every 32-element block of a bf16
+// row becomes two e4m3 parts with one power-of-two scale s = 2^(e - 7), e the
+// exponent of the block's largest magnitude:
+//   hi = RNE(v / s),  lo = RNE((v / s - hi) * 32),  v = (hi + lo / 32) * s,
+// exact for every |v| >= max * 2^-13 and within max * 2^-17 below.  Row r,
+// block b: q[r][64 b .. 64 b + 31] = hi, [+32 .. +63] = lo;
+// qs[r][b] = e8m0 code of s | (code of s / 32) << 8.  A block holding inf or
+// NaN gets NaN parts.
+hipError_t launch_quant_fp8x2(const uint16_t* x, int rows, int K, uint8_t* q, uint32_t* qs, hipStream_t s,
+                              const KernelTimer& t = KernelTimer{});
 
 // Row-major MXFP4 [N][K/2] + [N][K/32] -> tiled layout.
 hipError_t launch_pack_tiled(const uint8_t* packed, const uint8_t* scales, int N, int K,

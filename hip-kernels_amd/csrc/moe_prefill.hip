@@ -104,6 +104,11 @@ struct GroupedParams {
   float alpha, limit;
   int nwt;                   // work-group n-tiles: ceil(N / (64 kGW))
   int* queue;                // null: one tile per work-group; else per-XCD tile counters (persistent grid)
+  // block-scaled variant (grouped_mx_kernel)
+  const uint8_t* xq;         // [*][K/32][64] e4m3 hi | lo parts of x's rows
+  const uint32_t* xqs;       // [*][K/32] their scale codes
+  uint8_t* outq;             // gated, may be null: [rows][N/64][64] the activations' parts
+  uint32_t* outqs;           // [rows][N/64] their scale codes
 };
 
 struct TileCoord {
@@ -471,6 +476,386 @@ __device__ __forceinline__ void run_tile(const GroupedParams& a, const TileCoord
     grouped_tile<kGated, false, 2>(a, tc, xs, lane, w);
 }
 
+// ---- block-scaled variant: v_mfma_scale_f32_16x16x128_f8f6f4 ----------------
+//
+// The same tiles (kBM tokens x 256 weight rows, four waves of one 64-row
+// tiled MXFP4 tile each), with the products on the block-scaled matrix core:
+// the fp4 weights and their e8m0 scales are its A operand and scale as they
+// are stored, and the activations enter as two e4m3 parts with per-block
+// scales (launch_quant_fp8x2), hi and lo, one product each.  No register
+// decodes the weights.  One product covers 128 K (four blocks): lane l holds
+// row l % 16 of a 16-row sub-tile and block l / 16 of the four (its 16 bytes
+// of fp4), and for B token l % 16 at K 16(l/16)..+15 and 64 + 16(l/16)..+15;
+// the scale of (row or token r, block kb) comes from lane r + 16 kb, its byte
+// picked by op_sel (sub-tile i: byte i of the dword holding rows 16i + r;
+// hi: byte 0, lo: byte 1 of the token's code pair).  Output layout as the
+// bf16 product: lane l holds rows 4(l/16)..+3 of the sub-tile for token l % 16.
+//
+// One work-group per CU; the LDS ring holds kMxGroups groups of four blocks
+// (stage = one block: the tokens' hi | lo rows, each wave's tiled KiB and its
+// scale dwords, the tokens' scale codes), every operand reaching it by direct
+// global -> LDS loads.  A group's products run while the next groups' loads
+// are in flight; the work-group synchronises once per group.
+constexpr int kMxW = 4;                       // waves per work-group (a 64-row weight tile each)
+constexpr int kMxRingBytes = 160 * 1024 - 64;  // the LDS of a CU, less the queue words
+
+template <int kFrags>
+struct MxRing {
+  static constexpr int kF = kFrags;                       // 16-token fragments per stage
+  static constexpr int kAOff = kFrags * 1024;             // tokens: 16 kF rows x 64 B
+  static constexpr int kASOff = kAOff + kMxW * 1024;      // each wave's tiled block
+  static constexpr int kBSOff = kASOff + kMxW * 64;       // each wave's scale dwords
+  static constexpr int kBytes = kBSOff + 64 * kFrags;     // the tokens' scale code pairs (4 B each)
+  static constexpr int kFit = kMxRingBytes / (4 * kBytes);
+  static constexpr int kGroups = kFit < 4 ? kFit : 4;     // 128-K groups in the ring
+  static constexpr int kStages = 4 * kGroups;
+  static constexpr int kKiBPerWave = kFrags >= kMxW ? kFrags / kMxW : 1;
+  static_assert(kGroups >= 3, "the ring holds the computed group and two in flight");
+};
+
+// s_waitcnt vmcnt(G * 4 * per) for a wave issuing `per` loads per block
+// (wave-uniform: 2, 4 or 6).
+template <int G>
+__device__ __forceinline__ void wait_mx_groups(int per) {
+  if (per >= 6) wait_vm<(G * 24 < 63 ? G * 24 : 63)>();
+  else if (per >= 4) wait_vm<(G * 16 < 63 ? G * 16 : 63)>();
+  else wait_vm<(G * 8 < 63 ? G * 8 : 63)>();
+}
+
+typedef int mx_v8i __attribute__((ext_vector_type(8)));
+
+template <bool kGated, bool kFull, int kCls, bool kLo>
+__device__ __forceinline__ void mx_tile(const GroupedParams& a, const TileCoord& tc, uint8_t* xs, int lane, int w) {
+  const TiledGeom& g = a.g;
+  const int N = g.N, nb = g.nb;
+  const int mc = min(kBM, tc.cnt - tc.m0);
+  using R = MxRing<kCls>;
+  constexpr int kFrags = R::kF, kStages = R::kStages, kStageBytes = R::kBytes, kGroups = R::kGroups;
+  constexpr int kAOff = R::kAOff, kASOff = R::kASOff, kBSOff = R::kBSOff, kKW = R::kKiBPerWave;
+  const int nfr = kFull ? kFrags : (mc + 15) >> 4;  // 16-token fragments holding rows
+  const int tile = tc.nt * kMxW + w;
+  const bool active = tile < N / kTileRows;  // wave-uniform
+  const int ngroups = (nb + 3) >> 2;
+  const size_t qrow = static_cast<size_t>(nb) * 64;
+
+  // Token KiBs this wave loads: kk = w + kMxW c.  Lane L stages token
+  // 16 kk + L / 4, 16-byte chunk L % 4 of its 64-byte block row, holding the
+  // row's chunk (L % 4) ^ swz (swz = (token / 4) % 4: the 16 tokens of a B
+  // read at one chunk hit distinct banks 8 lanes at a time).  Lanes < 16 also
+  // stage the scale code pair of token 16 kk + L.
+  const uint8_t* qsrc[kKW];
+  const uint32_t* ssrc[kKW];
+  int nkw = 0;
+#pragma unroll
+  for (int c = 0; c < kKW; ++c) {
+    const int kk = w + kMxW * c;
+    if (kk < kFrags) nkw = c + 1;
+    const int j = 16 * (kk < kFrags ? kk : 0) + (lane >> 2);
+    const int jr = j < mc ? j : 0;
+    const int prow = a.row_index ? a.row_index[tc.off + tc.m0 + jr] : tc.off + tc.m0 + jr;
+    qsrc[c] = a.xq + static_cast<size_t>(prow) * qrow + 16 * ((lane & 3) ^ ((j >> 2) & 3));
+    const int js = 16 * (kk < kFrags ? kk : 0) + (lane & 15);
+    const int jsr = js < mc ? js : 0;
+    const int psrow = a.row_index ? a.row_index[tc.off + tc.m0 + jsr] : tc.off + tc.m0 + jsr;
+    ssrc[c] = a.xqs + static_cast<size_t>(psrow) * nb;
+  }
+  const int per = 2 + 2 * nkw;  // this wave's loads per block
+
+  const size_t eoff_n = static_cast<size_t>(tc.e) * g.nib_bytes;
+  const size_t eoff_s = static_cast<size_t>(tc.e) * g.scale_bytes + g.mscale_off;
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.wn + eoff_n), 0, static_cast<int>(g.nib_bytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.ws + eoff_s), 0, static_cast<int>(static_cast<size_t>(N) * nb), 0x00020000);
+  const int wvoff = active ? tile * nb * 1024 + 16 * lane : static_cast<int>(g.nib_bytes);
+  const int svoff = active ? tile * nb * 64 + 4 * (lane & 15) : N * nb;
+
+  // Block kb's loads into its stage (blocks past nb load block nb - 1: they
+  // keep every wave's load count uniform and are never read as data).
+  auto issue = [&](int kb) __attribute__((always_inline)) {
+    const int bb = kb < nb ? kb : nb - 1;
+    uint8_t* sp = xs + (kb % kStages) * kStageBytes;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void_t*)(sp + kAOff + 1024 * w), 16, wvoff, bb * 1024, 0, 0);
+    if (lane < 16)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_void_t*)(sp + kASOff + 64 * w), 4, svoff, bb * 64, 0, 0);
+#pragma unroll
+    for (int c = 0; c < kKW; ++c)
+      if (c < nkw) {
+        const int kk = w + kMxW * c;
+        __builtin_amdgcn_global_load_lds(qsrc[c] + static_cast<size_t>(bb) * 64, (lds_void_t*)(sp + 1024 * kk), 16, 0, 0);
+        if (lane < 16)
+          __builtin_amdgcn_global_load_lds(ssrc[c] + bb, (lds_void_t*)(sp + kBSOff + 64 * kk), 4, 0, 0);
+      }
+  };
+#pragma unroll
+  for (int kb = 0; kb < 4 * kGroups; ++kb) issue(kb);
+
+  f32x4_t acc[4][kFrags];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < kFrags; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int n = lane & 15, gq = lane >> 4;
+  const int swz = (n >> 2) & 3;
+  bool spec = false;
+  for (int q = 0; q < ngroups; ++q) {
+    // This wave's loads of group q have landed once at most the groups
+    // issued after it are outstanding; after the barrier every wave's have,
+    // and no wave reads group q - 1's stages any more.
+    if (q == 0) wait_mx_groups<kGroups - 1>(per);
+    else wait_mx_groups<kGroups - 2>(per);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    if (q > 0) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) issue(4 * (q + kGroups - 1) + b);
+    }
+    if (!active) continue;
+    // A operands: the lane's block 4q + gq, the four 16-byte slots holding its
+    // row of each sub-tile; dword i of slot 16 g' + n = bytes 4 g'..4 g' + 3
+    // of row 16 i + n.  Blocks past nb contribute zeros.
+    const int ba = 4 * q + gq;
+    mx_v8i av[4];
+    uint32_t sa = 0x7f7f7f7fu;
+    if (ba < nb) {
+      const uint8_t* sp = xs + (ba % kStages) * kStageBytes;
+      u32x4_t r[4];
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) r[gg] = *reinterpret_cast<const u32x4_t*>(sp + kAOff + 1024 * w + 16 * (16 * gg + n));
+      sa = *reinterpret_cast<const uint32_t*>(sp + kASOff + 64 * w + 4 * n);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        av[i] = mx_v8i{static_cast<int>(r[0][i]), static_cast<int>(r[1][i]), static_cast<int>(r[2][i]),
+                       static_cast<int>(r[3][i]), 0, 0, 0, 0};
+      spec |= has_special_code(sa, 0xffffffffu);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = mx_v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    // B operands: chunks g % 2 (hi) and 2 + g % 2 (lo) of block 4q + g/2 (K
+    // 16 g..16 g + 15) and of block 4q + 2 + g/2 (K 64 + 16 g..); the scale
+    // pair of block 4q + g.
+    const int b0 = 4 * q + (gq >> 1), b1 = b0 + 2;
+    const uint8_t* s0 = xs + (b0 % kStages) * kStageBytes;
+    const uint8_t* s1 = xs + (b1 % kStages) * kStageBytes;
+    const uint8_t* ss = xs + ((4 * q + gq) % kStages) * kStageBytes + kBSOff;
+    const int ch = 16 * ((gq & 1) ^ swz), cl = 16 * ((2 + (gq & 1)) ^ swz);
+    const bool h0 = b0 < nb, h1 = b1 < nb, hs = 4 * q + gq < nb;
+#pragma unroll
+    for (int t = 0; t < kFrags; ++t) {
+      if (kFull || t < nfr) {
+        const int ro = 1024 * t + 64 * n;
+        u32x4_t z{0u, 0u, 0u, 0u};
+        const u32x4_t hA = h0 ? *reinterpret_cast<const u32x4_t*>(s0 + ro + ch) : z;
+        const u32x4_t hB = h1 ? *reinterpret_cast<const u32x4_t*>(s1 + ro + ch) : z;
+        const u32x4_t lA = kLo && h0 ? *reinterpret_cast<const u32x4_t*>(s0 + ro + cl) : z;
+        const u32x4_t lB = kLo && h1 ? *reinterpret_cast<const u32x4_t*>(s1 + ro + cl) : z;
+        const uint32_t sb = hs ? *reinterpret_cast<const uint32_t*>(ss + 4 * (16 * t + n)) : 0x7f7fu;
+        const mx_v8i bh{static_cast<int>(hA[0]), static_cast<int>(hA[1]), static_cast<int>(hA[2]), static_cast<int>(hA[3]),
+                        static_cast<int>(hB[0]), static_cast<int>(hB[1]), static_cast<int>(hB[2]), static_cast<int>(hB[3])};
+        const mx_v8i bl{static_cast<int>(lA[0]), static_cast<int>(lA[1]), static_cast<int>(lA[2]), static_cast<int>(lA[3]),
+                        static_cast<int>(lB[0]), static_cast<int>(lB[1]), static_cast<int>(lB[2]), static_cast<int>(lB[3])};
+        const int sai = static_cast<int>(sa), sbi = static_cast<int>(sb);
+        acc[0][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bh, acc[0][t], 4, 0, 0, sai, 0, sbi);
+        acc[1][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bh, acc[1][t], 4, 0, 1, sai, 0, sbi);
+        acc[2][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[2], bh, acc[2][t], 4, 0, 2, sai, 0, sbi);
+        acc[3][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[3], bh, acc[3][t], 4, 0, 3, sai, 0, sbi);
+        if constexpr (kLo) {
+          acc[0][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bl, acc[0][t], 4, 0, 0, sai, 1, sbi);
+          acc[1][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bl, acc[1][t], 4, 0, 1, sai, 1, sbi);
+          acc[2][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[2], bl, acc[2][t], 4, 0, 2, sai, 1, sbi);
+          acc[3][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[3], bl, acc[3][t], 4, 0, 3, sai, 1, sbi);
+        }
+      }
+    }
+  }
+  wait_vm<0>();  // the clamped loads past the last block land before the work-group ends
+  if (!active) return;
+
+  const int bj = n;
+  // Scale codes 0 and 255 (none in a regular checkpoint; the block-scaled
+  // product cannot express the reference's decode of them): redo the wave's
+  // tile block by block with that decode on the bf16 product, tokens read
+  // from the bf16 rows of x.
+  if (__builtin_expect(__ballot(spec) != 0ull, 0)) {
+    const uint16_t* trow[kFrags];
+#pragma unroll
+    for (int t = 0; t < kFrags; ++t) {
+      const int j = min(16 * t + bj, mc - 1);
+      const int prow = a.row_index ? a.row_index[tc.off + tc.m0 + j] : tc.off + tc.m0 + j;
+      trow[t] = a.x + static_cast<size_t>(prow) * g.K + 8 * (lane >> 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int t = 0; t < kFrags; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb = 0; kb < nb; ++kb) {
+      const u32x4_t wv = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff, kb * 1024, 0));
+      const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b32(srs, svoff, kb * 64, 0);
+      bf16x8_t av1[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av1[i] = decode8_bf16_special(wv[i], (sv >> (8 * i)) & 0xffu);
+#pragma unroll
+      for (int t = 0; t < kFrags; ++t)
+        if (kFull || t < nfr) {
+          const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(trow[t] + kb * 32);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av1[i], b1, acc[i][t], 0, 0, 0);
+        }
+    }
+  }
+
+  // Epilogue.  acc[i][t][r] is row 16i + 4(l/16) + r of the tile for token
+  // 16t + l % 16.  gated with outq: the tile's 32 activations of a token are
+  // one block of the down product's input; its four lanes (l / 16 = 0..3)
+  // hold positions 8i + 2(l/16) + {0, 1} and quantise them with a common scale.
+  const int nrow0 = tile * kTileRows + 4 * (lane >> 4);
+  const uint16_t* brow = a.bias ? a.bias + static_cast<size_t>(tc.e) * N : nullptr;
+  float bias[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int nn = nrow0 + 16 * i;
+    bias[i][0] = bias[i][1] = bias[i][2] = bias[i][3] = 0.0f;
+    if (brow) {
+      const uint2 bb = *reinterpret_cast<const uint2*>(brow + nn);
+      bias[i][0] = bf16_to_f32(static_cast<uint16_t>(bb.x));
+      bias[i][1] = bf16_to_f32(static_cast<uint16_t>(bb.x >> 16));
+      bias[i][2] = bf16_to_f32(static_cast<uint16_t>(bb.y));
+      bias[i][3] = bf16_to_f32(static_cast<uint16_t>(bb.y >> 16));
+    }
+  }
+  const int nbo = N / kTileRows;  // blocks of a quantised activation row (gated)
+#pragma unroll
+  for (int t = 0; t < kFrags; ++t) {
+    const int j = 16 * t + bj;
+    const bool live = j < mc;
+    const size_t p = static_cast<size_t>(tc.off + tc.m0 + (live ? j : 0));
+    if constexpr (kGated) {
+      float act[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int nn = nrow0 + 16 * i;
+        uint16_t y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = f32_to_bf16(acc[i][t][r] + bias[i][r]);
+        // rows nn, nn+2 are gate (even), nn+1, nn+3 up (odd)
+        const uint16_t a0 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[0]), bf16_to_f32(y[1]), a.alpha, a.limit));
+        const uint16_t a1 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[2]), bf16_to_f32(y[3]), a.alpha, a.limit));
+        act[i][0] = bf16_to_f32(a0);
+        act[i][1] = bf16_to_f32(a1);
+        if (live) {
+          *reinterpret_cast<uint32_t*>(a.out + p * (N / 2) + nn / 2) = a0 | (static_cast<uint32_t>(a1) << 16);
+          if (a.gate_up)
+            *reinterpret_cast<uint2*>(a.gate_up + p * N + nn) =
+                make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
+        }
+      }
+      if (a.outq != nullptr) {
+        float m = 0.0f;
+        bool fin = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const float v = __builtin_fabsf(act[i][r]);
+            m = __builtin_fmaxf(m, v);
+            fin = fin && (__float_as_uint(v) < 0x7f800000u);
+          }
+        // the token's four lanes: l, l ^ 16, l ^ 32, l ^ 48
+        m = __builtin_fmaxf(m, __shfl_xor(m, 16, kWave));
+        m = __builtin_fmaxf(m, __shfl_xor(m, 32, kWave));
+        int fi = fin ? 1 : 0;
+        fi &= __shfl_xor(fi, 16, kWave);
+        fi &= __shfl_xor(fi, 32, kWave);
+        float inv_s;
+        const uint32_t codes = fp8x2_codes(m, inv_s);
+        uint32_t h01, l01, h23, l23;
+        fp8x2_quant4(act[0][0], act[0][1], act[1][0], act[1][1], inv_s, fi != 0, h01, l01);
+        fp8x2_quant4(act[2][0], act[2][1], act[3][0], act[3][1], inv_s, fi != 0, h23, l23);
+        if (live) {
+          uint8_t* qo = a.outq + (p * nbo + tile) * 64 + 2 * (lane >> 4);
+          *reinterpret_cast<uint16_t*>(qo + 0) = static_cast<uint16_t>(h01);
+          *reinterpret_cast<uint16_t*>(qo + 8) = static_cast<uint16_t>(h01 >> 16);
+          *reinterpret_cast<uint16_t*>(qo + 16) = static_cast<uint16_t>(h23);
+          *reinterpret_cast<uint16_t*>(qo + 24) = static_cast<uint16_t>(h23 >> 16);
+          *reinterpret_cast<uint16_t*>(qo + 32) = static_cast<uint16_t>(l01);
+          *reinterpret_cast<uint16_t*>(qo + 40) = static_cast<uint16_t>(l01 >> 16);
+          *reinterpret_cast<uint16_t*>(qo + 48) = static_cast<uint16_t>(l23);
+          *reinterpret_cast<uint16_t*>(qo + 56) = static_cast<uint16_t>(l23 >> 16);
+          if ((lane >> 4) == 0) a.outqs[p * nbo + tile] = codes;
+        }
+      }
+    } else {
+      if (live) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int nn = nrow0 + 16 * i;
+          uint16_t y[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = f32_to_bf16(acc[i][t][r] + bias[i][r]);
+          *reinterpret_cast<uint2*>(a.out + p * N + nn) =
+              make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
+        }
+      }
+    }
+  }
+}
+
+template <bool kGated, bool kLo>
+__device__ __forceinline__ void run_mx_tile(const GroupedParams& a, const TileCoord& tc, uint8_t* xs, int lane,
+                                            int w) {
+  const int mc = min(kBM, tc.cnt - tc.m0);
+  if (mc == kBM)
+    mx_tile<kGated, true, 8, kLo>(a, tc, xs, lane, w);
+  else if (mc > 64)
+    mx_tile<kGated, false, 8, kLo>(a, tc, xs, lane, w);
+  else if (mc > 32)
+    mx_tile<kGated, false, 4, kLo>(a, tc, xs, lane, w);
+  else
+    mx_tile<kGated, false, 2, kLo>(a, tc, xs, lane, w);
+}
+
+__global__ __launch_bounds__(256) void quant_fp8x2_kernel(const uint16_t* __restrict__ x, int rows, int K,
+                                                         uint8_t* __restrict__ q, uint32_t* __restrict__ qs) {
+  const int nb = K >> 5;
+  const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<long>(rows) * nb) return;
+  const long r = i / nb;
+  const int b = static_cast<int>(i - r * nb);
+  const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(r) * K + 32 * b);
+  float v[32];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint4 u = src[c];
+    const uint32_t d[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[8 * c + 2 * e] = bf16_to_f32(static_cast<uint16_t>(d[e]));
+      v[8 * c + 2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(d[e] >> 16));
+    }
+  }
+  float m = 0.0f;
+  bool fin = true;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const float av = __builtin_fabsf(v[e]);
+    m = __builtin_fmaxf(m, av);
+    fin = fin && (__float_as_uint(av) < 0x7f800000u);
+  }
+  float inv_s;
+  const uint32_t codes = fp8x2_codes(m, inv_s);
+  uint32_t hi[8], lo[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) fp8x2_quant4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3], inv_s, fin, hi[c], lo[c]);
+  uint4* dst = reinterpret_cast<uint4*>(q + static_cast<size_t>(i) * 64);
+  dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  dst[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+  dst[2] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  dst[3] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+  qs[i] = codes;
+}
+
 // Counters of the persistent grid: XCD x's queue at queue[kQueueStride x],
 // the finished work-groups at queue[kQueueStride * 8].  All start at zero;
 // the last work-group to finish zeroes them for the next launch.
@@ -522,7 +907,49 @@ __global__ __launch_bounds__(kGW * kWave, kWGPerCU) void grouped_mfma_kernel(Gro
   }
 }
 
+// The block-scaled grouped product: the persistent loop of
+// grouped_mfma_kernel over the same tile queues, one work-group per CU.
+template <bool kGated, bool kLo>
+__global__ __launch_bounds__(kMxW * kWave, 1) void grouped_mx_kernel(GroupedParams a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[kMxRingBytes + 64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int x0 = static_cast<int>(blockIdx.x) & 7;  // work-group vb runs on XCD vb % 8
+  int* word = reinterpret_cast<int*>(xs + kMxRingBytes);
+  int k = 0;  // queues found empty
+  for (int round = 0;; ++round) {
+    const int x = (x0 + k) & 7;
+    if (threadIdx.x == 0) word[round & 1] = atomicAdd(&a.queue[kQueueStride * x], 1);
+    __syncthreads();
+    const int t = __builtin_amdgcn_readfirstlane(word[round & 1]);
+    const TileList L = make_tile_list(a.offsets, a.E, lane);
+    int lenF;
+    if (t >= queue_len(L, a.nwt, x, lenF)) {
+      if (++k == 8) break;
+      continue;
+    }
+    TileCoord tc;
+    tile_at(L, a.offsets, a.nwt, x, t, lenF, lane, tc);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    run_mx_tile<kGated, kLo>(a, tc, xs, ln, w);
+  }
+  if (threadIdx.x == 0 && atomicAdd(&a.queue[kQueueStride * 8], 1) == static_cast<int>(gridDim.x) - 1) {
+#pragma unroll
+    for (int x = 0; x <= 8; ++x) atomicExch(&a.queue[kQueueStride * x], 0);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_quant_fp8x2(const uint16_t* x, int rows, int K, uint8_t* q, uint32_t* qs, hipStream_t s,
+                              const KernelTimer& t) {
+  if (rows <= 0) return hipSuccess;
+  if (K <= 0 || K % 32 != 0) return hipErrorInvalidValue;
+  const long n = static_cast<long>(rows) * (K / 32);
+  gx_launch(quant_fp8x2_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, t, x, rows, K, q, qs);
+  return hipGetLastError();
+}
 
 bool grouped_supported(int N, int K, int E) {
   return N > 0 && K > 0 && N % kTileRows == 0 && K % 32 == 0 && E > 0 && E <= kMaxExperts;
@@ -546,6 +973,16 @@ hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s) {
   p.limit = a.limit;
   p.nwt = (a.N / kTileRows + kGW - 1) / kGW;
   p.queue = a.queue;
+  p.xq = a.xq;
+  p.xqs = a.xqs;
+  p.outq = a.gated ? a.outq : nullptr;
+  p.outqs = a.gated ? a.outqs : nullptr;
+  const bool mx = a.xq != nullptr;
+  if (mx) {  // the block-scaled kernel: persistent grid, a queue and four-wave tiles
+    if (a.queue == nullptr || a.xqs == nullptr || a.num_cus <= 0 || (a.outq != nullptr) != (a.outqs != nullptr))
+      return hipErrorInvalidValue;
+    p.nwt = (a.N / kTileRows + kMxW - 1) / kMxW;
+  }
   // full m-tiles <= rows / kBM, partial ones <= experts with rows; the
   // kernel counts the real tiles
   const long fb = static_cast<long>(a.rows / kBM) * p.nwt, pb = static_cast<long>(a.E < a.rows ? a.E : a.rows) * p.nwt;
@@ -554,6 +991,21 @@ hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s) {
       p.g.nib_bytes >= (static_cast<size_t>(1) << 31))
     return hipErrorInvalidValue;  // tile counts (16-bit scan fields) and buffer offsets (32-bit)
   int grid = static_cast<int>(8 * per_xcd);
+  if (mx) {
+    const int slots = 8 * ((a.num_cus + 7) / 8);  // one work-group per CU, a multiple of 8
+    grid = grid < slots ? grid : slots;
+    if (a.mx_single) {
+      if (a.gated)
+        gx_launch(grouped_mx_kernel<true, false>, dim3(grid), dim3(kMxW * kWave), 0, s, a.timer, p);
+      else
+        gx_launch(grouped_mx_kernel<false, false>, dim3(grid), dim3(kMxW * kWave), 0, s, a.timer, p);
+    } else if (a.gated) {
+      gx_launch(grouped_mx_kernel<true, true>, dim3(grid), dim3(kMxW * kWave), 0, s, a.timer, p);
+    } else {
+      gx_launch(grouped_mx_kernel<false, true>, dim3(grid), dim3(kMxW * kWave), 0, s, a.timer, p);
+    }
+    return hipGetLastError();
+  }
   if (a.queue) {
     const int slots = 8 * ((kWGPerCU * a.num_cus + 7) / 8);  // every work-group slot, a multiple of 8
     if (a.num_cus <= 0) return hipErrorInvalidValue;

@@ -54,7 +54,8 @@ class ValueErrorG(GptossError, ValueError):
 class MoeConfig(ctypes.Structure):
     _fields_ = [("hidden_size", _I), ("num_experts", _I), ("top_k", _I), ("intermediate_size", _I),
                 ("swiglu_alpha", _F), ("swiglu_limit", _F), ("rms_norm_eps", _F), ("logits_fp32", _I),
-                ("max_tokens", _I), ("prefill_min_tokens", _I), ("decode_exact", _I)]
+                ("max_tokens", _I), ("prefill_min_tokens", _I), ("decode_exact", _I),
+                ("prefill_block_scaled", _I)]
 
 
 class MoeWeights(ctypes.Structure):
@@ -192,13 +193,16 @@ def _stream(stream):
 
 
 def default_config(num_experts: int = 128, max_tokens: int = 64, logits_fp32: bool = False,
-                   prefill_min_tokens: int | None = None, decode_exact: bool = False) -> MoeConfig:
+                   prefill_min_tokens: int | None = None, decode_exact: bool = False,
+                   prefill_block_scaled: int | None = None) -> MoeConfig:
     cfg = MoeConfig()
     check(_lib.gptoss_moe_config_default(ctypes.byref(cfg), num_experts, max_tokens))
     cfg.logits_fp32 = 1 if logits_fp32 else 0
     if prefill_min_tokens is not None:
         cfg.prefill_min_tokens = prefill_min_tokens
     cfg.decode_exact = 1 if decode_exact else 0
+    if prefill_block_scaled is not None:
+        cfg.prefill_block_scaled = int(prefill_block_scaled)
     return cfg
 
 

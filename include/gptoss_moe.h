@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GPTOSS_MOE_ABI_VERSION 5
+#define GPTOSS_MOE_ABI_VERSION 6
 
 enum {
   GPTOSS_OK = 0,
@@ -66,6 +66,18 @@ typedef struct gptoss_moe_config {
    * are bit-identical to the canonical order (one ascending fma chain per
    * K-part, parts added in order), at a lower streaming rate. */
   int decode_exact;
+  /* Prefill expert products (T >= prefill_min_tokens).  0 (default): the
+   * bf16 matrix core with the weights decoded in registers; fp32 accumulation.
+   * 1: the block-scaled matrix core (v_mfma_scale_f32_16x16x128_f8f6f4): the
+   * fp4 weights with their e8m0 scales as stored, times the activations split
+   * into two e4m3 parts per 32-element block (hi + lo/32, exact for every
+   * value above 2^-13 of its block's largest), two products each.  2: the
+   * same with the hi part alone (each activation rounded to four significant
+   * bits).  The block-scaled product sums inside each instruction at less
+   * than fp32 precision, so 1 and 2 fall outside the north-star tolerance at
+   * GPT-OSS-120B's K = 2880, and on gfx950 neither is faster than 0: they
+   * are kept as measured alternatives, not as the default. */
+  int prefill_block_scaled;
 } gptoss_moe_config;
 
 /* Fill `cfg` with the GPT-OSS constants for `num_experts` experts. */

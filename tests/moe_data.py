@@ -100,4 +100,19 @@ def mfma_stats(got, ref) -> dict:
                 over_abs_frac=float((d > 2e-2).mean()) if d.size else 0.0,
                 max_ulps=float((d / ulp_bf16(r[f])).max(initial=0.0)),
                 # largest difference beyond one bf16 step of the reference
-                max_excess=float((d - ulp_bf16(r[f])).max(initial=0.0)))
+                max_excess=float((d - ulp_bf16(r[f])).max(initial=0.0)),
+                # norm-wise relative error ||got - ref|| / ||ref||
+                norm_rel=float(np.sqrt((d * d).sum() / max((r[f] ** 2).sum(), 1e-300))) if d.size else 0.0,
+                # largest difference in bf16 steps at the largest magnitude
+                # of its row (token): a reordered sum moves an output by a
+                # few steps of the values it adds, whatever the output's size
+                row_steps=_row_steps(g, r))
+
+
+def _row_steps(g, r) -> float:
+    if g.ndim != 2 or g.size == 0:
+        return 0.0
+    f = np.isfinite(r) & np.isfinite(g)
+    rowmax = np.where(f, np.abs(r), 0.0).max(axis=1, keepdims=True)
+    d = np.where(f, np.abs(g - r), 0.0)
+    return float((d / ulp_bf16(rowmax)).max(initial=0.0))

@@ -24,7 +24,7 @@ def gptoss():
 
 def test_module_attributes_and_config(gptoss):
     assert gptoss.__version__ == "0.1.0" and gptoss.MODEL_NAME == "gpt-oss-120b"
-    assert gptoss.ABI_VERSION == 5
+    assert gptoss.ABI_VERSION == 6
     assert gptoss.profiler_enabled() is True
     C = gptoss.ModelConfig
     assert (C.num_layers, C.hidden_size, C.num_q_heads, C.num_kv_heads, C.head_dim) == (36, 2880, 64, 8, 64)
