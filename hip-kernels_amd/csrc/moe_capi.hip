@@ -29,10 +29,31 @@ thread_local std::string g_last_error;
 
 namespace gxmoe {
 
+// Messages quote names and paths read from files: keep well-formed UTF-8
+// (the bindings decode it as such) and write every other byte, including
+// a sequence cut by the buffer's end, as '?'.
+static void assign_utf8(std::string& dst, const char* s) {
+  dst.clear();
+  const auto* u = reinterpret_cast<const unsigned char*>(s);
+  size_t left = strlen(s);
+  while (left > 0) {
+    const int n = utf8_seq_len(u, left);
+    if (n == 0) {
+      dst.push_back('?');
+      ++u;
+      --left;
+    } else {
+      dst.append(reinterpret_cast<const char*>(u), static_cast<size_t>(n));
+      u += n;
+      left -= static_cast<size_t>(n);
+    }
+  }
+}
+
 int vset_error(int code, const char* fmt, va_list ap) {
   char buf[512];
   vsnprintf(buf, sizeof(buf), fmt, ap);
-  g_last_error = buf;
+  assign_utf8(g_last_error, buf);
   return code;
 }
 

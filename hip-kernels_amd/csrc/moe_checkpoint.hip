@@ -146,7 +146,15 @@ struct Json {
         return false;
       }
       if (c != '\\') {
-        out += c;
+        // JSON text is UTF-8 (and safetensors requires it): take whole,
+        // well-formed sequences only
+        const int n = utf8_seq_len(reinterpret_cast<const unsigned char*>(p - 1), static_cast<size_t>(end - p + 1));
+        if (n == 0) {
+          err = "string is not UTF-8";
+          return false;
+        }
+        out.append(p - 1, static_cast<size_t>(n));
+        p += n - 1;
         continue;
       }
       if (p >= end) break;
@@ -175,6 +183,12 @@ struct Json {
             } else {
               p = save;
             }
+          }
+          // a surrogate left unpaired has no UTF-8 form; NUL cannot pass
+          // the C ABI's name strings
+          if ((cp >= 0xd800 && cp < 0xe000) || cp == 0) {
+            err = cp == 0 ? "NUL in string" : "unpaired surrogate in \\u escape";
+            return false;
           }
           utf8(out, cp);
           break;

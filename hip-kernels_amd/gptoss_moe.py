@@ -18,7 +18,9 @@ from dataclasses import dataclass
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libgptoss_moe.so")
+# GPTOSS_MOE_LIB: another build of the same library (the sanitizer build of
+# tests/sanitize loads its instrumented copy this way)
+LIB_PATH = os.environ.get("GPTOSS_MOE_LIB") or os.path.join(HERE, "libgptoss_moe.so")
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C hip-kernels_amd)")

@@ -38,7 +38,8 @@ enum {
   GPTOSS_ERR_IO = 7            /* checkpoint file unreadable or not valid safetensors */
 };
 
-/* Message of the last failing call on this thread ("" if none). */
+/* Message of the last failing call on this thread ("" if none); UTF-8, with
+ * any byte of a quoted name or path that is not well-formed UTF-8 as '?'. */
 const char* gptoss_last_error(void);
 int gptoss_abi_version(void);
 

@@ -14,7 +14,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmoe_oracle.so")
+# GPTOSS_ORACLE_LIB: another build of the oracle (tests/sanitize's instrumented copy)
+LIB_PATH = os.environ.get("GPTOSS_ORACLE_LIB") or os.path.join(HERE, "libmoe_oracle.so")
 
 _lib = None
 

@@ -195,11 +195,12 @@ def test_bench_rejects_several_gpus():
     assert r.returncode == 2 and "one GPU only" in r.stderr and r.stdout == ""
 
 
-def test_binding_fails_loudly_without_library(tmp_path):
+def test_binding_fails_loudly_without_library(tmp_path, monkeypatch):
     """The Python binding has no CPU fallback: imported from a directory that
     holds no built libgptoss_moe.so, it raises ImportError naming the library."""
     import importlib.util
     import shutil
+    monkeypatch.delenv("GPTOSS_MOE_LIB", raising=False)
     src = os.path.join(ROOT, "hip-kernels_amd", "gptoss_moe.py")
     shutil.copy(src, tmp_path / "gptoss_moe_nolib.py")
     spec = importlib.util.spec_from_file_location("gptoss_moe_nolib", tmp_path / "gptoss_moe_nolib.py")

@@ -98,7 +98,7 @@ def test_hand_written_headers(g, tmp_path):
 
 
 @pytest.mark.parametrize("case", ["short", "hlen", "json", "trailing", "past_end", "size", "no_offsets",
-                                  "neg_shape", "float_offset"])
+                                  "neg_shape", "float_offset", "bad_utf8", "cut_utf8", "lone_surrogate", "nul"])
 def test_malformed_files_fail_with_io(g, tmp_path, case):
     p = tmp_path / "bad.safetensors"
     ok_entry = {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}
@@ -120,10 +120,60 @@ def test_malformed_files_fail_with_io(g, tmp_path, case):
         _raw_file(p, {"t": {"dtype": "F32", "shape": [-2], "data_offsets": [0, 8]}}, bytes(8))
     elif case == "float_offset":
         _raw_file(p, b'{"t": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8.0]}}', bytes(8))
+    elif case == "bad_utf8":   # a name that is not UTF-8 (JSON text must be)
+        _raw_file(p, b'{"t\xd6x": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}', bytes(8))
+    elif case == "cut_utf8":   # a multi-byte sequence cut by the closing quote
+        _raw_file(p, b'{"t\xe2\x82": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}', bytes(8))
+    elif case == "lone_surrogate":
+        _raw_file(p, b'{"t\\ud83d": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}', bytes(8))
+    elif case == "nul":
+        _raw_file(p, b'{"t\\u0000x": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}', bytes(8))
     with pytest.raises(g.GptossError) as e:
         g.Checkpoint(str(p))
     assert e.value.code == g.GPTOSS_ERR_IO, str(e.value)
     assert "bad.safetensors" in str(e.value)
+
+
+def test_mutated_headers_fail_cleanly(g, tmp_path):
+    """Seeded mutations of a valid header (byte flips, inserted and deleted
+    bytes, truncations, a wrong length prefix): every open either succeeds
+    with tensors whose byte ranges lie inside the file or fails with a status
+    code.  Under tests/sanitize (ASan + UBSan) this is the parser's fuzz pass."""
+    hdr = json.dumps({"__metadata__": {"format": "pt"},
+                      "a.w": {"dtype": "BF16", "shape": [3, 4], "data_offsets": [0, 24]},
+                      "b\u00e9": {"dtype": "U8", "shape": [8], "data_offsets": [24, 32]},
+                      "c": {"dtype": "F32", "shape": [], "data_offsets": [32, 36]}}).encode()
+    data = bytes(range(36))
+    rng = np.random.default_rng(11)
+    p = tmp_path / "m.safetensors"
+    n_ok = 0
+    for it in range(400):
+        h = bytearray(hdr)
+        for _ in range(int(rng.integers(1, 4))):
+            op = int(rng.integers(0, 4))
+            i = int(rng.integers(0, len(h))) if h else 0
+            if op == 0 and h:
+                h[i] = int(rng.integers(0, 256))
+            elif op == 1:
+                h[i:i] = bytes([int(rng.choice(list(b'{}[]",:0-9e.\\u ')))])
+            elif op == 2 and h:
+                del h[i]
+            else:
+                h = h[:i]
+        hlen = len(h) + int(rng.integers(-3, 4)) if it % 7 == 0 else len(h)
+        p.write_bytes(struct.pack("<Q", max(hlen, 0)) + bytes(h) + data)
+        try:
+            ck = g.Checkpoint(str(p))
+        except g.GptossError as e:
+            assert e.code in (g.GPTOSS_ERR_IO, g.GPTOSS_ERR_INVALID), str(e)
+            continue
+        with ck:
+            for n in ck.names():
+                inf = ck.info(n)
+                assert inf["nbytes"] <= len(data)
+                ck.numpy(n)
+            n_ok += 1
+    assert 0 < n_ok < 400
 
 
 def test_missing_paths(g, tmp_path):
