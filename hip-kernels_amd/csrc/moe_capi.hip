@@ -294,7 +294,7 @@ struct gptoss_moe_layer {
   int32_t* special2 = nullptr;
   int special_any1 = 0, special_any2 = 0;
   int num_cus = 0;
-  int mc_shape[3] = {0, 0, 0};  // matrix-core decode launch shape override
+  int mc_shape[6] = {0, 0, 0, 0, 0, 0};  // matrix-core decode launch shape overrides (gate_up, down)
   bool trace_gu = false;
   // per-launch timing (gptoss_moe_layer_set_profiling): 4 events per recorded forward
   std::vector<hipEvent_t> prof_events;
@@ -486,16 +486,20 @@ static int layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int dev
       L->special_any2 |= f2[e] != 0;
     }
   }
-  // Tuning override of the matrix-core decode launch shape: "P,D,NC" (waves
-  // per work-group, ring depth, 16-token chunks); ignored unless compiled
-  // and fitting both expert matrices.
+  // Tuning override of the matrix-core decode launch shapes: "P,D,NC" for
+  // both expert products or "P,D,NC/P,D,NC" for gate_up, then down (waves
+  // per work-group, ring depth, 16-token chunks); a shape that is not
+  // compiled for its matrix is ignored.
   if (const char* ov = getenv("GPTOSS_MOE_DECODE_SHAPE")) {
-    int P = 0, D = 0, NC = 0;
-    if (sscanf(ov, "%d,%d,%d", &P, &D, &NC) == 3 && decode_shape_valid(H / 32, P, D, NC) &&
-        decode_shape_valid(I / 32, P, D, NC)) {
-      L->mc_shape[0] = P;
-      L->mc_shape[1] = D;
-      L->mc_shape[2] = NC;
+    int v[6] = {0, 0, 0, 0, 0, 0};
+    const int n = sscanf(ov, "%d,%d,%d/%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5]);
+    if (n == 3)
+      for (int i = 0; i < 3; ++i) v[3 + i] = v[i];
+    if (n == 3 || n == 6) {
+      if (decode_shape_valid(H / 32, v[0], v[1], v[2]))
+        for (int i = 0; i < 3; ++i) L->mc_shape[i] = v[i];
+      if (decode_shape_valid(I / 32, v[3], v[4], v[5]))
+        for (int i = 3; i < 6; ++i) L->mc_shape[i] = v[i];
     }
   }
   if (err != hipSuccess) {
@@ -614,9 +618,7 @@ static int layer_experts(gptoss_moe_layer* L, const Scratch& S, const uint16_t* 
   ea.special_any1 = L->special_any1;
   ea.special_any2 = L->special_any2;
   ea.num_cus = L->num_cus;
-  ea.mc_shape[0] = L->mc_shape[0];
-  ea.mc_shape[1] = L->mc_shape[1];
-  ea.mc_shape[2] = L->mc_shape[2];
+  for (int i = 0; i < 6; ++i) ea.mc_shape[i] = L->mc_shape[i];
   if (route_in_w1) {  // the gate_up launch selects the experts from the router's logits
     ea.route_logits = S.logits;
     ea.route_fp32 = c.logits_fp32;

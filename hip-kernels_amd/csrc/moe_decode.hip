@@ -109,14 +109,14 @@ template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = 
 __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   constexpr int kFr = 4 * NC;   // accumulator fragments: (sub-tile, chunk)
   constexpr int kTok = 16 * NC; // token columns per step
-  constexpr int kRed = P > 1 ? 2 * P * kFr * kWave : 1;
+  constexpr int kRed = P > 1 ? P * kFr * kWave : 1;
   constexpr int kOwn = (kFr + P - 1) / P;  // fragments this wave finishes
   // the routing prologue's selections and plan scratch (ints), dead before
   // the epilogue's first use of red, live in red
   constexpr int kRouteInts = 2 * kSmallTopkMaxT * kMaxTopK + 3 * kMaxExperts;
   constexpr int kRedAll = kRoute && kRed * 4 < kRouteInts ? (kRouteInts + 3) / 4 : kRed;
   __shared__ int2 hdr[kMaxExperts];
-  __shared__ f32x4 red[kRedAll];  // [2 buffers][P][kFr][64 lanes]
+  __shared__ f32x4 red[kRedAll];  // [P][kFr][64 lanes]
   __shared__ int32_t tok[kGated ? kLdsSlots : 1];  // slot -> token (gate_up, S <= kLdsSlots)
 
   const TiledGeom& g = a.g;
@@ -130,32 +130,45 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   int nact;
   if constexpr (kRoute) {
     static_assert(kGated && !kSpec, "the routing prologue is a gate_up variant for regular scale codes");
-    // Wave w selects tokens w, w + P, ... (topk_token, as the router's own
-    // small top-k launch does); wave 0 then builds the task headers and the
-    // slot -> token map in LDS.  Every work-group computes the same plan.
+    // One token with bf16 logits: wave 0 selects and plans it in one pass
+    // (route_one_token).  Otherwise wave w selects tokens w, w + P, ...
+    // (topk_token, as the router's own small top-k launch does) and wave 0
+    // then builds the plan.  Either way the plan's task headers and slot ->
+    // token map land in LDS; every work-group computes the same plan and
+    // work-group 0 also writes it (and idx, w) for the later launches.
     int32_t* r_idx = reinterpret_cast<int32_t*>(red);
     float* r_w = reinterpret_cast<float*>(r_idx + kSmallTopkMaxT * kMaxTopK);
     int32_t* r_cnt = reinterpret_cast<int32_t*>(r_w + kSmallTopkMaxT * kMaxTopK);
     int32_t* r_off = r_cnt + kMaxExperts;
     int32_t* r_aidx = r_off + kMaxExperts;
     __shared__ int r_nact;
-    for (int t = p; t < a.r_T; t += P) {
-      float lv[kMaxExperts / kWave];
-      if (a.r_fp32) load_token_logits<true, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
-      else load_token_logits<false, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
-      topk_token(lv, a.r_k, a.r_variant, r_idx + t * a.r_k, r_w + t * a.r_k, nullptr, lane);
-    }
-    __syncthreads();
-    if (p == 0) {
-      const int S = a.r_T * a.r_k;
-      const bool w0 = blockIdx.x == 0;
-      if (w0 && lane < S) {
-        a.r_idx[lane] = r_idx[lane];
-        a.r_w[lane] = r_w[lane];
+    const bool w0 = blockIdx.x == 0;
+    if (a.r_T == 1 && !a.r_fp32) {
+      if (p == 0) {
+        float lv[kMaxExperts / kWave];
+        load_token_logits<false, kMaxExperts / kWave>(a.r_logits, 0, a.r_E, lane, lv);
+        const int na = route_one_token_k<kMaxExperts / kWave>(lv, a.r_k, a.r_E, a.r_variant, a.r_plan, vb, G, a.r_idx,
+                                                              a.r_w, lane, hdr, tok);
+        if (lane == 0) r_nact = na;
       }
-      const int na = plan_one_wave<kMaxExperts / kWave>(r_idx, S, a.r_k, a.r_E, w0 ? a.r_plan : PlanBufs{}, lane,
-                                                        r_cnt, r_off, r_aidx, hdr, tok);
-      if (lane == 0) r_nact = na;
+    } else {
+      for (int t = p; t < a.r_T; t += P) {
+        float lv[kMaxExperts / kWave];
+        if (a.r_fp32) load_token_logits<true, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
+        else load_token_logits<false, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
+        topk_token(lv, a.r_k, a.r_variant, r_idx + t * a.r_k, r_w + t * a.r_k, nullptr, lane);
+      }
+      __syncthreads();
+      if (p == 0) {
+        const int S = a.r_T * a.r_k;
+        if (w0 && lane < S) {
+          a.r_idx[lane] = r_idx[lane];
+          a.r_w[lane] = r_w[lane];
+        }
+        const int na = plan_one_wave<kMaxExperts / kWave>(r_idx, S, a.r_k, a.r_E, w0 ? a.r_plan : PlanBufs{}, lane,
+                                                          r_cnt, r_off, r_aidx, hdr, tok);
+        if (lane == 0) r_nact = na;
+      }
     }
     __syncthreads();
     nact = __builtin_amdgcn_readfirstlane(r_nact);
@@ -261,7 +274,6 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   }
 
   f32x4 acc[4][NC];
-  int buf = 0;
   for (;;) {
     const McStep nxt = next_of(cur);
     int nrow[NC];
@@ -375,9 +387,10 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
           for (int i = 0; i < 4; ++i) emit(i, c, braw[4 * c + i], acc[i][c]);
     } else {
       // Partial sums through LDS; fragment f = 4 c + i is finished by wave
-      // f % P, adding the parts in order.  Two buffers: a step's writes never
-      // meet the previous step's reads (a barrier separates them).
-      f32x4* rb0 = red + static_cast<size_t>(buf) * P * kFr * kWave;
+      // f % P, adding the parts in order.  One buffer (half the LDS of two,
+      // so two 6-wave work-groups fit a CU): a second LDS-only barrier keeps
+      // the next step's writes behind this step's reads.
+      f32x4* rb0 = red;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -393,7 +406,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
           emit(f & 3, f >> 2, braw[j], sum);
         }
       }
-      buf ^= 1;
+      if (nxt.valid) lds_barrier();  // work-group uniform
     }
     if (!nxt.valid) break;
     cur = nxt;
@@ -444,10 +457,14 @@ constexpr int kNbGptOss = 90;
   X(6, 15, 1)           \
   X(6, 5, 1)            \
   X(3, 10, 1)           \
+  X(3, 15, 1)           \
   X(3, 5, 1)            \
   X(2, 9, 1)            \
   X(2, 15, 1)           \
   X(1, 9, 1)            \
+  X(5, 9, 1)            \
+  X(5, 18, 1)           \
+  X(9, 10, 1)           \
   X(2, 9, 2)
 #define GX_MC_GENERIC(X) \
   X(1, 4, 1)             \
@@ -485,19 +502,38 @@ hipError_t launch_mc_shape(const McParams& p, int P, int D, int NC, int max_item
   return hipErrorInvalidValue;
 }
 
-// Shapes compiled with the routing prologue: those pick_shape chooses for
-// up to kSmallTopkMaxT tokens.
+// Shapes compiled with the routing prologue (used for one token): pick_shape's
+// choice and the alternatives the tuning override may select.
+#define GX_MC_ROUTE_SHAPES(X) \
+  X(3, 5)                     \
+  X(3, 10)                    \
+  X(3, 15)                    \
+  X(2, 9)                     \
+  X(6, 5)                     \
+  X(6, 15)                    \
+  X(5, 9)                     \
+  X(5, 18)                    \
+  X(9, 10)
+
 bool route_shape(int nb, int P, int D, int NC) {
   if (NC != 1) return false;
-  if (nb == kNbGptOss) return (P == 3 && D == 5) || (P == 2 && D == 9);
+  if (nb == kNbGptOss) {
+#define GX_MC_IS(p_, d_) \
+  if (P == p_ && D == d_) return true;
+    GX_MC_ROUTE_SHAPES(GX_MC_IS)
+#undef GX_MC_IS
+    return false;
+  }
   return P == 1 && D >= 1 && D <= 4 && nb % D == 0;
 }
 
 hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int num_cus, hipStream_t s,
                            const KernelTimer& timer) {
   if (p.g.nb == kNbGptOss) {
-    if (P == 3 && D == 5) return launch_mc_t<true, 3, 5, 1, false, kNbGptOss / 3, true>(p, max_items, num_cus, s, timer);
-    if (P == 2 && D == 9) return launch_mc_t<true, 2, 9, 1, false, kNbGptOss / 2, true>(p, max_items, num_cus, s, timer);
+#define GX_MC_GO(p_, d_) \
+  if (P == p_ && D == d_) return launch_mc_t<true, p_, d_, 1, false, kNbGptOss / p_, true>(p, max_items, num_cus, s, timer);
+    GX_MC_ROUTE_SHAPES(GX_MC_GO)
+#undef GX_MC_GO
   }
   if (P == 1 && D == 4) return launch_mc_t<true, 1, 4, 1, false, 0, true>(p, max_items, num_cus, s, timer);
   if (P == 1 && D == 3) return launch_mc_t<true, 1, 3, 1, false, 0, true>(p, max_items, num_cus, s, timer);
@@ -507,16 +543,18 @@ hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int n
 }
 
 // Default shape for nb blocks and S routed slots, measured on MI355X at the
-// GPT-OSS-120B shape (graph-replayed steps at 1..64 tokens; the shapes differ
-// by a few percent): three K-parts with a short ring up to 2 tokens and at
-// 8, two parts at 4, six parts with each wave's whole part (15 blocks) in
-// flight from 16 tokens.
+// GPT-OSS-120B shape (graph-replayed steps at 1..64 tokens, 12 compiled
+// shapes; most differ by a few percent): three K-parts with a 5-block ring
+// up to 2 tokens and at 8, two parts with a 9-block ring at 4, three parts
+// with a 10-block ring from 16 tokens (1-2 % ahead of six parts with each
+// wave's whole 15-block part in flight, in repeated runs at 16, 32 and 64).
+// The same shape serves both products.
 void pick_shape(int nb, int S, int& P, int& D, int& NC) {
   NC = 1;
   if (nb == kNbGptOss) {
     if (S <= 8 || (S > 16 && S <= 32)) { P = 3; D = 5; }
     else if (S <= 16) { P = 2; D = 9; }
-    else { P = 6; D = 15; }
+    else { P = 3; D = 10; }
     return;
   }
   P = 1;
@@ -551,10 +589,11 @@ hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
   p.x_bytes = static_cast<uint32_t>(x_bytes);
   int P, D, NC;
   pick_shape(g.nb, a.T * a.k, P, D, NC);
-  if (a.mc_shape[0] > 0 && shape_compiled(g.nb, a.mc_shape[0], a.mc_shape[1], a.mc_shape[2])) {
-    P = a.mc_shape[0];
-    D = a.mc_shape[1];
-    NC = a.mc_shape[2];
+  const int* ov = a.mc_shape + (gated ? 0 : 3);
+  if (ov[0] > 0 && shape_compiled(g.nb, ov[0], ov[1], ov[2])) {
+    P = ov[0];
+    D = ov[1];
+    NC = ov[2];
   }
   const int max_items = a.max_active * (g.N / kTileRows);
   if (gated && a.route_logits != nullptr) {  // routing in the prologue (decode_route_in_w1 said yes)

@@ -158,7 +158,7 @@ struct ExpertArgs {
   const int32_t* special2;    // [E] same for W2
   int special_any1, special_any2;  // any flag set (read back at layer init)
   int num_cus;                // compute units of the device (persistent grid size)
-  int mc_shape[3];            // {P, D, NC} launch shape override, {0,0,0} = automatic
+  int mc_shape[6];            // {P, D, NC} launch shape overrides of gate_up, then down; 0 = automatic
   KernelTimer timer;          // of the next launch_w1* / launch_w2* / launch_combine_slots
   // launch_w1_mc with the routing in its prologue (decode_route_in_w1): the
   // router's logits; idx, w and plan are written by the launch.

@@ -136,18 +136,16 @@ __device__ __forceinline__ float slot_sum_k(const float* ex, int k, int variant)
 
 // Softmax over the selected slots and the slot outputs (topk_softmax.cu:
 // 160-215, 339-375): sel_i[0] == -1 means no finite logit at all (experts
-// 0..k-1, weight 1/k); padded slots (index -1) get weight 0.
-__device__ __forceinline__ void write_slots(const float* sel_v, const int* sel_i, int k, int variant, int32_t* out_idx,
-                                            float* out_w, int32_t* tokens_per_expert) {
+// 0..k-1, weight 1/k); padded slots (index -1) get weight 0.  oi / ow are
+// set for slots s < k.
+__device__ __forceinline__ void slot_values(const float* sel_v, const int* sel_i, int k, int variant, int* oi,
+                                            float* ow) {
   if (sel_i[0] == -1) {
 #pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) {
-        out_idx[s] = s;
-        out_w[s] = 1.0f / static_cast<float>(k);
-      }
-    if (tokens_per_expert)
-      for (int s = 0; s < k; ++s) atomicAdd(&tokens_per_expert[s], 1);
+    for (int s = 0; s < kMaxTopK; ++s) {
+      oi[s] = s;
+      ow[s] = 1.0f / static_cast<float>(k);
+    }
     return;
   }
   float mx = -FLT_MAX;
@@ -160,10 +158,22 @@ __device__ __forceinline__ void write_slots(const float* sel_v, const int* sel_i
   const float inv = 1.0f / slot_sum_k(ex, k, variant);
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s) {
+    oi[s] = sel_i[s];
+    ow[s] = (sel_i[s] < 0) ? 0.0f : ex[s] * inv;
+  }
+}
+
+__device__ __forceinline__ void write_slots(const float* sel_v, const int* sel_i, int k, int variant, int32_t* out_idx,
+                                            float* out_w, int32_t* tokens_per_expert) {
+  int oi[kMaxTopK];
+  float ow[kMaxTopK];
+  slot_values(sel_v, sel_i, k, variant, oi, ow);
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
     if (s < k) {
-      out_idx[s] = sel_i[s];
-      out_w[s] = (sel_i[s] < 0) ? 0.0f : ex[s] * inv;
-      if (tokens_per_expert && sel_i[s] >= 0) atomicAdd(&tokens_per_expert[sel_i[s]], 1);
+      out_idx[s] = oi[s];
+      out_w[s] = ow[s];
+      if (tokens_per_expert && oi[s] >= 0) atomicAdd(&tokens_per_expert[oi[s]], 1);
     }
   }
 }
@@ -316,6 +326,145 @@ __device__ __forceinline__ int plan_one_wave(const int32_t* s_idx, int S, int k,
     p.gather_map[lane] = -1;
   }
   return nact;
+}
+
+// One token with bf16 logits, routed and planned by one wave: the outputs of
+// topk_token followed by plan_one_wave (S = K slots), for the decode gate_up
+// prologue at T = 1, where every work-group of the launch computes the plan.
+// A bf16 logit's selection key fits 16 bits, so key and expert index share
+// one 32-bit word (larger key, then smaller index, wins) and each selected
+// slot takes one wave reduction.  The K selected experts are distinct (or -1
+// padding), so every active expert holds one slot, and an expert's offset,
+// its slot's permuted position and its active index are all the number of
+// selected experts below it.  Every work-group writes the LDS task headers
+// and slot -> token map; the plan buffers p are written once over the grid:
+// work-group wg of G writes the entries of experts and task records wg,
+// wg + G, ... (and offsets[E]), work-group 0 the per-slot arrays.  v: the
+// lanes' logits as load_token_logits<false> gives them.  Returns the number
+// of active experts.
+template <int NV, int K>
+__device__ __forceinline__ int route_one_token(const float (&v_in)[NV], int E, int variant, PlanBufs p, int wg, int G,
+                                               int32_t* g_idx, float* g_w, int lane, int2* l_hdr, int32_t* l_tok) {
+  float v[NV];
+  uint32_t key[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    v[j] = sanitize_logit(v_in[j]);
+    const uint32_t k32 = select_key(v[j]);  // low 16 bits all equal for a bf16 value
+    key[j] = k32 == 0u ? 0u : (k32 & 0xffff0000u) | static_cast<uint32_t>(0xffff - (lane + kWave * j));
+  }
+  float sel_v[kMaxTopK];
+  int sel_i[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    sel_v[s] = -FLT_MAX;
+    sel_i[s] = -1;
+    if (s < K) {
+      uint32_t best = key[0];
+#pragma unroll
+      for (int j = 1; j < NV; ++j) best = max(best, key[j]);
+      const uint32_t W = wave_max_u32(best);
+      if (W != 0u) {
+        const int I = 0xffff - static_cast<int>(W & 0xffffu);
+        const int jj = I >> 6, ll = I & 63;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          if (j == jj) {
+            sel_v[s] = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v[j])), ll)));
+            if (lane == ll) key[j] = 0u;
+          }
+        }
+        sel_i[s] = I;
+      }
+    }
+  }
+  int oi[kMaxTopK];
+  float ow[kMaxTopK];
+  slot_values(sel_v, sel_i, K, variant, oi, ow);
+  // wave-uniform: validity, permuted positions, active count
+  bool ok[K];
+  int pos[K];
+  int nact = 0;
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    ok[s] = oi[s] >= 0 && oi[s] < E;
+    nact += ok[s] ? 1 : 0;
+  }
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    int q = 0;
+#pragma unroll
+    for (int t = 0; t < K; ++t) q += (ok[t] && oi[t] < oi[s]) ? 1 : 0;
+    pos[s] = q;
+  }
+  if (lane < K) {
+    int e = -1, q = 0;
+    bool o = false;
+    float w = 0.0f;
+#pragma unroll
+    for (int s = 0; s < K; ++s)
+      if (s == lane) {
+        e = oi[s];
+        w = ow[s];
+        o = ok[s];
+        q = pos[s];
+      }
+    if (o) {
+      if (l_hdr) l_hdr[q] = make_int2(e | (1 << 9), q);
+      if (l_tok) l_tok[q] = 0;
+    }
+    if (p.counts != nullptr && wg == 0) {
+      g_idx[lane] = e;
+      g_w[lane] = w;
+      p.gather_map[lane] = o ? q : -1;
+      if (o) p.perm_token[q] = 0;
+    }
+  }
+  if (p.counts != nullptr) {
+    if (wg == 0 && lane == 0) *p.n_active = nact;
+    // expert (and task record) r = wg + G lane' for lanes with r <= E
+    for (int r = wg + G * lane; r <= E; r += G * kWave) {
+      int c = 0, off = 0, er = -1;
+#pragma unroll
+      for (int s = 0; s < K; ++s) {
+        c += (ok[s] && oi[s] == r) ? 1 : 0;
+        off += (ok[s] && oi[s] < r) ? 1 : 0;
+        if (ok[s] && pos[s] == r) er = oi[s];
+      }
+      if (r == E) {
+        p.offsets[E] = nact;
+        continue;
+      }
+      p.counts[r] = c;
+      p.offsets[r] = off;
+      if (r < nact) {  // the r-th active expert
+        p.active[r] = er;
+        if (p.tasks) {
+          int32_t* t = p.tasks + static_cast<size_t>(r) * kTaskInts;
+          t[0] = er;
+          t[1] = r;
+          t[2] = 1;
+          t[3] = 0;
+          t[4] = 0;  // the slot's token
+        }
+      } else if (p.tasks) {
+        p.tasks[static_cast<size_t>(r) * kTaskInts] = -1;
+      }
+    }
+  }
+  return nact;
+}
+
+template <int NV>
+__device__ __forceinline__ int route_one_token_k(const float (&v)[NV], int k, int E, int variant, PlanBufs p, int wg,
+                                                 int G, int32_t* g_idx, float* g_w, int lane, int2* l_hdr,
+                                                 int32_t* l_tok) {
+  switch (k) {
+    case 1: return route_one_token<NV, 1>(v, E, variant, p, wg, G, g_idx, g_w, lane, l_hdr, l_tok);
+    case 2: return route_one_token<NV, 2>(v, E, variant, p, wg, G, g_idx, g_w, lane, l_hdr, l_tok);
+    case 4: return route_one_token<NV, 4>(v, E, variant, p, wg, G, g_idx, g_w, lane, l_hdr, l_tok);
+    default: return route_one_token<NV, 8>(v, E, variant, p, wg, G, g_idx, g_w, lane, l_hdr, l_tok);
+  }
 }
 
 }  // namespace

@@ -167,19 +167,22 @@ def test_mc_many_tokens_per_expert(gpu, orc, torch_mod, pair120):
 
 # every compiled launch shape for the GPT-OSS K (90 blocks per row): waves
 # per work-group P, ring depth D, 16-token chunks NC
-MC_SHAPES = ["6,15,1", "6,5,1", "3,10,1", "3,5,1", "2,9,1", "2,15,1", "1,9,1", "2,9,2"]
+MC_SHAPES = ["6,15,1", "6,5,1", "3,10,1", "3,15,1", "3,5,1", "2,9,1", "2,15,1", "1,9,1", "5,9,1", "5,18,1",
+             "9,10,1", "2,9,2", "3,15,1/6,5,1"]
 
 
 @pytest.mark.parametrize("shape", MC_SHAPES)
 def test_mc_launch_shapes(gpu, orc, torch_mod, pair120, shape, monkeypatch):
     """Each compiled launch shape (selected by GPTOSS_MOE_DECODE_SHAPE at
-    layer init) at T = 64 and T = 3, against the exact path."""
+    layer init) at T = 64, 3 and 1 (one token: the gate_up launch with the
+    routing in its prologue, for the shapes compiled with it), against the
+    exact path."""
     torch = torch_mod
     w, ex, _ = pair120
     monkeypatch.setenv("GPTOSS_MOE_DECODE_SHAPE", shape)
     mc = DeviceLayer(gpu, torch, w, E120, K120, H120, I120, max_tokens=64, exact=False, tiled=ex.tiled, t=ex.t)
     try:
-        for T in (64, 3):
+        for T in (64, 3, 1):
             x, res = moe_data.make_tokens(900 + T, T, H120)
             say("mc shape", shape, "T", T)
             _stagewise_vs_exact(gpu, orc, torch, ex, mc, x, res, T, f"mc shape {shape} T={T}")
@@ -319,6 +322,78 @@ def test_mc_one_token_dropped_slots(gpu, orc, torch_mod):
                 assert np.array_equal(out, r if r is not None else np.zeros_like(out)), case
             else:
                 check_layer_out(out, ref, f"one token {case} residual={r is not None}")
+
+
+def _one_token_router(case, E, H, seed):
+    """Router weights and bias (bf16) whose logits on an all-ones token hit
+    the top-k's edge cases: exact ties, NaN / +inf / -inf logits, fewer
+    visible experts than k, all NaN (degenerate: experts 0..k-1, weight
+    1/k), all zero (+-0 ties)."""
+    rng = np.random.default_rng(seed)
+    W = rng.normal(0.0, 0.02, (E, H)).astype(np.float32)
+    b = rng.normal(0.0, 0.02, E).astype(np.float32)
+    if case == "ties":
+        for e in range(0, E, 3):
+            W[e + 1:e + 3] = W[e]
+            b[e + 1:e + 3] = b[e]
+    elif case == "nonfinite":
+        W[5::7, 3] = np.nan
+        W[2::9, 4] = np.inf
+        W[1::11, 5] = -np.inf
+    elif case == "three_visible":
+        W[:, 7] = -np.inf
+        W[[4, 40, 90], 7] = 0.0
+    elif case == "all_nan":
+        W[:, 0] = np.nan
+    elif case == "zero":
+        W[:] = 0.0
+        b[:] = 0.0
+        b[1::2] = -0.0
+    return moe_data.bf16(W), moe_data.bf16(b)
+
+
+@pytest.mark.parametrize("k", [1, 4, 8])
+@pytest.mark.parametrize("case", ["ties", "nonfinite", "three_visible", "all_nan", "zero"])
+def test_mc_one_token_routing_prologue(gpu, orc, torch_mod, case, k):
+    """One token on the matrix-core path routes inside the gate_up launch
+    (one wave selects the top-k with packed key/index words and builds the
+    plan of the k distinct experts): indices, weights, gather map and expert
+    offsets bit-identical to the exact path's router launch and to the
+    oracle, on logits with ties, non-finite values, fewer visible experts
+    than k, none visible and all zero; the output within the matrix-core
+    tolerance of the exact path."""
+    torch = torch_mod
+    E, H, I = 128, 128, 128
+    w = moe_data.make_layer(70 + k, E, H, I, bias="random")
+    w["router_w"], w["router_b"] = _one_token_router(case, E, H, 80 + k)
+    x = moe_data.bf16(np.ones((1, H), np.float32))
+    _, res = moe_data.make_tokens(71, 1, H)
+    ex = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=1, via_tables=False, exact=True)
+    mc = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=1, exact=False, tiled=ex.tiled, t=ex.t)
+    dx, dr = dev(x, torch), dev(res, torch)
+    out_mc = host(mc.layer.forward_prenormed(dx, dr))
+    tr_mc = _trace_arrays(gpu, mc.layer, 1, k, E, H, I, torch, False)
+    out_ex = host(ex.layer.forward_prenormed(dx, dr))
+    tr_ex = _trace_arrays(gpu, ex.layer, 1, k, E, H, I, torch, False)
+    torch.cuda.synchronize()
+    ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    for name in ("idx", "gather_map"):
+        assert np.array_equal(tr_mc[name], tr_ex[name]), (case, k, name, tr_mc[name], tr_ex[name])
+        assert np.array_equal(tr_mc[name], tr[name]), (case, k, name)
+    assert np.array_equal(tr_mc["w"].view(np.uint32), tr_ex["w"].view(np.uint32)), (case, k)
+    assert np.array_equal(tr_mc["w"].view(np.uint32), tr["w"].view(np.uint32)), (case, k)
+    rd = lambda p, n: gpu.copy_device_to_tensor(p, n * 4).cpu().numpy().view(np.int32)  # noqa
+    tm, te = mc.layer.trace(), ex.layer.trace()
+    assert np.array_equal(rd(tm.expert_offsets, E + 1), rd(te.expert_offsets, E + 1))
+    assert np.array_equal(rd(tm.expert_counts, E), rd(te.expert_counts, E))
+    na = int(rd(tm.n_active, 1)[0])
+    assert na == int(rd(te.n_active, 1)[0]) == len(set(tr["idx"][0][tr["idx"][0] >= 0].tolist()))
+    assert np.array_equal(rd(tm.active_experts, E)[:na], rd(te.active_experts, E)[:na])
+    assert np.array_equal(rd(tm.perm_token, na), rd(te.perm_token, na))
+    assert np.array_equal(out_ex, ref)
+    check_layer_out(out_mc, out_ex, f"one-token prologue {case} k={k}")
+    mc.layer.destroy()
+    ex.layer.destroy()
 
 
 @pytest.mark.parametrize("T", [127, 128])
