@@ -230,6 +230,88 @@ __device__ __forceinline__ void wait_blocks(int per) {
   else wait_vm<NB * 2>();
 }
 
+// Scale codes 0 and 255 (none in a regular checkpoint): the wave's tile
+// recomputed block by block with the reference's decode of those codes,
+// tokens read from global memory (no LDS, no barriers: the other waves are
+// not involved).
+template <bool kFull, int kFrags>
+__device__ __forceinline__ void tile_special_pass(const GroupedParams& a, const TileCoord& tc,
+                                                  __amdgpu_buffer_rsrc_t wrs, __amdgpu_buffer_rsrc_t srs, int wvoff,
+                                                  int svoff, int nfr, int mc, int lane, f32x4_t (&acc)[4][kFrags]) {
+  const int K = a.g.K, nb = a.g.nb;
+  const int bj = lane & 15;
+  const uint16_t* trow[kFrags];
+#pragma unroll
+  for (int t = 0; t < kFrags; ++t) {
+    const int j = min(16 * t + bj, mc - 1);
+    const int prow = a.row_index ? a.row_index[tc.off + tc.m0 + j] : tc.off + tc.m0 + j;
+    trow[t] = a.x + static_cast<size_t>(prow) * K + 8 * (lane >> 4);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < kFrags; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kb = 0; kb < nb; ++kb) {
+    const u32x4_t wv = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff, kb * 1024, 0));
+    const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b32(srs, svoff, kb * 64, 0);
+    bf16x8_t av1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) av1[i] = decode8_bf16_special(wv[i], (sv >> (8 * i)) & 0xffu);
+#pragma unroll
+    for (int t = 0; t < kFrags; ++t)
+      if (kFull || t < nfr) {
+        const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(trow[t] + kb * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av1[i], b1, acc[i][t], 0, 0, 0);
+      }
+  }
+}
+
+// Epilogue of a wave's 64-row tile.  acc[i][t][r] is row 16i + 4(l/16) + r of
+// the tile for token 16t + l % 16.
+template <bool kGated, int kFrags>
+__device__ __forceinline__ void tile_epilogue(const GroupedParams& a, const TileCoord& tc, int tile, int mc, int lane,
+                                              const f32x4_t (&acc)[4][kFrags]) {
+  const int N = a.g.N;
+  const int bj = lane & 15;
+  const int nrow0 = tile * kTileRows + 4 * (lane >> 4);
+  const uint16_t* brow = a.bias ? a.bias + static_cast<size_t>(tc.e) * N : nullptr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = nrow0 + 16 * i;  // four consecutive rows n..n+3
+    float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (brow) {
+      const uint2 bb = *reinterpret_cast<const uint2*>(brow + n);
+      bias[0] = bf16_to_f32(static_cast<uint16_t>(bb.x));
+      bias[1] = bf16_to_f32(static_cast<uint16_t>(bb.x >> 16));
+      bias[2] = bf16_to_f32(static_cast<uint16_t>(bb.y));
+      bias[3] = bf16_to_f32(static_cast<uint16_t>(bb.y >> 16));
+    }
+#pragma unroll
+    for (int t = 0; t < kFrags; ++t) {
+      const int j = 16 * t + bj;
+      if (j < mc) {
+        const size_t p = static_cast<size_t>(tc.off + tc.m0 + j);
+        uint16_t y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = f32_to_bf16(acc[i][t][r] + bias[r]);
+        if constexpr (kGated) {
+          // rows n, n+2 are gate (even), n+1, n+3 up (odd)
+          const uint16_t a0 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[0]), bf16_to_f32(y[1]), a.alpha, a.limit));
+          const uint16_t a1 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[2]), bf16_to_f32(y[3]), a.alpha, a.limit));
+          *reinterpret_cast<uint32_t*>(a.out + p * (N / 2) + n / 2) = a0 | (static_cast<uint32_t>(a1) << 16);
+          if (a.gate_up)
+            *reinterpret_cast<uint2*>(a.gate_up + p * N + n) =
+                make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
+        } else {
+          *reinterpret_cast<uint2*>(a.out + p * N + n) =
+              make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
+        }
+      }
+    }
+  }
+}
+
 template <bool kGated, bool kFull, int kCls>
 __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileCoord& tc, uint8_t* xs, int lane,
                                              int w) {
@@ -391,76 +473,9 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
   wait_vm<0>();  // the clamped loads past the last block land before the work-group ends
   if (!active) return;
 
-  // Scale codes 0 and 255 (none in a regular checkpoint): redo the wave's
-  // tile block by block with the reference's decode of those codes, tokens
-  // read from global memory (no LDS, no barriers: the other waves are not
-  // involved).
-  if (__builtin_expect(__ballot(spec) != 0ull, 0)) {
-    const uint16_t* trow[kFrags];
-#pragma unroll
-    for (int t = 0; t < kFrags; ++t) {
-      const int j = min(16 * t + bj, mc - 1);
-      const int prow = a.row_index ? a.row_index[tc.off + tc.m0 + j] : tc.off + tc.m0 + j;
-      trow[t] = a.x + static_cast<size_t>(prow) * K + 8 * (lane >> 4);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int t = 0; t < kFrags; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int kb = 0; kb < nb; ++kb) {
-      const u32x4_t wv = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff, kb * 1024, 0));
-      const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b32(srs, svoff, kb * 64, 0);
-      bf16x8_t av1[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av1[i] = decode8_bf16_special(wv[i], (sv >> (8 * i)) & 0xffu);
-#pragma unroll
-      for (int t = 0; t < kFrags; ++t)
-        if (kFull || t < nfr) {
-          const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(trow[t] + kb * 32);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av1[i], b1, acc[i][t], 0, 0, 0);
-        }
-    }
-  }
-
-  // Epilogue.  acc[i][t][r] is row 16i + 4(l/16) + r of the tile for token
-  // 16t + l % 16.
-  const int nrow0 = tile * kTileRows + 4 * (lane >> 4);
-  const uint16_t* brow = a.bias ? a.bias + static_cast<size_t>(tc.e) * N : nullptr;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int n = nrow0 + 16 * i;  // four consecutive rows n..n+3
-    float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (brow) {
-      const uint2 bb = *reinterpret_cast<const uint2*>(brow + n);
-      bias[0] = bf16_to_f32(static_cast<uint16_t>(bb.x));
-      bias[1] = bf16_to_f32(static_cast<uint16_t>(bb.x >> 16));
-      bias[2] = bf16_to_f32(static_cast<uint16_t>(bb.y));
-      bias[3] = bf16_to_f32(static_cast<uint16_t>(bb.y >> 16));
-    }
-#pragma unroll
-    for (int t = 0; t < kFrags; ++t) {
-      const int j = 16 * t + bj;
-      if (j < mc) {
-        const size_t p = static_cast<size_t>(tc.off + tc.m0 + j);
-        uint16_t y[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = f32_to_bf16(acc[i][t][r] + bias[r]);
-        if constexpr (kGated) {
-          // rows n, n+2 are gate (even), n+1, n+3 up (odd)
-          const uint16_t a0 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[0]), bf16_to_f32(y[1]), a.alpha, a.limit));
-          const uint16_t a1 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[2]), bf16_to_f32(y[3]), a.alpha, a.limit));
-          *reinterpret_cast<uint32_t*>(a.out + p * (N / 2) + n / 2) = a0 | (static_cast<uint32_t>(a1) << 16);
-          if (a.gate_up)
-            *reinterpret_cast<uint2*>(a.gate_up + p * N + n) =
-                make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
-        } else {
-          *reinterpret_cast<uint2*>(a.out + p * N + n) =
-              make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
-        }
-      }
-    }
-  }
+  if (__builtin_expect(__ballot(spec) != 0ull, 0))
+    tile_special_pass<kFull, kFrags>(a, tc, wrs, srs, wvoff, svoff, nfr, mc, lane, acc);
+  tile_epilogue<kGated, kFrags>(a, tc, tile, mc, lane, acc);
 }
 
 template <bool kGated>
