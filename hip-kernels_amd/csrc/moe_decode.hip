@@ -154,9 +154,15 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     } else {
       for (int t = p; t < a.r_T; t += P) {
         float lv[kMaxExperts / kWave];
-        if (a.r_fp32) load_token_logits<true, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
-        else load_token_logits<false, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
-        topk_token(lv, a.r_k, a.r_variant, r_idx + t * a.r_k, r_w + t * a.r_k, nullptr, lane);
+        if (a.r_fp32) {
+          load_token_logits<true, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
+          topk_token<kMaxExperts / kWave, false>(lv, a.r_k, a.r_variant, r_idx + t * a.r_k, r_w + t * a.r_k, nullptr,
+                                                 lane);
+        } else {
+          load_token_logits<false, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
+          topk_token<kMaxExperts / kWave, true>(lv, a.r_k, a.r_variant, r_idx + t * a.r_k, r_w + t * a.r_k, nullptr,
+                                                lane);
+        }
       }
       __syncthreads();
       if (p == 0) {

@@ -493,7 +493,7 @@ __global__ __launch_bounds__(kRouteThreads) void topk_kernel(const void* logits,
   if (t >= T) return;
   float v[NV];
   load_token_logits<F32, NV>(logits, t, E, lane, v);
-  topk_token(v, k, variant, idx + static_cast<size_t>(t) * k, w + static_cast<size_t>(t) * k, tpe, lane);
+  topk_token<NV, !F32>(v, k, variant, idx + static_cast<size_t>(t) * k, w + static_cast<size_t>(t) * k, tpe, lane);
 }
 
 // Top-k of all T <= kTopkPlanMaxT tokens (16 waves, tokens w, w + 16, ...),
@@ -518,7 +518,7 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_kernel(const void* log
 #pragma unroll
   for (int i = 0; i < kTPW; ++i) {
     const int t = wv + kWaves * i;
-    if (t < T) topk_token(v[i], k, variant, s_idx + t * k, s_w + t * k, nullptr, lane);
+    if (t < T) topk_token<NV, !F32>(v[i], k, variant, s_idx + t * k, s_w + t * k, nullptr, lane);
   }
   __syncthreads();
   for (int q = threadIdx.x; q < T * k; q += kPlanThreads) {
@@ -644,7 +644,7 @@ __global__ __launch_bounds__(kSmallTopkMaxT * kWave) void topk_plan_small_kernel
   if (wv < T) {
     float v[NV];
     load_token_logits<F32, NV>(logits, wv, E, lane, v);
-    topk_token(v, k, variant, s_idx + wv * k, s_w + wv * k, nullptr, lane);
+    topk_token<NV, !F32>(v, k, variant, s_idx + wv * k, s_w + wv * k, nullptr, lane);
   }
   __syncthreads();
   if (wv != 0) return;

@@ -178,23 +178,23 @@ __device__ __forceinline__ void write_slots(const float* sel_v, const int* sel_i
   }
 }
 
-// Top-k of one token and the softmax over the selected k (topk_softmax.cu:
-// 77-375), from the lanes' logits v.  Round s takes the largest visible key
-// (value desc) and, among equal keys, the smallest expert index; a round with
-// nothing visible yields (-FLT_MAX, -1), the reference's padding.  Lane 0
-// writes the slot outputs (v1 sequential sum for variant 1, v2 butterfly tree
-// otherwise).  Control flow is wave-uniform.
-template <int NV>
-__device__ __forceinline__ void topk_token(float (&v)[NV], int k, int variant, int32_t* out_idx, float* out_w,
-                                           int32_t* tokens_per_expert, int lane) {
+// The k selections of one token from the lanes' sanitized logits v
+// (expert lane + 64 j).  Round s takes the largest visible key (value desc)
+// and, among equal keys, the smallest expert index; a round with nothing
+// visible yields (-FLT_MAX, -1), the reference's padding.  kPacked: the
+// logits are bf16 values, whose selection key fits 16 bits, so key and
+// (0xffff - index) share one 32-bit word and each round is one wave
+// max-reduction instead of a max and an index min.  Wave-uniform results.
+template <int NV, bool kPacked>
+__device__ __forceinline__ void select_topk(const float (&v)[NV], int k, int lane, float (&sel_v)[kMaxTopK],
+                                            int (&sel_i)[kMaxTopK]) {
   uint32_t key[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    v[j] = sanitize_logit(v[j]);
-    key[j] = select_key(v[j]);
+    const uint32_t k32 = select_key(v[j]);  // for a bf16 value the low 16 bits are all equal
+    key[j] = !kPacked || k32 == 0u ? k32
+                                   : (k32 & 0xffff0000u) | static_cast<uint32_t>(0xffff - (lane + kWave * j));
   }
-  float sel_v[kMaxTopK];
-  int sel_i[kMaxTopK];
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s) {
     sel_v[s] = -FLT_MAX;
@@ -203,27 +203,44 @@ __device__ __forceinline__ void topk_token(float (&v)[NV], int k, int variant, i
       uint32_t best = key[0];
 #pragma unroll
       for (int j = 1; j < NV; ++j) best = max(best, key[j]);
-      const uint32_t K = wave_max_u32(best);
-      if (K != 0u) {
-        uint32_t cand = 0xffffffffu;
+      const uint32_t W = wave_max_u32(best);
+      if (W != 0u) {
+        int I;
+        if constexpr (kPacked) {
+          I = 0xffff - static_cast<int>(W & 0xffffu);
+        } else {
+          uint32_t cand = 0xffffffffu;
 #pragma unroll
-        for (int j = NV - 1; j >= 0; --j)
-          if (key[j] == K) cand = static_cast<uint32_t>(lane + kWave * j);
-        const int I = static_cast<int>(wave_min_u32(cand));
+          for (int j = NV - 1; j >= 0; --j)
+            if (key[j] == W) cand = static_cast<uint32_t>(lane + kWave * j);
+          I = static_cast<int>(wave_min_u32(cand));
+        }
         const int jj = I >> 6, ll = I & 63;
-        float val = 0.0f;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
           if (j == jj) {
-            val = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v[j])), ll)));
+            sel_v[s] = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v[j])), ll)));
             if (lane == ll) key[j] = 0u;
           }
         }
-        sel_v[s] = val;
         sel_i[s] = I;
       }
     }
   }
+}
+
+// Top-k of one token and the softmax over the selected k (topk_softmax.cu:
+// 77-375), from the lanes' logits v (select_topk; kPacked for bf16 logits).
+// Lane 0 writes the slot outputs (v1 sequential sum for variant 1, v2
+// butterfly tree otherwise).  Control flow is wave-uniform.
+template <int NV, bool kPacked = false>
+__device__ __forceinline__ void topk_token(float (&v)[NV], int k, int variant, int32_t* out_idx, float* out_w,
+                                           int32_t* tokens_per_expert, int lane) {
+#pragma unroll
+  for (int j = 0; j < NV; ++j) v[j] = sanitize_logit(v[j]);
+  float sel_v[kMaxTopK];
+  int sel_i[kMaxTopK];
+  select_topk<NV, kPacked>(v, k, lane, sel_v, sel_i);
   if (lane != 0) return;
   write_slots(sel_v, sel_i, k, variant, out_idx, out_w, tokens_per_expert);
 }
@@ -231,20 +248,18 @@ __device__ __forceinline__ void topk_token(float (&v)[NV], int k, int variant, i
 // The plan of S <= 64 slots (values from LDS) built by one wave with no
 // barrier: lane s holds slot s; its rank among equal experts comes from
 // ballots over the expert bits; the counts go through LDS to the lanes that
-// own the experts (expert lane + 64 j), which scan them into offsets and the
-// ascending active list.  Same outputs as build_plan, written to p unless
-// p.counts is null.  With l_hdr, also the LDS task headers of a decode
-// kernel: l_hdr[a] = {expert | sp[j] << 8 | count << 9, offset} for active
-// expert a (sp[j]: the lane's flag for expert lane + 64 j, 0 without sp)
-// and l_tok[pos] =
-// token of permuted slot pos.  LDS accesses of one wave execute in order, so
-// values written are read back without a wait.  Returns the number of
-// active experts (every lane).
+// own the experts (lane l: experts NV l .. NV l + NV - 1), which add them up
+// and take one wave scan of the packed (slots, active experts) sums for the
+// offsets and the ascending active list.  Same outputs as build_plan,
+// written to p unless p.counts is null.  With l_hdr, also the LDS task
+// headers of a decode kernel: l_hdr[a] = {expert | count << 9, offset} for
+// active expert a, and l_tok[pos] = token of permuted slot pos.  LDS
+// accesses of one wave execute in order, so values written are read back
+// without a wait.  Returns the number of active experts (every lane).
 template <int NV>
 __device__ __forceinline__ int plan_one_wave(const int32_t* s_idx, int S, int k, int E, PlanBufs p, int lane,
                                              int32_t* s_cnt, int32_t* s_off, int32_t* s_aidx,
-                                             int2* l_hdr = nullptr, int32_t* l_tok = nullptr,
-                                             const int* sp = nullptr) {
+                                             int2* l_hdr = nullptr, int32_t* l_tok = nullptr) {
   const bool gw = p.counts != nullptr;
   const int e = lane < S ? s_idx[lane] : -1;
   const bool valid = e >= 0 && e < E;
@@ -257,52 +272,57 @@ __device__ __forceinline__ int plan_one_wave(const int32_t* s_idx, int S, int k,
   }
   const int rank = __popcll(peers & ((1ull << lane) - 1ull));
 #pragma unroll
-  for (int j = 0; j < NV; ++j) s_cnt[lane + kWave * j] = 0;
+  for (int j = 0; j < NV; ++j) s_cnt[NV * lane + j] = 0;
   __builtin_amdgcn_wave_barrier();
   if (valid && rank == 0) s_cnt[e] = __popcll(peers);
   __builtin_amdgcn_wave_barrier();
-  // experts lane + 64 j: counts, exclusive offsets (scan over j-major order)
-  int base = 0, abase = 0;
+  // experts NV lane + j: counts, and one scan of (slots | active experts << 16)
+  int c[NV];
+  int csum = 0, asum = 0;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int ex = lane + kWave * j;
-    const int c = ex < E ? s_cnt[ex] : 0;
-    int incl = c;
+    const int ex = NV * lane + j;
+    c[j] = ex < E ? s_cnt[ex] : 0;
+    csum += c[j];
+    asum += c[j] > 0 ? 1 : 0;
+  }
+  const int packed = csum | (asum << 16);  // slots <= 64, experts <= 256
+  int incl = packed;
 #pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int o = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += o;
-    }
-    const int excl = base + incl - c;
-    const bool act = c > 0;
-    const unsigned long long am = __ballot(act);
-    const int aidx = abase + __popcll(am & ((1ull << lane) - 1ull));
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+  const int nact = __builtin_amdgcn_readlane(incl, kWave - 1) >> 16;
+  int excl = (incl - packed) & 0xffff, aidx = (incl - packed) >> 16;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int ex = NV * lane + j;
     if (ex < E) {
       s_off[ex] = excl;
       if (gw) {
-        p.counts[ex] = c;
+        p.counts[ex] = c[j];
         p.offsets[ex] = excl;
-        if (ex == E - 1) p.offsets[E] = excl + c;
+        if (ex == E - 1) p.offsets[E] = excl + c[j];
       }
-    }
-    if (act) {
-      s_aidx[ex] = aidx;
-      if (l_hdr) l_hdr[aidx] = make_int2(ex | ((sp ? sp[j] : 0) << 8) | (c << 9), excl);
-      if (gw) {
-        p.active[aidx] = ex;
-        if (p.tasks) {
-          int32_t* t = p.tasks + static_cast<size_t>(aidx) * kTaskInts;
-          t[0] = ex;
-          t[1] = excl;
-          t[2] = c;
-          t[3] = 0;
+      if (c[j] > 0) {
+        s_aidx[ex] = aidx;
+        if (l_hdr) l_hdr[aidx] = make_int2(ex | (c[j] << 9), excl);
+        if (gw) {
+          p.active[aidx] = ex;
+          if (p.tasks) {
+            int32_t* t = p.tasks + static_cast<size_t>(aidx) * kTaskInts;
+            t[0] = ex;
+            t[1] = excl;
+            t[2] = c[j];
+            t[3] = 0;
+          }
         }
+        ++aidx;
       }
     }
-    base += __shfl(incl, kWave - 1, kWave);
-    abase += __popcll(am);
+    excl += c[j];
   }
-  const int nact = abase;
   if (gw) {
     if (lane == 0) *p.n_active = nact;
     if (p.tasks) {
@@ -346,38 +366,11 @@ template <int NV, int K>
 __device__ __forceinline__ int route_one_token(const float (&v_in)[NV], int E, int variant, PlanBufs p, int wg, int G,
                                                int32_t* g_idx, float* g_w, int lane, int2* l_hdr, int32_t* l_tok) {
   float v[NV];
-  uint32_t key[NV];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    v[j] = sanitize_logit(v_in[j]);
-    const uint32_t k32 = select_key(v[j]);  // low 16 bits all equal for a bf16 value
-    key[j] = k32 == 0u ? 0u : (k32 & 0xffff0000u) | static_cast<uint32_t>(0xffff - (lane + kWave * j));
-  }
+  for (int j = 0; j < NV; ++j) v[j] = sanitize_logit(v_in[j]);
   float sel_v[kMaxTopK];
   int sel_i[kMaxTopK];
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) {
-    sel_v[s] = -FLT_MAX;
-    sel_i[s] = -1;
-    if (s < K) {
-      uint32_t best = key[0];
-#pragma unroll
-      for (int j = 1; j < NV; ++j) best = max(best, key[j]);
-      const uint32_t W = wave_max_u32(best);
-      if (W != 0u) {
-        const int I = 0xffff - static_cast<int>(W & 0xffffu);
-        const int jj = I >> 6, ll = I & 63;
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-          if (j == jj) {
-            sel_v[s] = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v[j])), ll)));
-            if (lane == ll) key[j] = 0u;
-          }
-        }
-        sel_i[s] = I;
-      }
-    }
-  }
+  select_topk<NV, true>(v, K, lane, sel_v, sel_i);
   int oi[kMaxTopK];
   float ow[kMaxTopK];
   slot_values(sel_v, sel_i, K, variant, oi, ow);
