@@ -225,15 +225,19 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     if ((s.cg + 1) * kTok < s.M) return step_of(s.q, s.cg + 1);
     return step_of(s.q + G, 0);
   };
-  // Input rows of the B operand for this lane's column of each chunk
-  // (clamped to the expert's last slot): gate_up gathers the slot's token,
-  // down reads the slot's activation row.
+  // Input rows of the B operand for this lane's column of each chunk:
+  // gate_up gathers the slot's token, down reads the slot's activation row.
+  // Columns past the expert's slots get -1: their B loads go past the end
+  // of the buffer (zeros, no memory traffic) and their outputs are not
+  // stored.
   auto rows_of = [&](const McStep& s, int (&row)[NC]) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int slot = s.valid ? s.off + min(s.cg * kTok + 16 * c + lo16, s.M - 1) : 0;
+      const int m = s.cg * kTok + 16 * c + lo16;
+      const int slot = s.valid ? s.off + min(m, s.M - 1) : 0;
       if constexpr (kGated) row[c] = s.valid ? tok[slot] : 0;
       else row[c] = slot;
+      if (s.valid && m >= s.M) row[c] = -1;
     }
   };
   auto src_of = [&](const McStep& s, const int (&row)[NC]) -> McSrc<NC> {
@@ -249,7 +253,9 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     r.bstr = s.valid ? 64u : 0u;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      r.vb[c] = s.valid ? static_cast<uint32_t>(row[c]) * static_cast<uint32_t>(K) * 2u + 16u * g16 : 0u;
+      r.vb[c] = !s.valid     ? 0u
+                : row[c] < 0 ? a.x_bytes
+                             : static_cast<uint32_t>(row[c]) * static_cast<uint32_t>(K) * 2u + 16u * g16;
     return r;
   };
 
