@@ -45,6 +45,10 @@ ROW_STEPS = 4.0         # and by how much: bf16 steps at the token's largest out
 MX_FLIP_FRAC = 5e-2
 MX_OUT_OVER_FRAC = 5e-2
 MX_ROW_STEPS = 16.0
+# Norm-wise relative error bounds of the block-scaled variants (about twice
+# what gfx950 gives at the GPT-OSS-120B shape; the north-star tolerance is
+# not met by either, which is why the default product is bf16).
+MX_NORM_REL = {1: 2e-3, 2: 0.1}  # measured: 8.8e-4 and 4.8e-2 end to end
 
 
 @pytest.fixture(scope="module")
@@ -235,6 +239,40 @@ def test_layer_prefill_path_vs_oracle(gpu, orc, torch_mod, mode):
     check_layer_out(out, ref, f"prefill layer out (mode {mode})", over, steps)
 
 
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_layer_prefill_special_scales(gpu, orc, torch_mod, mode):
+    """e8m0 codes 0 (+0) and 255 (+inf) in some experts' W1 and W2 blocks, on
+    the prefill path of every product variant: the waves holding such a
+    block redo their tile with the reference's decode of those codes (for
+    the block-scaled variants, on the bf16 product, tokens from the bf16
+    rows).  NaN and inf positions of the layer output match the oracle's;
+    the finite outputs agree to the variant's tolerance."""
+    torch = torch_mod
+    E, k, H, I, T = 8, 2, 256, 320, 300
+    w = moe_data.make_layer(52, E, H, I, bias="random")
+    rng = np.random.default_rng(52)
+    for e in (1, 6):
+        for name, n, kk in (("w1_scales", 2 * I, H), ("w2_scales", H, I)):
+            sc = w[name][e]
+            sc[rng.integers(0, n, 3), rng.integers(0, kk // 32, 3)] = 0
+            sc[rng.integers(0, n, 1), rng.integers(0, kk // 32, 1)] = 255
+    x, res = moe_data.make_tokens(52, T, H)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T, via_tables=False)
+    cfg = gpu.default_config(E, T, prefill_block_scaled=mode)
+    cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, k
+    L.layer.destroy()
+    L.layer = gpu.MoELayer().init(cfg, 0, L.t["router_w"], L.t.get("router_b"), L.t.get("w1_bias"),
+                                  L.t.get("w2_bias"), tiled=L.tiled)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    torch.cuda.synchronize()
+    ref = orc.moe_forward(w, x, res, E, k, H, I)
+    c = moe_data.mfma_stats(out, ref)
+    say(f"prefill special scales (mode {mode})", c)
+    assert c["nan_ok"] and c["inf_ok"], c
+    assert c["norm_rel"] <= (1e-3 if mode == 0 else MX_NORM_REL[mode]), c
+    L.layer.destroy()
+
+
 @pytest.fixture(scope="module")
 def zipf120(gpu, torch_mod):
     """GPT-OSS-120B-shaped layer (E=128, H=I=2880) over one tiled weight
@@ -310,12 +348,6 @@ def test_gptoss120b_prefill_zipf_4096(gpu, orc, torch_mod, zipf120):
     assert np.array_equal(out_mc, out_mc2)  # run-to-run deterministic
     layer.set_trace_gate_up(False)
     exact.set_trace_gate_up(False)
-
-
-# Norm-wise relative error bounds of the block-scaled variants at this shape
-# (about twice what gfx950 gives; the north-star tolerance is not met by
-# either, which is why the default product is bf16).
-MX_NORM_REL = {1: 1e-2, 2: 0.15}
 
 
 @pytest.mark.parametrize("mode", [1, 2])
