@@ -636,11 +636,12 @@ hipError_t launch_w2_mc(const ExpertArgs& a, hipStream_t s) { return launch_mc(a
 
 bool decode_shape_valid(int nb, int P, int D, int NC) { return shape_compiled(nb, P, D, NC); }
 
-// Measured on MI355X (GPT-OSS-120B, graph-replayed steps): at one token the
-// prologue's top-k and plan cost less than the launch they replace (28.4 vs
-// 29.5 us per layer); from two tokens the waves' serial selections before
-// the first weight load cost more (B=8: 81.7 vs 77.3 us).
-constexpr int kRouteInW1MaxT = 1;
+// Measured on MI355X (GPT-OSS-120B, graph-replayed steps, packed-key
+// selection): up to two tokens the prologue's top-k and plan cost less than
+// the launch they replace (B=2: 35.1 vs 36.2 us per layer); from four the
+// waves' serial selections before the first weight load cost more (B=4:
+// 57.8-58.5 vs 57.5, B=8: 79.7 vs 76.8 us).
+constexpr int kRouteInW1MaxT = 2;
 
 bool decode_route_in_w1(int T, int k, int E, int H, int I, const int* mc_shape) {
   if (T < 1 || T > kRouteInW1MaxT || T * k > kWave || E > kMaxExperts) return false;
