@@ -18,13 +18,20 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round to nearest even; NaN stays a quiet NaN with its sign.  Both results
-// are computed and one is selected (no divergent branch in epilogues).
+// Round to nearest even; NaN stays a quiet NaN with its sign and leading
+// payload bits (the upper half of the input with the quiet bit set).  This is
+// what gfx950's v_cvt_pk_bf16_f32 computes (checked on the device against
+// the integer form  nan ? (u >> 16) | 0x40 : (u + 0x7fff + ((u >> 16) & 1))
+// >> 16  over 4.2 M inputs: random bit patterns, every exponent with tie and
+// near-tie mantissas, denormals, infinities and NaN payloads), so one
+// instruction rounds two values.
+typedef __bf16 gx_bf16x2_cvt __attribute__((ext_vector_type(2)));
+typedef float gx_f32x2_cvt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(gx_f32x2_cvt{lo, hi}, gx_bf16x2_cvt));
+}
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const bool nan = (u & 0x7fffffffu) > 0x7f800000u;
-  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  return static_cast<uint16_t>(nan ? ((u >> 16) | 0x0040u) : rne);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -50,8 +57,12 @@ __device__ __forceinline__ float gx_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  const float v = __builtin_ldexpf(p, static_cast<int>(n));
-  return x != x ? x : x > 88.72283935546875f ? __builtin_inff() : x < -103.97208404541015625f ? 0.0f : v;
+  float v = __builtin_ldexpf(p, static_cast<int>(n));
+  // three independent selects (a nested conditional expression compiles to
+  // exec-mask branches here)
+  v = x < -103.97208404541015625f ? 0.0f : v;
+  v = x > 88.72283935546875f ? __builtin_inff() : v;
+  return x != x ? x : v;
 }
 
 // GPT-OSS clamped SwiGLU on one (gate, up) pair: gate clamped above at

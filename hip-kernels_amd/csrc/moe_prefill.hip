@@ -268,44 +268,45 @@ __device__ __forceinline__ void tile_special_pass(const GroupedParams& a, const 
 }
 
 // Epilogue of a wave's 64-row tile.  acc[i][t][r] is row 16i + 4(l/16) + r of
-// the tile for token 16t + l % 16.
-template <bool kGated, int kFrags>
+// the tile for token 16t + l % 16.  Token by token: one row check (none in
+// full tiles) and one output address per token, the sub-tiles' stores at
+// fixed offsets from it.
+template <bool kGated, bool kFull, int kFrags>
 __device__ __forceinline__ void tile_epilogue(const GroupedParams& a, const TileCoord& tc, int tile, int mc, int lane,
                                               const f32x4_t (&acc)[4][kFrags]) {
   const int N = a.g.N;
   const int bj = lane & 15;
   const int nrow0 = tile * kTileRows + 4 * (lane >> 4);
-  const uint16_t* brow = a.bias ? a.bias + static_cast<size_t>(tc.e) * N : nullptr;
+  // bias rows nrow0 + 16 i .. + 3, packed bf16 pairs
+  uint2 bb[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int n = nrow0 + 16 * i;  // four consecutive rows n..n+3
-    float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (brow) {
-      const uint2 bb = *reinterpret_cast<const uint2*>(brow + n);
-      bias[0] = bf16_to_f32(static_cast<uint16_t>(bb.x));
-      bias[1] = bf16_to_f32(static_cast<uint16_t>(bb.x >> 16));
-      bias[2] = bf16_to_f32(static_cast<uint16_t>(bb.y));
-      bias[3] = bf16_to_f32(static_cast<uint16_t>(bb.y >> 16));
-    }
+  for (int i = 0; i < 4; ++i) bb[i] = make_uint2(0u, 0u);
+  if (a.bias) {
+    const uint16_t* brow = a.bias + static_cast<size_t>(tc.e) * N + nrow0;
 #pragma unroll
-    for (int t = 0; t < kFrags; ++t) {
-      const int j = 16 * t + bj;
-      if (j < mc) {
-        const size_t p = static_cast<size_t>(tc.off + tc.m0 + j);
-        uint16_t y[4];
+    for (int i = 0; i < 4; ++i) bb[i] = *reinterpret_cast<const uint2*>(brow + 16 * i);
+  }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = f32_to_bf16(acc[i][t][r] + bias[r]);
+  for (int t = 0; t < kFrags; ++t) {
+    const int j = 16 * t + bj;
+    if (kFull || j < mc) {
+      const size_t p = static_cast<size_t>(tc.off + tc.m0 + j);
+      uint16_t* const orow = a.out + p * (kGated ? N / 2 : N) + (kGated ? nrow0 / 2 : nrow0);
+      uint16_t* const grow = kGated && a.gate_up ? a.gate_up + p * N + nrow0 : nullptr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t y01 = pack_bf16x2(acc[i][t][0] + __uint_as_float(bb[i].x << 16),
+                                         acc[i][t][1] + __uint_as_float(bb[i].x & 0xffff0000u));
+        const uint32_t y23 = pack_bf16x2(acc[i][t][2] + __uint_as_float(bb[i].y << 16),
+                                         acc[i][t][3] + __uint_as_float(bb[i].y & 0xffff0000u));
         if constexpr (kGated) {
           // rows n, n+2 are gate (even), n+1, n+3 up (odd)
-          const uint16_t a0 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[0]), bf16_to_f32(y[1]), a.alpha, a.limit));
-          const uint16_t a1 = f32_to_bf16(gx_swiglu(bf16_to_f32(y[2]), bf16_to_f32(y[3]), a.alpha, a.limit));
-          *reinterpret_cast<uint32_t*>(a.out + p * (N / 2) + n / 2) = a0 | (static_cast<uint32_t>(a1) << 16);
-          if (a.gate_up)
-            *reinterpret_cast<uint2*>(a.gate_up + p * N + n) =
-                make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
+          const float a0 = gx_swiglu(__uint_as_float(y01 << 16), __uint_as_float(y01 & 0xffff0000u), a.alpha, a.limit);
+          const float a1 = gx_swiglu(__uint_as_float(y23 << 16), __uint_as_float(y23 & 0xffff0000u), a.alpha, a.limit);
+          *reinterpret_cast<uint32_t*>(orow + 8 * i) = pack_bf16x2(a0, a1);
+          if (grow) *reinterpret_cast<uint2*>(grow + 16 * i) = make_uint2(y01, y23);
         } else {
-          *reinterpret_cast<uint2*>(a.out + p * N + n) =
-              make_uint2(y[0] | (static_cast<uint32_t>(y[1]) << 16), y[2] | (static_cast<uint32_t>(y[3]) << 16));
+          *reinterpret_cast<uint2*>(orow + 16 * i) = make_uint2(y01, y23);
         }
       }
     }
@@ -406,12 +407,16 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
     for (int i = 0; i < 4; ++i) av[i] = decode8_bf16(wv[i], __uint_as_float(((sv >> (8 * i)) & 0xffu) << 23));
   };
   bf16x8_t av[2][4], bv[2][kFrags];
+#ifndef GX_PREFILL_ACTIVE_BRANCH
+#define GX_PREFILL_ACTIVE_BRANCH 1
+#endif
+  const bool prod = GX_PREFILL_ACTIVE_BRANCH ? active : true;
 
   // Block 0: its loads were followed by those of blocks 1 .. kStages - 2.
   const int per = nxw + 2;  // this wave's loads per block
   wait_blocks<kStages - 2, R::kMaxLoads>(per);
   __builtin_amdgcn_s_barrier();
-  if (active) {
+  if (prod) {
     u32x4_t wv;
     uint32_t sv;
     read_stage(0, wv, sv, bv[0]);
@@ -431,7 +436,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
       __builtin_amdgcn_s_barrier();
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (active) {
+    if (prod) {
       // Block kb + 1's reads go out in two halves, each ahead of the
       // products of the half of block kb whose fragments it replaces.
       const uint8_t* sp = xs + st1 * kStageBytes;
@@ -475,7 +480,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
 
   if (__builtin_expect(__ballot(spec) != 0ull, 0))
     tile_special_pass<kFull, kFrags>(a, tc, wrs, srs, wvoff, svoff, nfr, mc, lane, acc);
-  tile_epilogue<kGated, kFrags>(a, tc, tile, mc, lane, acc);
+  tile_epilogue<kGated, kFull, kFrags>(a, tc, tile, mc, lane, acc);
 }
 
 template <bool kGated>
