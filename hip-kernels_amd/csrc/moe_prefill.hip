@@ -14,10 +14,9 @@
 //
 // Work decomposition: a work-group (gate_up: four waves, two work-groups per
 // CU; down: eight waves, one per CU) computes a tile of kBM = 128 permuted
-// rows (one expert's tokens) x 64 rows per wave of the weights; each wave
-// owns one 64-row tile of the tiled MXFP4 layout (the
-// layout the decode kernels stream, so one copy of the weights serves both
-// paths).  The m-tiles are counted expert by expert from the plan's offsets
+// rows (one expert's tokens) x 64 weight rows per wave; each wave owns one
+// 64-row tile of the tiled MXFP4 layout (the layout the decode kernels
+// stream, so one copy of the weights serves both paths).  The m-tiles are counted expert by expert from the plan's offsets
 // on the device (no host synchronisation); the tile sequence runs kGroupM
 // m-tiles x all n-tiles at a time (a weight tile is read by the group's
 // m-tiles close together, from L2) and is cut into eight equal contiguous
