@@ -421,16 +421,12 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
     for (int i = 0; i < 4; ++i) av[i] = decode8_bf16(wv[i], __uint_as_float(((sv >> (8 * i)) & 0xffu) << 23));
   };
   bf16x8_t av[2][4], bv[2][kFrags];
-#ifndef GX_PREFILL_ACTIVE_BRANCH
-#define GX_PREFILL_ACTIVE_BRANCH 1
-#endif
-  const bool prod = GX_PREFILL_ACTIVE_BRANCH ? active : true;
 
   // Block 0: its loads were followed by those of blocks 1 .. kStages - 2.
   const int per = nxw + 2;  // this wave's loads per block
   wait_blocks<kStages - 2, R::kMaxLoads>(per);
   __builtin_amdgcn_s_barrier();
-  if (prod) {
+  if (active) {
     u32x4_t wv;
     uint32_t sv;
     read_stage(0, wv, sv, bv[0]);
@@ -450,7 +446,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedParams& a, const TileC
       __builtin_amdgcn_s_barrier();
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (prod) {
+    if (active) {
       // Block kb + 1's reads go out in two halves, each ahead of the
       // products of the half of block kb whose fragments it replaces.
       const uint8_t* sp = xs + st1 * kStageBytes;
