@@ -560,11 +560,15 @@ hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int n
 // up to 2 tokens and at 8, two parts with a 9-block ring at 4, three parts
 // with a 10-block ring from 16 tokens (1-2 % ahead of six parts with each
 // wave's whole 15-block part in flight, in repeated runs at 16, 32 and 64).
-// The same shape serves both products.
-void pick_shape(int nb, int S, int& P, int& D, int& NC) {
+// The same shape serves both products, except the down product of one token
+// (k x 45 items, one per work-group), which takes the 10-block ring (B=1:
+// 24.0 against 24.5 us per layer in three paired runs; from two tokens the
+// shared shape is ahead).
+void pick_shape(int nb, int S, bool gated, int T, int& P, int& D, int& NC) {
   NC = 1;
   if (nb == kNbGptOss) {
-    if (S <= 8 || (S > 16 && S <= 32)) { P = 3; D = 5; }
+    if (!gated && T == 1) { P = 3; D = 10; }
+    else if (S <= 8 || (S > 16 && S <= 32)) { P = 3; D = 5; }
     else if (S <= 16) { P = 2; D = 9; }
     else { P = 3; D = 10; }
     return;
@@ -600,7 +604,7 @@ hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
   p.ws_bytes = static_cast<uint32_t>(ws_bytes);
   p.x_bytes = static_cast<uint32_t>(x_bytes);
   int P, D, NC;
-  pick_shape(g.nb, a.T * a.k, P, D, NC);
+  pick_shape(g.nb, a.T * a.k, gated, a.T, P, D, NC);
   const int* ov = a.mc_shape + (gated ? 0 : 3);
   if (ov[0] > 0 && shape_compiled(g.nb, ov[0], ov[1], ov[2])) {
     P = ov[0];
@@ -647,7 +651,7 @@ bool decode_route_in_w1(int T, int k, int E, int H, int I, const int* mc_shape) 
   if (T < 1 || T > kRouteInW1MaxT || T * k > kWave || E > kMaxExperts) return false;
   const TiledGeom g = tiled_geom(2 * I, H);
   int P, D, NC;
-  pick_shape(g.nb, T * k, P, D, NC);
+  pick_shape(g.nb, T * k, true, T, P, D, NC);
   if (mc_shape && mc_shape[0] > 0 && shape_compiled(g.nb, mc_shape[0], mc_shape[1], mc_shape[2])) {
     P = mc_shape[0];
     D = mc_shape[1];
