@@ -133,15 +133,23 @@ struct TileCoord {
 // M_e % kBM != 0, one partial m-tile (its last rows); each m-tile pairs with
 // nwt n-tiles.  The full tiles come first, group by group (kGroupM m-tiles
 // x nwt n-tiles, m fastest: a weight tile is read by the group's m-tiles
-// close together, from L2), then the partial tiles (an m-tile's n-tiles in
-// a row: they share its tokens).  Each part is cut into 8 contiguous chunks
-// and XCD x's queue holds full chunk x then partial chunk x, so every XCD
-// gets an even share of long and short tiles, long ones first.
+// close together, from L2), cut into 8 contiguous chunks, chunk x heading
+// XCD x's queue.  The partial m-tiles follow, longest first: ranked by
+// class (more than 64 rows, more than 32, the rest; the loop's cost follows
+// the 16-token fragments it loads), by expert within a class, and dealt
+// round-robin, rank i to XCD i % 8, each with its nwt n-tiles in a row
+// (they share its tokens).  The shortest tiles end every queue, so the last
+// work-groups to finish wait least for each other.
+__device__ __forceinline__ int partial_class(int rem) {  // 0: no partial m-tile, else 1..3
+  return rem == 0 ? 0 : (rem > 64 ? 1 : (rem > 32 ? 2 : 3));
+}
+
 struct TileList {
   int f[kExpertsPerLane];  // full m-tiles of the lane's experts
-  int q[kExpertsPerLane];  // partial m-tiles (0 or 1)
-  int ef, ep;              // lane's exclusive prefix of full / partial m-tiles
-  int F, P;                // totals (every lane)
+  int q[kExpertsPerLane];  // class of their partial m-tile, 0 if none
+  int ef;                  // lane's exclusive prefix of full m-tiles
+  int ep1, ep2, ep3;       // and of partial m-tiles of class 1, 2, 3
+  int F, P1, P2, P3;       // totals (every lane)
 };
 
 __device__ __forceinline__ TileList make_tile_list(const int32_t* __restrict__ offsets, int E, int lane) {
@@ -150,36 +158,48 @@ __device__ __forceinline__ TileList make_tile_list(const int32_t* __restrict__ o
   const int e0 = lane * kExpertsPerLane;
 #pragma unroll
   for (int i = 0; i <= kExpertsPerLane; ++i) o[i] = offsets[min(e0 + i, E)];  // all in flight at once
-  int lf = 0, lp = 0;
+  int lf = 0, l1 = 0, l2 = 0, l3 = 0;
 #pragma unroll
   for (int i = 0; i < kExpertsPerLane; ++i) {
     const int m = e0 + i < E ? o[i + 1] - o[i] : 0;
     L.f[i] = m / kBM;
-    L.q[i] = m % kBM != 0;
+    L.q[i] = partial_class(m % kBM);
     lf += L.f[i];
-    lp += L.q[i];
+    l1 += L.q[i] == 1;
+    l2 += L.q[i] == 2;
+    l3 += L.q[i] == 3;
   }
-  // both prefix sums in one scan: full in the low 16 bits, partial above
-  int incl = lf | (lp << 16);
+  // four prefix sums in two scans of 16-bit fields (full counts < 2^16,
+  // the launcher checks; partial counts <= kMaxExperts)
+  int ia = lf | (l1 << 16), ib = l2 | (l3 << 16);
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
-    const int t = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += t;
+    const int ta = __shfl_up(ia, d, kWave);
+    const int tb = __shfl_up(ib, d, kWave);
+    if (lane >= d) {
+      ia += ta;
+      ib += tb;
+    }
   }
-  const int tot = __builtin_amdgcn_readlane(incl, kWave - 1);
-  L.ef = (incl & 0xffff) - lf;
-  L.ep = (incl >> 16) - lp;
-  L.F = tot & 0xffff;
-  L.P = tot >> 16;
+  const int ta = __builtin_amdgcn_readlane(ia, kWave - 1), tb = __builtin_amdgcn_readlane(ib, kWave - 1);
+  L.ef = (ia & 0xffff) - lf;
+  L.ep1 = (ia >> 16) - l1;
+  L.ep2 = (ib & 0xffff) - l2;
+  L.ep3 = (ib >> 16) - l3;
+  L.F = ta & 0xffff;
+  L.P1 = ta >> 16;
+  L.P2 = tb & 0xffff;
+  L.P3 = tb >> 16;
   return L;
 }
 
 // Tiles in XCD x's queue; `lenF` of them full.
 __device__ __forceinline__ int queue_len(const TileList& L, int nwt, int x, int& lenF) {
-  const int totF = L.F * nwt, totP = L.P * nwt;
-  const int cf = (totF + 7) >> 3, cp = (totP + 7) >> 3;
+  const int totF = L.F * nwt;
+  const int cf = (totF + 7) >> 3;
   lenF = min(max(totF - x * cf, 0), cf);
-  return lenF + min(max(totP - x * cp, 0), cp);
+  const int P = L.P1 + L.P2 + L.P3;
+  return lenF + (P > x ? ((P - x + 7) >> 3) * nwt : 0);  // ranks x, x + 8, ... below P
 }
 
 // Coordinates of entry t < queue_len of XCD x's queue.  Every lane returns
@@ -187,7 +207,8 @@ __device__ __forceinline__ int queue_len(const TileList& L, int nwt, int x, int&
 __device__ __forceinline__ void tile_at(const TileList& L, const int32_t* __restrict__ offsets, int nwt, int x, int t,
                                         int lenF, int lane, TileCoord& tc) {
   const int e0 = lane * kExpertsPerLane;
-  int key, nt;  // m-tile index within its part
+  int key, nt;  // m-tile index within its part (full) or class (partial)
+  int cls = 0;  // 0: full, else the partial class
   const bool full = t < lenF;
   if (full) {
     const int v = x * ((L.F * nwt + 7) >> 3) + t;
@@ -198,15 +219,28 @@ __device__ __forceinline__ void tile_at(const TileList& L, const int32_t* __rest
     key = grp * kGroupM + r % gm;
     nt = r / gm;
   } else {
-    const int v = x * ((L.P * nwt + 7) >> 3) + (t - lenF);
-    key = v / nwt;
-    nt = v - key * nwt;
+    const int v = t - lenF;
+    const int j = v / nwt;
+    nt = v - j * nwt;
+    key = x + 8 * j;  // rank among the partial m-tiles
+    cls = 1;
+    if (key >= L.P1) {
+      key -= L.P1;
+      cls = 2;
+      if (key >= L.P2) {
+        key -= L.P2;
+        cls = 3;
+      }
+    }
   }
+  // the lane's start in its part, as a sum (a select between the fields
+  // becomes a load from a selected address, which puts the list on the stack)
+  const int start = L.ef * (cls == 0) + L.ep1 * (cls == 1) + L.ep2 * (cls == 2) + L.ep3 * (cls == 3);
   // the lane holding m-tile `key` and its expert
-  int ee = -1, base = 0, run = full ? L.ef : L.ep;
+  int ee = -1, base = 0, run = start;
 #pragma unroll
   for (int k = 0; k < kExpertsPerLane; ++k) {
-    const int c = full ? L.f[k] : L.q[k];
+    const int c = full ? L.f[k] : L.q[k] == cls;
     if (ee < 0 && key < run + c) {
       ee = e0 + k;
       base = run;
@@ -214,7 +248,7 @@ __device__ __forceinline__ void tile_at(const TileList& L, const int32_t* __rest
     run += c;
   }
   // ee >= 0: key below the lane's end; key >= the lane's start: the one owner
-  const unsigned long long bal = __ballot(ee >= 0 && key >= (full ? L.ef : L.ep));
+  const unsigned long long bal = __ballot(ee >= 0 && key >= start);
   const int src = __ffsll(static_cast<long long>(bal)) - 1;
   tc.e = __builtin_amdgcn_readfirstlane(__shfl(ee, src, kWave));
   tc.off = __builtin_amdgcn_readfirstlane(offsets[tc.e]);
@@ -1017,8 +1051,8 @@ hipError_t launch_grouped_mxfp4(const GroupedArgs& a, hipStream_t s) {
   }
   // full m-tiles <= rows / kBM, partial ones <= experts with rows; the
   // kernel counts the real tiles
-  const long fb = static_cast<long>(a.rows / kBM) * p.nwt, pb = static_cast<long>(a.E < a.rows ? a.E : a.rows) * p.nwt;
-  const long per_xcd = (fb + 7) / 8 + (pb + 7) / 8;
+  const long fb = static_cast<long>(a.rows / kBM) * p.nwt, pm = a.E < a.rows ? a.E : a.rows;
+  const long per_xcd = (fb + 7) / 8 + (pm + 7) / 8 * p.nwt;
   if (per_xcd > (1L << 27) || fb >= (1L << 16) * p.nwt || static_cast<size_t>(a.N) * (a.K / 32) > (1u << 30) ||
       p.g.nib_bytes >= (static_cast<size_t>(1) << 31))
     return hipErrorInvalidValue;  // tile counts (16-bit scan fields) and buffer offsets (32-bit)
