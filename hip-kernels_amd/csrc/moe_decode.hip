@@ -62,6 +62,7 @@ struct McParams {
   uint16_t* gate_up;          // [S][N] bf16 trace or null (gate_up only)
   uint32_t wn_bytes, ws_bytes, x_bytes;  // buffer extents (each < 2^32 - 2^16)
   int slots;                  // S = T * k (gate_up: slot -> token map length)
+  int max_tasks;              // task records readable at tasks (>= *n_active)
   int bpp;                    // blocks per K-part: nb / P, a multiple of D
   float alpha, limit;
   TiledGeom g;
@@ -128,10 +129,15 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   const int vb = static_cast<int>(blockIdx.x);
   const int v = (vb & 7) * (G >> 3) + (vb >> 3);
   int nact;
+  int4 hpre = make_int4(0, 0, 0, 0);
+  OneTokenRoute r1;          // one-token routing, published once the stream is in flight
+  bool r1_publish = false;   // this wave publishes it (wave 0, one token, bf16 logits)
   if constexpr (kRoute) {
     static_assert(kGated && !kSpec, "the routing prologue is a gate_up variant for regular scale codes");
-    // One token with bf16 logits: wave 0 selects and plans it in one pass
-    // (route_one_token).  Otherwise wave w selects tokens w, w + P, ...
+    // One token with bf16 logits: wave 0 selects it and writes the task
+    // headers (route_one_token_select); the plan for the later launches is
+    // written after the work-group's first weight loads are issued.
+    // Otherwise wave w selects tokens w, w + P, ...
     // (topk_token, as the router's own small top-k launch does) and wave 0
     // then builds the plan.  Either way the plan's task headers and slot ->
     // token map land in LDS; every work-group computes the same plan and
@@ -147,9 +153,9 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
       if (p == 0) {
         float lv[kMaxExperts / kWave];
         load_token_logits<false, kMaxExperts / kWave>(a.r_logits, 0, a.r_E, lane, lv);
-        const int na = route_one_token_k<kMaxExperts / kWave>(lv, a.r_k, a.r_E, a.r_variant, a.r_plan, vb, G, a.r_idx,
-                                                              a.r_w, lane, hdr, tok);
+        const int na = route_one_token_select_k<kMaxExperts / kWave>(lv, a.r_k, a.r_E, lane, hdr, tok, r1);
         if (lane == 0) r_nact = na;
+        r1_publish = true;
       }
     } else {
       for (int t = p; t < a.r_T; t += P) {
@@ -179,16 +185,32 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     __syncthreads();
     nact = __builtin_amdgcn_readfirstlane(r_nact);
   } else {
+    // The first task headers are read together with the active count (one
+    // memory latency instead of two): records below max_tasks are in the
+    // buffer, and those past the count are not used.
+    if (static_cast<int>(threadIdx.x) < a.max_tasks)
+      hpre = reinterpret_cast<const int4*>(a.tasks)[static_cast<size_t>(threadIdx.x) * (kTaskInts / 4)];
     nact = __builtin_amdgcn_readfirstlane(*a.n_active);
   }
+  auto publish = [&]() __attribute__((always_inline)) {
+    if constexpr (kRoute)
+      if (r1_publish)
+        route_one_token_publish_k(r1, a.r_k, a.r_E, a.r_variant, a.r_plan, vb, G, a.r_idx, a.r_w, lane);
+  };
   const int n_items = nact * ntiles;
-  if (v >= n_items) return;  // the whole work-group, before any further barrier
+  if (v >= n_items) {  // the whole work-group, before any further barrier
+    publish();
+    return;
+  }
 
   if constexpr (!kRoute) {
-    // Task headers: {expert | special << 8 | count << 9, offset}.
+    // Task headers: {expert | special << 8 | count << 9, offset}.  The
+    // special flag is read only by the variant that branches on it.
     for (int i = threadIdx.x; i < nact; i += P * kWave) {
-      const int4 h = reinterpret_cast<const int4*>(a.tasks)[static_cast<size_t>(i) * (kTaskInts / 4)];
-      const int sp = a.special ? (a.special[h.x] != 0) : 1;
+      const int4 h = i == static_cast<int>(threadIdx.x)
+                         ? hpre
+                         : reinterpret_cast<const int4*>(a.tasks)[static_cast<size_t>(i) * (kTaskInts / 4)];
+      const int sp = !kSpec ? 0 : a.special ? (a.special[h.x] != 0) : 1;
       hdr[i] = make_int2(h.x | (sp << 8) | (h.z << 9), h.y);
     }
     // The next step's token ids are read while the weight stream is in
@@ -284,6 +306,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     issue(u, cs, u);
     __builtin_amdgcn_sched_barrier(0);
   }
+  publish();
 
   f32x4 acc[4][NC];
   for (;;) {
@@ -594,6 +617,7 @@ hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
   p.alpha = a.alpha;
   p.limit = a.limit;
   p.slots = a.T * a.k;
+  p.max_tasks = a.max_active;
   p.g = g;
   if (p.slots > kLdsSlots) return hipErrorInvalidValue;  // decode_mc_supported() is false
   const size_t wn_bytes = g.nib_bytes * a.E, ws_bytes = g.scale_bytes * a.E;

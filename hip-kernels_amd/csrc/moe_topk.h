@@ -85,18 +85,29 @@ __device__ __forceinline__ uint32_t select_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// The bf16 value whose select_key has high half key >> 16 (+0 for -0):
+// the inverse of select_key on bf16 values, which the key's high half holds
+// exactly.
+__device__ __forceinline__ float bf16_of_key(uint32_t key) {
+  const uint32_t h = key >> 16;
+  return __uint_as_float(((h & 0x8000u) ? (h & 0x7fffu) : (~h & 0xffffu)) << 16);
+}
+
 // Logits of one token as the lanes of a wave hold them: expert lane + 64 j
-// (NV = ceil(E / 64) values per lane).
+// (NV = ceil(E / 64) values per lane).  Every load reads an in-range
+// expert and the ones past E are replaced afterwards, so the loads are all
+// in flight before one wait (a conditional load compiles to a branch with
+// its own wait).
 template <bool F32, int NV>
 __device__ __forceinline__ void load_token_logits(const void* logits, int t, int E, int lane, float (&v)[NV]) {
+  float r[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int e = lane + kWave * j;
-    const size_t o = static_cast<size_t>(t) * E + e;
-    v[j] = e >= E ? -FLT_MAX
-           : F32  ? reinterpret_cast<const float*>(logits)[o]
-                  : bf16_to_f32(reinterpret_cast<const uint16_t*>(logits)[o]);
+    const size_t o = static_cast<size_t>(t) * E + min(lane + kWave * j, E - 1);
+    r[j] = F32 ? reinterpret_cast<const float*>(logits)[o] : bf16_to_f32(reinterpret_cast<const uint16_t*>(logits)[o]);
   }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) v[j] = lane + kWave * j >= E ? -FLT_MAX : r[j];
 }
 
 // Sum of the k selected exponentials in the reference's order: v1
@@ -125,41 +136,42 @@ __device__ __forceinline__ float slot_sum(const float* ex, int variant) {
   return t[0];
 }
 
-__device__ __forceinline__ float slot_sum_k(const float* ex, int k, int variant) {
-  switch (k) {
-    case 1: return slot_sum<1>(ex, variant);
-    case 2: return slot_sum<2>(ex, variant);
-    case 4: return slot_sum<4>(ex, variant);
-    default: return slot_sum<8>(ex, variant);
-  }
-}
-
 // Softmax over the selected slots and the slot outputs (topk_softmax.cu:
 // 160-215, 339-375): sel_i[0] == -1 means no finite logit at all (experts
 // 0..k-1, weight 1/k); padded slots (index -1) get weight 0.  oi / ow are
 // set for slots s < k.
-__device__ __forceinline__ void slot_values(const float* sel_v, const int* sel_i, int k, int variant, int* oi,
-                                            float* ow) {
+// K is the compile-time k: straight-line code for the k slots.
+template <int K>
+__device__ __forceinline__ void slot_values_k(const float* sel_v, const int* sel_i, int variant, int* oi, float* ow) {
   if (sel_i[0] == -1) {
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s) {
       oi[s] = s;
-      ow[s] = 1.0f / static_cast<float>(k);
+      ow[s] = 1.0f / static_cast<float>(K);
     }
     return;
   }
   float mx = -FLT_MAX;
-  float ex[kMaxTopK];
 #pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s)
-    if (s < k && sel_v[s] > mx) mx = sel_v[s];
+  for (int s = 0; s < K; ++s) mx = sel_v[s] > mx ? sel_v[s] : mx;
+  float ex[K];
 #pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) ex[s] = (s < k) ? gx_expf(sel_v[s] - mx) : 0.0f;
-  const float inv = 1.0f / slot_sum_k(ex, k, variant);
+  for (int s = 0; s < K; ++s) ex[s] = gx_expf(sel_v[s] - mx);
+  const float inv = 1.0f / slot_sum<K>(ex, variant);
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s) {
     oi[s] = sel_i[s];
-    ow[s] = (sel_i[s] < 0) ? 0.0f : ex[s] * inv;
+    ow[s] = (s >= K || sel_i[s] < 0) ? 0.0f : ex[s < K ? s : 0] * inv;
+  }
+}
+
+__device__ __forceinline__ void slot_values(const float* sel_v, const int* sel_i, int k, int variant, int* oi,
+                                            float* ow) {
+  switch (k) {
+    case 1: slot_values_k<1>(sel_v, sel_i, variant, oi, ow); return;
+    case 2: slot_values_k<2>(sel_v, sel_i, variant, oi, ow); return;
+    case 4: slot_values_k<4>(sel_v, sel_i, variant, oi, ow); return;
+    default: slot_values_k<8>(sel_v, sel_i, variant, oi, ow); return;
   }
 }
 
@@ -184,7 +196,9 @@ __device__ __forceinline__ void write_slots(const float* sel_v, const int* sel_i
 // visible yields (-FLT_MAX, -1), the reference's padding.  kPacked: the
 // logits are bf16 values, whose selection key fits 16 bits, so key and
 // (0xffff - index) share one 32-bit word and each round is one wave
-// max-reduction instead of a max and an index min.  Wave-uniform results.
+// max-reduction instead of a max and an index min; the winning word also
+// gives back the value (bf16_of_key) and clears itself by equality (words
+// are distinct), so the round has no branch.  Wave-uniform results.
 template <int NV, bool kPacked>
 __device__ __forceinline__ void select_topk(const float (&v)[NV], int k, int lane, float (&sel_v)[kMaxTopK],
                                             int (&sel_i)[kMaxTopK]) {
@@ -194,6 +208,24 @@ __device__ __forceinline__ void select_topk(const float (&v)[NV], int k, int lan
     const uint32_t k32 = select_key(v[j]);  // for a bf16 value the low 16 bits are all equal
     key[j] = !kPacked || k32 == 0u ? k32
                                    : (k32 & 0xffff0000u) | static_cast<uint32_t>(0xffff - (lane + kWave * j));
+  }
+  if constexpr (kPacked) {
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s) {
+      sel_v[s] = -FLT_MAX;
+      sel_i[s] = -1;
+      if (s < k) {
+        uint32_t best = key[0];
+#pragma unroll
+        for (int j = 1; j < NV; ++j) best = max(best, key[j]);
+        const uint32_t W = wave_max_u32(best);
+        sel_v[s] = W != 0u ? bf16_of_key(W) : -FLT_MAX;
+        sel_i[s] = W != 0u ? 0xffff - static_cast<int>(W & 0xffffu) : -1;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) key[j] = key[j] == W ? 0u : key[j];
+      }
+    }
+    return;
   }
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s) {
@@ -205,16 +237,11 @@ __device__ __forceinline__ void select_topk(const float (&v)[NV], int k, int lan
       for (int j = 1; j < NV; ++j) best = max(best, key[j]);
       const uint32_t W = wave_max_u32(best);
       if (W != 0u) {
-        int I;
-        if constexpr (kPacked) {
-          I = 0xffff - static_cast<int>(W & 0xffffu);
-        } else {
-          uint32_t cand = 0xffffffffu;
+        uint32_t cand = 0xffffffffu;
 #pragma unroll
-          for (int j = NV - 1; j >= 0; --j)
-            if (key[j] == W) cand = static_cast<uint32_t>(lane + kWave * j);
-          I = static_cast<int>(wave_min_u32(cand));
-        }
+        for (int j = NV - 1; j >= 0; --j)
+          if (key[j] == W) cand = static_cast<uint32_t>(lane + kWave * j);
+        const int I = static_cast<int>(wave_min_u32(cand));
         const int jj = I >> 6, ll = I & 63;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
@@ -348,38 +375,31 @@ __device__ __forceinline__ int plan_one_wave(const int32_t* s_idx, int S, int k,
   return nact;
 }
 
-// One token with bf16 logits, routed and planned by one wave: the outputs of
-// topk_token followed by plan_one_wave (S = K slots), for the decode gate_up
-// prologue at T = 1, where every work-group of the launch computes the plan.
-// A bf16 logit's selection key fits 16 bits, so key and expert index share
-// one 32-bit word (larger key, then smaller index, wins) and each selected
-// slot takes one wave reduction.  The K selected experts are distinct (or -1
-// padding), so every active expert holds one slot, and an expert's offset,
-// its slot's permuted position and its active index are all the number of
-// selected experts below it.  Every work-group writes the LDS task headers
-// and slot -> token map; the plan buffers p are written once over the grid:
-// work-group wg of G writes the entries of experts and task records wg,
-// wg + G, ... (and offsets[E]), work-group 0 the per-slot arrays.  v: the
-// lanes' logits as load_token_logits<false> gives them.  Returns the number
-// of active experts.
-template <int NV, int K>
-__device__ __forceinline__ int route_one_token(const float (&v_in)[NV], int E, int variant, PlanBufs p, int wg, int G,
-                                               int32_t* g_idx, float* g_w, int lane, int2* l_hdr, int32_t* l_tok) {
-  float v[NV];
-#pragma unroll
-  for (int j = 0; j < NV; ++j) v[j] = sanitize_logit(v_in[j]);
-  float sel_v[kMaxTopK];
-  int sel_i[kMaxTopK];
-  select_topk<NV, true>(v, K, lane, sel_v, sel_i);
-  int oi[kMaxTopK];
-  float ow[kMaxTopK];
-  slot_values(sel_v, sel_i, K, variant, oi, ow);
-  // wave-uniform: validity, permuted positions, active count
-  bool ok[K];
-  int pos[K];
+// One token with bf16 logits, routed and planned by one wave, for the
+// decode gate_up prologue at T = 1, where every work-group of the launch
+// routes the token.  Two parts: route_one_token_select gives the selections
+// and the LDS task headers the work-group's items need;
+// route_one_token_publish, called once the work-group's weight stream is in
+// flight, writes the plan for the later launches.  Together they give the
+// outputs of topk_token followed by plan_one_wave (S = K slots).  Selection
+// as select_topk<NV, true>.  The K selected experts are distinct (or -1
+// padding, which only follows the valid ones), so every active expert
+// holds one slot, and an expert's offset, its slot's permuted position and
+// its active index are all the number of selected experts below it.
+struct OneTokenRoute {
+  float sel_v[kMaxTopK];  // selected logits, in selection order
+  int sel_i[kMaxTopK];    // selected experts, -1: none
+};
+
+// Slot experts (experts 0..K-1 when no logit is finite, topk_softmax.cu:
+// 160-215), their validity, positions and the active count; wave-uniform.
+template <int K>
+__device__ __forceinline__ int one_token_slots(const OneTokenRoute& r, int E, int (&oi)[K], bool (&ok)[K],
+                                               int (&pos)[K]) {
   int nact = 0;
 #pragma unroll
   for (int s = 0; s < K; ++s) {
+    oi[s] = r.sel_i[0] == -1 ? s : r.sel_i[s];
     ok[s] = oi[s] >= 0 && oi[s] < E;
     nact += ok[s] ? 1 : 0;
   }
@@ -390,73 +410,126 @@ __device__ __forceinline__ int route_one_token(const float (&v_in)[NV], int E, i
     for (int t = 0; t < K; ++t) q += (ok[t] && oi[t] < oi[s]) ? 1 : 0;
     pos[s] = q;
   }
+  return nact;
+}
+
+// The selections, and the LDS task headers in selection order: header s
+// holds the s-th selected expert (count 1) and its position.  That is the
+// plan's active order permuted, so a work-group's items cover the same
+// (expert, tile) pairs and every output lands at its permuted slot.
+// l_tok[position] = 0 (the one token).  Returns the number of active experts.
+template <int NV, int K>
+__device__ __forceinline__ int route_one_token_select(const float (&v_in)[NV], int E, int lane, int2* l_hdr,
+                                                      int32_t* l_tok, OneTokenRoute& r) {
+  float v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) v[j] = sanitize_logit(v_in[j]);
+  select_topk<NV, true>(v, K, lane, r.sel_v, r.sel_i);
+  int oi[K], pos[K];
+  bool ok[K];
+  const int nact = one_token_slots<K>(r, E, oi, ok, pos);
   if (lane < K) {
     int e = -1, q = 0;
     bool o = false;
-    float w = 0.0f;
 #pragma unroll
     for (int s = 0; s < K; ++s)
       if (s == lane) {
         e = oi[s];
-        w = ow[s];
         o = ok[s];
         q = pos[s];
       }
     if (o) {
-      if (l_hdr) l_hdr[q] = make_int2(e | (1 << 9), q);
-      if (l_tok) l_tok[q] = 0;
-    }
-    if (p.counts != nullptr && wg == 0) {
-      g_idx[lane] = e;
-      g_w[lane] = w;
-      p.gather_map[lane] = o ? q : -1;
-      if (o) p.perm_token[q] = 0;
-    }
-  }
-  if (p.counts != nullptr) {
-    if (wg == 0 && lane == 0) *p.n_active = nact;
-    // expert (and task record) r = wg + G lane' for lanes with r <= E
-    for (int r = wg + G * lane; r <= E; r += G * kWave) {
-      int c = 0, off = 0, er = -1;
-#pragma unroll
-      for (int s = 0; s < K; ++s) {
-        c += (ok[s] && oi[s] == r) ? 1 : 0;
-        off += (ok[s] && oi[s] < r) ? 1 : 0;
-        if (ok[s] && pos[s] == r) er = oi[s];
-      }
-      if (r == E) {
-        p.offsets[E] = nact;
-        continue;
-      }
-      p.counts[r] = c;
-      p.offsets[r] = off;
-      if (r < nact) {  // the r-th active expert
-        p.active[r] = er;
-        if (p.tasks) {
-          int32_t* t = p.tasks + static_cast<size_t>(r) * kTaskInts;
-          t[0] = er;
-          t[1] = r;
-          t[2] = 1;
-          t[3] = 0;
-          t[4] = 0;  // the slot's token
-        }
-      } else if (p.tasks) {
-        p.tasks[static_cast<size_t>(r) * kTaskInts] = -1;
-      }
+      l_hdr[lane] = make_int2(e | (1 << 9), q);
+      l_tok[q] = 0;
     }
   }
   return nact;
 }
 
 template <int NV>
-__device__ __forceinline__ int route_one_token_k(const float (&v)[NV], int k, int E, int variant, PlanBufs p, int wg,
-                                                 int G, int32_t* g_idx, float* g_w, int lane, int2* l_hdr,
-                                                 int32_t* l_tok) {
+__device__ __forceinline__ int route_one_token_select_k(const float (&v)[NV], int k, int E, int lane, int2* l_hdr,
+                                                        int32_t* l_tok, OneTokenRoute& r) {
   switch (k) {
-    case 1: return route_one_token<NV, 1>(v, E, variant, p, wg, G, g_idx, g_w, lane, l_hdr, l_tok);
-    case 2: return route_one_token<NV, 2>(v, E, variant, p, wg, G, g_idx, g_w, lane, l_hdr, l_tok);
-    case 4: return route_one_token<NV, 4>(v, E, variant, p, wg, G, g_idx, g_w, lane, l_hdr, l_tok);
-    default: return route_one_token<NV, 8>(v, E, variant, p, wg, G, g_idx, g_w, lane, l_hdr, l_tok);
+    case 1: return route_one_token_select<NV, 1>(v, E, lane, l_hdr, l_tok, r);
+    case 2: return route_one_token_select<NV, 2>(v, E, lane, l_hdr, l_tok, r);
+    case 4: return route_one_token_select<NV, 4>(v, E, lane, l_hdr, l_tok, r);
+    default: return route_one_token_select<NV, 8>(v, E, lane, l_hdr, l_tok, r);
+  }
+}
+
+// The plan buffers p, written once over the grid: work-group wg of G writes
+// the entries of experts and task records wg, wg + G, ... (and offsets[E]),
+// work-group 0 the per-slot arrays and the routing weights (softmax over
+// the selected logits, computed there only).
+template <int K>
+__device__ __forceinline__ void route_one_token_publish(const OneTokenRoute& r, int E, int variant, PlanBufs p,
+                                                        int wg, int G, int32_t* g_idx, float* g_w, int lane) {
+  if (p.counts == nullptr) return;
+  int oi[K], pos[K];
+  bool ok[K];
+  const int nact = one_token_slots<K>(r, E, oi, ok, pos);
+  if (wg == 0) {
+    int si[kMaxTopK];
+    float ow[kMaxTopK];
+    slot_values_k<K>(r.sel_v, r.sel_i, variant, si, ow);
+    if (lane < K) {
+      int e = -1, q = 0;
+      bool o = false;
+      float w = 0.0f;
+#pragma unroll
+      for (int s = 0; s < K; ++s)
+        if (s == lane) {
+          e = oi[s];
+          w = ow[s];
+          o = ok[s];
+          q = pos[s];
+        }
+      g_idx[lane] = e;
+      g_w[lane] = w;
+      p.gather_map[lane] = o ? q : -1;
+      if (o) p.perm_token[q] = 0;
+    }
+    if (lane == 0) *p.n_active = nact;
+  }
+  // expert (and task record) e = wg + G lane' for lanes with e <= E
+  for (int e = wg + G * lane; e <= E; e += G * kWave) {
+    int c = 0, off = 0, er = -1;
+#pragma unroll
+    for (int s = 0; s < K; ++s) {
+      c += (ok[s] && oi[s] == e) ? 1 : 0;
+      off += (ok[s] && oi[s] < e) ? 1 : 0;
+      if (ok[s] && pos[s] == e) er = oi[s];
+    }
+    if (e == E) {
+      p.offsets[E] = nact;
+      continue;
+    }
+    p.counts[e] = c;
+    p.offsets[e] = off;
+    if (e < nact) {  // the e-th active expert
+      p.active[e] = er;
+      if (p.tasks) {
+        int32_t* t = p.tasks + static_cast<size_t>(e) * kTaskInts;
+        t[0] = er;
+        t[1] = e;
+        t[2] = 1;
+        t[3] = 0;
+        t[4] = 0;  // the slot's token
+      }
+    } else if (p.tasks) {
+      p.tasks[static_cast<size_t>(e) * kTaskInts] = -1;
+    }
+  }
+}
+
+__device__ __forceinline__ void route_one_token_publish_k(const OneTokenRoute& r, int k, int E, int variant,
+                                                          PlanBufs p, int wg, int G, int32_t* g_idx, float* g_w,
+                                                          int lane) {
+  switch (k) {
+    case 1: route_one_token_publish<1>(r, E, variant, p, wg, G, g_idx, g_w, lane); return;
+    case 2: route_one_token_publish<2>(r, E, variant, p, wg, G, g_idx, g_w, lane); return;
+    case 4: route_one_token_publish<4>(r, E, variant, p, wg, G, g_idx, g_w, lane); return;
+    default: route_one_token_publish<8>(r, E, variant, p, wg, G, g_idx, g_w, lane); return;
   }
 }
 
