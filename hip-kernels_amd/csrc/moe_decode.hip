@@ -130,25 +130,31 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   const int v = (vb & 7) * (G >> 3) + (vb >> 3);
   int nact;
   int4 hpre = make_int4(0, 0, 0, 0);
-  OneTokenRoute r1;          // one-token routing, published once the stream is in flight
-  bool r1_publish = false;   // this wave publishes it (wave 0, one token, bf16 logits)
+  OneTokenRoute r1;          // one-token routing
+  bool r1_publish = false;   // held by wave 0 (one token, bf16 logits)
   if constexpr (kRoute) {
     static_assert(kGated && !kSpec, "the routing prologue is a gate_up variant for regular scale codes");
     // One token with bf16 logits: wave 0 selects it and writes the task
-    // headers (route_one_token_select); the plan for the later launches is
-    // written after the work-group's first weight loads are issued.
+    // headers (route_one_token_select).  The plan for the later launches is
+    // written by the work-groups past the items (the launch adds 8), so no
+    // streaming wave issues a store before its epilogue (stores share the
+    // load counter and would hold up the ring's first waits); without such
+    // work-groups, by all after their items.
     // Otherwise wave w selects tokens w, w + P, ...
     // (topk_token, as the router's own small top-k launch does) and wave 0
     // then builds the plan.  Either way the plan's task headers and slot ->
     // token map land in LDS; every work-group computes the same plan and
-    // work-group 0 also writes it (and idx, w) for the later launches.
+    // the last one, which holds no item, also writes it (and idx, w) for the
+    // later launches; only it computes the routing weights.
     int32_t* r_idx = reinterpret_cast<int32_t*>(red);
     float* r_w = reinterpret_cast<float*>(r_idx + kSmallTopkMaxT * kMaxTopK);
     int32_t* r_cnt = reinterpret_cast<int32_t*>(r_w + kSmallTopkMaxT * kMaxTopK);
     int32_t* r_off = r_cnt + kMaxExperts;
     int32_t* r_aidx = r_off + kMaxExperts;
     __shared__ int r_nact;
-    const bool w0 = blockIdx.x == 0;
+    // the plan writer of the multi-token path: the last work-group, which
+    // holds no item unless the grid is capped at the resident work-groups
+    const bool w0 = blockIdx.x == gridDim.x - 1;
     if (a.r_T == 1 && !a.r_fp32) {
       if (p == 0) {
         float lv[kMaxExperts / kWave];
@@ -162,12 +168,12 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
         float lv[kMaxExperts / kWave];
         if (a.r_fp32) {
           load_token_logits<true, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
-          topk_token<kMaxExperts / kWave, false>(lv, a.r_k, a.r_variant, r_idx + t * a.r_k, r_w + t * a.r_k, nullptr,
-                                                 lane);
+          topk_token<kMaxExperts / kWave, false>(lv, a.r_k, a.r_variant, r_idx + t * a.r_k,
+                                                 w0 ? r_w + t * a.r_k : nullptr, nullptr, lane);
         } else {
           load_token_logits<false, kMaxExperts / kWave>(a.r_logits, t, a.r_E, lane, lv);
-          topk_token<kMaxExperts / kWave, true>(lv, a.r_k, a.r_variant, r_idx + t * a.r_k, r_w + t * a.r_k, nullptr,
-                                                lane);
+          topk_token<kMaxExperts / kWave, true>(lv, a.r_k, a.r_variant, r_idx + t * a.r_k,
+                                                w0 ? r_w + t * a.r_k : nullptr, nullptr, lane);
         }
       }
       __syncthreads();
@@ -192,14 +198,12 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
       hpre = reinterpret_cast<const int4*>(a.tasks)[static_cast<size_t>(threadIdx.x) * (kTaskInts / 4)];
     nact = __builtin_amdgcn_readfirstlane(*a.n_active);
   }
-  auto publish = [&]() __attribute__((always_inline)) {
-    if constexpr (kRoute)
-      if (r1_publish)
-        route_one_token_publish_k(r1, a.r_k, a.r_E, a.r_variant, a.r_plan, vb, G, a.r_idx, a.r_w, lane);
-  };
   const int n_items = nact * ntiles;
   if (v >= n_items) {  // the whole work-group, before any further barrier
-    publish();
+    if constexpr (kRoute)
+      if (r1_publish)
+        route_one_token_publish_k(r1, a.r_k, a.r_E, a.r_variant, a.r_plan, v - n_items, G - n_items, a.r_idx, a.r_w,
+                                  lane);
     return;
   }
 
@@ -306,7 +310,6 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     issue(u, cs, u);
     __builtin_amdgcn_sched_barrier(0);
   }
-  publish();
 
   f32x4 acc[4][NC];
   for (;;) {
@@ -447,6 +450,11 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     cur = nxt;
     cs = ns;
   }
+  // a grid capped at the resident work-groups may leave none idle: then
+  // every work-group writes its share of the one-token plan here
+  if constexpr (kRoute)
+    if (r1_publish && G <= n_items)
+      route_one_token_publish_k(r1, a.r_k, a.r_E, a.r_variant, a.r_plan, v, G, a.r_idx, a.r_w, lane);
 }
 
 // Per-expert flag: does the slot-order scale region hold code 0 or 255?
@@ -476,6 +484,7 @@ hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_
   const long resident = static_cast<long>(per_cu) * (num_cus > 0 ? num_cus : 256);
   long grid = max_items < resident ? max_items : resident;
   grid = (grid + 7) & ~7L;  // a multiple of 8 for the XCD-grouped block order
+  if constexpr (kRoute) grid += 8;  // work-groups past the items: they write the one-token plan
   McParams q = p;
   q.bpp = p.g.nb / P;
   gx_launch(mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute>, dim3(static_cast<unsigned>(grid)),

@@ -175,16 +175,22 @@ __device__ __forceinline__ void slot_values(const float* sel_v, const int* sel_i
   }
 }
 
+// out_w null: the indices only (no softmax).
 __device__ __forceinline__ void write_slots(const float* sel_v, const int* sel_i, int k, int variant, int32_t* out_idx,
                                             float* out_w, int32_t* tokens_per_expert) {
   int oi[kMaxTopK];
   float ow[kMaxTopK];
-  slot_values(sel_v, sel_i, k, variant, oi, ow);
+  if (out_w) {
+    slot_values(sel_v, sel_i, k, variant, oi, ow);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s) oi[s] = sel_i[0] == -1 ? s : sel_i[s];
+  }
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s) {
     if (s < k) {
       out_idx[s] = oi[s];
-      out_w[s] = ow[s];
+      if (out_w) out_w[s] = ow[s];
       if (tokens_per_expert && oi[s] >= 0) atomicAdd(&tokens_per_expert[oi[s]], 1);
     }
   }
@@ -379,8 +385,8 @@ __device__ __forceinline__ int plan_one_wave(const int32_t* s_idx, int S, int k,
 // decode gate_up prologue at T = 1, where every work-group of the launch
 // routes the token.  Two parts: route_one_token_select gives the selections
 // and the LDS task headers the work-group's items need;
-// route_one_token_publish, called once the work-group's weight stream is in
-// flight, writes the plan for the later launches.  Together they give the
+// route_one_token_publish, called by work-groups without items, writes the
+// plan for the later launches.  Together they give the
 // outputs of topk_token followed by plan_one_wave (S = K slots).  Selection
 // as select_topk<NV, true>.  The K selected experts are distinct (or -1
 // padding, which only follows the valid ones), so every active expert
@@ -457,10 +463,10 @@ __device__ __forceinline__ int route_one_token_select_k(const float (&v)[NV], in
   }
 }
 
-// The plan buffers p, written once over the grid: work-group wg of G writes
-// the entries of experts and task records wg, wg + G, ... (and offsets[E]),
-// work-group 0 the per-slot arrays and the routing weights (softmax over
-// the selected logits, computed there only).
+// The plan buffers p, written once by G >= 1 work-groups: work-group wg
+// writes the entries of experts and task records wg, wg + G, ... (and
+// offsets[E]), work-group 0 the per-slot arrays and the routing weights
+// (softmax over the selected logits, computed there only).
 template <int K>
 __device__ __forceinline__ void route_one_token_publish(const OneTokenRoute& r, int E, int variant, PlanBufs p,
                                                         int wg, int G, int32_t* g_idx, float* g_w, int lane) {
