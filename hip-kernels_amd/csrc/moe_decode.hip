@@ -106,7 +106,15 @@ struct McSrc {
 // exactly which ring slot each block needs); 0 = a.bpp, a multiple of D.
 // kRoute (gate_up, T <= kSmallTopkMaxT): the routing plan is made in the
 // prologue (McParams r_*) instead of read from a plan launch.
-template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false>
+// kStage (at most 2 slots per expert, one 16-token chunk): each wave copies
+// its K-part of the step's input rows and of its scales into LDS once and
+// reads the B operand and the scale dword of every block from there.  Per
+// block the global loads are then the 1 KiB of weights alone, where the
+// per-lane B and scale loads would return 1.25 KiB more, nearly all of it
+// repeated (one or two distinct 64-byte rows).  Meant for one item per
+// work-group; a work-group given another item copies that item's rows with
+// a full wait first.
+template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false, bool kStage = false>
 __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   constexpr int kFr = 4 * NC;   // accumulator fragments: (sub-tile, chunk)
   constexpr int kTok = 16 * NC; // token columns per step
@@ -119,6 +127,11 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   __shared__ int2 hdr[kMaxExperts];
   __shared__ f32x4 red[kRedAll];  // [P][kFr][64 lanes]
   __shared__ int32_t tok[kGated ? kLdsSlots : 1];  // slot -> token (gate_up, S <= kLdsSlots)
+  static_assert(!kStage || (BPP > 0 && NC == 1 && !kSpec), "staged operands: straight-line steps, one chunk");
+  // staged operands, per wave: the part's scales, input rows 0 and 1, each
+  // kStgU4 16-byte words (whole 64-lane loads)
+  constexpr int kStgU4 = kStage ? (BPP * 4 + kWave - 1) / kWave * kWave : 1;
+  __shared__ gx_u32x4 stg[kStage ? P * 3 * kStgU4 : 1];
 
   const TiledGeom& g = a.g;
   const int lane = threadIdx.x & 63;
@@ -288,27 +301,84 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   gx_u32x4 ra[D];
   uint32_t rs[D];
   gx_u32x4 rb[D][NC];
-  auto issue = [&](int u, const McSrc<NC>& s, int blk) __attribute__((always_inline)) {
+  // kStage: this wave's staged words and the staged row of this lane's column
+  gx_u32x4* const stg_w = stg + (kStage ? p * 3 * kStgU4 : 0);
+  int bcol = 0;
+  // block blk's scale dword and B operand from the staged words
+  auto issue_lds = [&](int u, int blk) __attribute__((always_inline)) {
+    if constexpr (kStage) {
+      rs[u] = reinterpret_cast<const uint32_t*>(stg_w)[blk * 16 + lo16];
+      rb[u][0] = stg_w[(1 + bcol) * kStgU4 + blk * 4 + g16];
+    }
+  };
+  // lds: kStage, block blk of the staged step (the next step's blocks are
+  // read from LDS once it is staged)
+  auto issue = [&](int u, const McSrc<NC>& s, int blk, bool lds) __attribute__((always_inline)) {
     const uint32_t ub = static_cast<uint32_t>(blk);
     ra[u] = __builtin_amdgcn_raw_buffer_load_b128(rA, voffA, s.a + ub * s.astr, kNT);
-    rs[u] = __builtin_amdgcn_raw_buffer_load_b32(rS, voffS, s.s + ub * s.sstr, kNT);
+    if constexpr (kStage) {
+      if (lds) issue_lds(u, blk);
+    } else {
+      rs[u] = __builtin_amdgcn_raw_buffer_load_b32(rS, voffS, s.s + ub * s.sstr, kNT);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) rb[u][c] = __builtin_amdgcn_raw_buffer_load_b128(rB, s.vb[c], s.b + ub * s.bstr, 0);
+      for (int c = 0; c < NC; ++c)
+        rb[u][c] = __builtin_amdgcn_raw_buffer_load_b128(rB, s.vb[c], s.b + ub * s.bstr, 0);
+    }
+  };
+  // kStage: the step's part of its scales and of the input rows of its
+  // columns 0 and 1 (lanes 0 and 1 hold them), loaded into registers
+  // (stage_load) and written to this wave's words (stage_store)
+  constexpr int kStgLd = kStgU4 / kWave;
+  struct Staged {
+    gx_u32x4 w[3][kStage ? kStgLd : 1];
+  };
+  auto stage_load = [&](const McStep& s, const McSrc<NC>& src, const int (&row)[NC], Staged& st)
+                        __attribute__((always_inline)) {
+    if constexpr (kStage) {
+      const int r0 = __builtin_amdgcn_readlane(row[0], 0), r1 = __builtin_amdgcn_readlane(row[0], 1);
+      const uint32_t part = static_cast<uint32_t>(p * bpp) * 64u;
+#pragma unroll
+      for (int q = 0; q < kStgLd; ++q) {
+        const uint32_t o = static_cast<uint32_t>(q * kWave + lane) * 16u;
+        st.w[0][q] = __builtin_amdgcn_raw_buffer_load_b128(rS, o, src.s, kNT);
+        // a row past the columns (r < 0) reads past the buffer: zeros
+        const uint32_t x0 = r0 < 0 ? a.x_bytes : static_cast<uint32_t>(r0) * static_cast<uint32_t>(K) * 2u + part;
+        const uint32_t x1 = r1 < 0 ? a.x_bytes : static_cast<uint32_t>(r1) * static_cast<uint32_t>(K) * 2u + part;
+        st.w[1][q] = __builtin_amdgcn_raw_buffer_load_b128(rB, o, x0, 0);
+        st.w[2][q] = __builtin_amdgcn_raw_buffer_load_b128(rB, o, x1, 0);
+      }
+      bcol = min(lo16, min(s.M - s.cg * kTok, 2) - 1);
+    }
+  };
+  auto stage_store = [&](const Staged& st) __attribute__((always_inline)) {
+    if constexpr (kStage) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int q = 0; q < kStgLd; ++q) stg_w[k * kStgU4 + q * kWave + lane] = st.w[k][q];
+    }
   };
 
   McStep cur = step_of(v, 0);
   McSrc<NC> cs;
+  Staged st0;
   {
     int crow[NC];
     rows_of(cur, crow);
     cs = src_of(cur, crow);
+    stage_load(cur, cs, crow, st0);  // ahead of the weights: the waits below then skip their loads
   }
   // the same load order as the steady state, so the waits for the first
   // step's blocks are as shallow as for every later step
 #pragma unroll
   for (int u = 0; u < D; ++u) {
-    issue(u, cs, u);
+    issue(u, cs, u, false);
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (kStage) {
+    stage_store(st0);
+#pragma unroll
+    for (int u = 0; u < D; ++u) issue_lds(u, u);
   }
 
   f32x4 acc[4][NC];
@@ -363,8 +433,8 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
 #pragma unroll
         for (int i = 0; i < BPP; ++i) {
           consume(i % D);
-          if (i + D < BPP) issue(i % D, cs, i + D);
-          else issue(i % D, ns, i + D - BPP);
+          if (i + D < BPP) issue(i % D, cs, i + D, true);
+          else issue(i % D, ns, i + D - BPP, false);
           __builtin_amdgcn_sched_barrier(0);  // keep the ring order: one block decoded at a time
         }
       } else {
@@ -372,7 +442,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
 #pragma unroll
           for (int u = 0; u < D; ++u) {
             consume(u);
-            issue(u, cs, i0 + u + D);
+            issue(u, cs, i0 + u + D, true);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
@@ -380,7 +450,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
           consume(u);
-          issue(u, ns, u);
+          issue(u, ns, u, false);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -447,6 +517,15 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
       if (nxt.valid) lds_barrier();  // work-group uniform
     }
     if (!nxt.valid) break;
+    if constexpr (kStage) {
+      // another item (a grid capped at the resident work-groups): its rows
+      // and scales, with a full wait, then its first blocks' LDS operands
+      Staged sn;
+      stage_load(nxt, ns, nrow, sn);
+      stage_store(sn);
+#pragma unroll
+      for (int u = 0; u < D; ++u) issue_lds(u, u);
+    }
     cur = nxt;
     cs = ns;
   }
@@ -471,11 +550,11 @@ __global__ void special_scan_kernel(const uint8_t* __restrict__ ws, TiledGeom g,
   }
 }
 
-template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false>
+template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false, bool kStage = false>
 hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_t s, const KernelTimer& timer) {
   static const int per_cu = [] {  // resident work-groups per CU (a property of the kernel)
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute, kStage>,
                                                      P * kWave, 0) != hipSuccess ||
         n < 1)
       n = 1;
@@ -487,7 +566,7 @@ hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_
   if constexpr (kRoute) grid += 8;  // work-groups past the items: they write the one-token plan
   McParams q = p;
   q.bpp = p.g.nb / P;
-  gx_launch(mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute>, dim3(static_cast<unsigned>(grid)),
+  gx_launch(mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute, kStage>, dim3(static_cast<unsigned>(grid)),
             dim3(P * kWave), 0, s, timer, q);
   return hipGetLastError();
 }
@@ -574,6 +653,9 @@ bool route_shape(int nb, int P, int D, int NC) {
 hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int num_cus, hipStream_t s,
                            const KernelTimer& timer) {
   if (p.g.nb == kNbGptOss) {
+    // the default shape with staged operands (at most 2 tokens: 2 slots per expert)
+    if (P == 3 && D == 5 && p.r_T <= 2)
+      return launch_mc_t<true, 3, 5, 1, false, 30, true, true>(p, max_items, num_cus, s, timer);
 #define GX_MC_GO(p_, d_) \
   if (P == p_ && D == d_) return launch_mc_t<true, p_, d_, 1, false, kNbGptOss / p_, true>(p, max_items, num_cus, s, timer);
     GX_MC_ROUTE_SHAPES(GX_MC_GO)
@@ -662,6 +744,12 @@ hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
   if (gated ? a.special_any1 : a.special_any2)  // weights with e8m0 code 0 or 255: the checking variant
     return gated ? launch_mc_t<true, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s, a.timer)
                  : launch_mc_t<false, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s, a.timer);
+  // down at one or two tokens (at most 2 slots per expert): the default
+  // shapes with staged operands
+  if (!gated && a.T <= 2 && g.nb == kNbGptOss && NC == 1 && P == 3) {
+    if (D == 10) return launch_mc_t<false, 3, 10, 1, false, 30, false, true>(p, max_items, a.num_cus, s, a.timer);
+    if (D == 5) return launch_mc_t<false, 3, 5, 1, false, 30, false, true>(p, max_items, a.num_cus, s, a.timer);
+  }
   return gated ? launch_mc_shape<true>(p, P, D, NC, max_items, a.num_cus, s, a.timer)
                : launch_mc_shape<false>(p, P, D, NC, max_items, a.num_cus, s, a.timer);
 }

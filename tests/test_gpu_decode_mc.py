@@ -431,12 +431,14 @@ def test_mc_decode_prefill_boundary(gpu, orc, torch_mod, pair120, T):
 
 
 @pytest.mark.parametrize("k", [1, 2, 8])
-@pytest.mark.parametrize("T", [1, 8])
+@pytest.mark.parametrize("T", [1, 2, 8])
 def test_mc_top_k_variants_gptoss20b(gpu, orc, torch_mod, k, T):
     """Top-k other than 4 at the GPT-OSS-20B shape (E=32, H=I=2880) on the
-    matrix-core decode path (one token: top-k and plan inside the gate_up
-    launch) against the exact path: indices and weights bit-exact, outputs
-    within the tolerance; token 0 against the oracle."""
+    matrix-core decode path (one and two tokens: top-k and plan inside the
+    gate_up launch, operands staged in LDS; two tokens at k=8 give 16
+    experts x 90 tiles, more than the resident work-groups, so work-groups
+    restage for further items) against the exact path: indices and weights
+    bit-exact, outputs within the tolerance; token 0 against the oracle."""
     torch = torch_mod
     E, H, I = 32, 2880, 2880
     w = moe_data.make_layer(950 + k, E, H, I, bias="random")
