@@ -106,15 +106,18 @@ struct McSrc {
 // exactly which ring slot each block needs); 0 = a.bpp, a multiple of D.
 // kRoute (gate_up, T <= kSmallTopkMaxT): the routing plan is made in the
 // prologue (McParams r_*) instead of read from a plan launch.
-// kStage (at most 2 slots per expert, one 16-token chunk): each wave copies
-// its K-part of the step's input rows and of its scales into LDS once and
-// reads the B operand and the scale dword of every block from there.  Per
-// block the global loads are then the 1 KiB of weights alone, where the
-// per-lane B and scale loads would return 1.25 KiB more, nearly all of it
-// repeated (one or two distinct 64-byte rows).  Meant for one item per
-// work-group; a work-group given another item copies that item's rows with
-// a full wait first.
-template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false, bool kStage = false>
+// kStg (straight-line steps): operands each wave copies into LDS once per
+// step, for its K-part, instead of loading them per block and lane.
+//   1: the scales.  Per block a lane needs one dword of 16, so the per-lane
+//      loads return 256 bytes for 64.
+//   2: the scales and the input rows of columns 0 and 1 (at most 2 slots
+//      per expert, one 16-token chunk).  The B loads would return 1 KiB per
+//      block for one or two distinct 64-byte rows.
+// With scales only, the next step's copy is loaded halfway through the step
+// and written to LDS after its last block, when every LDS read of the step
+// is issued.  With rows (one or two tokens, so mostly one item per
+// work-group) a work-group given another item copies it with a full wait.
+template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false, int kStg = 0>
 __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   constexpr int kFr = 4 * NC;   // accumulator fragments: (sub-tile, chunk)
   constexpr int kTok = 16 * NC; // token columns per step
@@ -127,11 +130,14 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   __shared__ int2 hdr[kMaxExperts];
   __shared__ f32x4 red[kRedAll];  // [P][kFr][64 lanes]
   __shared__ int32_t tok[kGated ? kLdsSlots : 1];  // slot -> token (gate_up, S <= kLdsSlots)
-  static_assert(!kStage || (BPP > 0 && NC == 1 && !kSpec), "staged operands: straight-line steps, one chunk");
-  // staged operands, per wave: the part's scales, input rows 0 and 1, each
-  // kStgU4 16-byte words (whole 64-lane loads)
-  constexpr int kStgU4 = kStage ? (BPP * 4 + kWave - 1) / kWave * kWave : 1;
-  __shared__ gx_u32x4 stg[kStage ? P * 3 * kStgU4 : 1];
+  constexpr bool kStageS = kStg >= 1, kStageB = kStg == 2;
+  static_assert(kStg == 0 || (BPP > 0 && !kSpec), "staged operands: straight-line steps");
+  static_assert(!kStageB || NC == 1, "staged rows: one chunk");
+  // staged operands, per wave: the part's scales (and input rows 0 and 1),
+  // kStgU4 16-byte words each (whole 64-lane loads)
+  constexpr int kStgRows = kStageB ? 3 : 1;
+  constexpr int kStgU4 = kStageS ? (BPP * 4 + kWave - 1) / kWave * kWave : 1;
+  __shared__ gx_u32x4 stg[kStageS ? P * kStgRows * kStgU4 : 1];
 
   const TiledGeom& g = a.g;
   const int lane = threadIdx.x & 63;
@@ -301,61 +307,68 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   gx_u32x4 ra[D];
   uint32_t rs[D];
   gx_u32x4 rb[D][NC];
-  // kStage: this wave's staged words and the staged row of this lane's column
-  gx_u32x4* const stg_w = stg + (kStage ? p * 3 * kStgU4 : 0);
+  // kStg: this wave's staged words and the staged row of this lane's column
+  gx_u32x4* const stg_w = stg + (kStageS ? p * kStgRows * kStgU4 : 0);
   int bcol = 0;
-  // block blk's scale dword and B operand from the staged words
+  // block blk's staged operands
   auto issue_lds = [&](int u, int blk) __attribute__((always_inline)) {
-    if constexpr (kStage) {
-      rs[u] = reinterpret_cast<const uint32_t*>(stg_w)[blk * 16 + lo16];
-      rb[u][0] = stg_w[(1 + bcol) * kStgU4 + blk * 4 + g16];
-    }
+    if constexpr (kStageS) rs[u] = reinterpret_cast<const uint32_t*>(stg_w)[blk * 16 + lo16];
+    if constexpr (kStageB) rb[u][0] = stg_w[(1 + bcol) * kStgU4 + blk * 4 + g16];
   };
-  // lds: kStage, block blk of the staged step (the next step's blocks are
-  // read from LDS once it is staged)
+  // lds: block blk belongs to the staged step (the next step's blocks read
+  // their staged operands once that step is staged)
   auto issue = [&](int u, const McSrc<NC>& s, int blk, bool lds) __attribute__((always_inline)) {
     const uint32_t ub = static_cast<uint32_t>(blk);
     ra[u] = __builtin_amdgcn_raw_buffer_load_b128(rA, voffA, s.a + ub * s.astr, kNT);
-    if constexpr (kStage) {
+    if constexpr (kStageS) {
       if (lds) issue_lds(u, blk);
     } else {
       rs[u] = __builtin_amdgcn_raw_buffer_load_b32(rS, voffS, s.s + ub * s.sstr, kNT);
+    }
+    if constexpr (!kStageB) {
 #pragma unroll
       for (int c = 0; c < NC; ++c)
         rb[u][c] = __builtin_amdgcn_raw_buffer_load_b128(rB, s.vb[c], s.b + ub * s.bstr, 0);
     }
   };
-  // kStage: the step's part of its scales and of the input rows of its
-  // columns 0 and 1 (lanes 0 and 1 hold them), loaded into registers
-  // (stage_load) and written to this wave's words (stage_store)
+  // The step's part of its scales (and of the input rows of its columns 0
+  // and 1, which lanes 0 and 1 hold), loaded into registers (stage_load)
+  // and written to this wave's words (stage_store).  A missing step reads
+  // past the buffers: zeros, never used.
   constexpr int kStgLd = kStgU4 / kWave;
   struct Staged {
-    gx_u32x4 w[3][kStage ? kStgLd : 1];
+    gx_u32x4 w[kStgRows][kStageS ? kStgLd : 1];
+    int bcol;
   };
   auto stage_load = [&](const McStep& s, const McSrc<NC>& src, const int (&row)[NC], Staged& st)
                         __attribute__((always_inline)) {
-    if constexpr (kStage) {
-      const int r0 = __builtin_amdgcn_readlane(row[0], 0), r1 = __builtin_amdgcn_readlane(row[0], 1);
+    if constexpr (kStageS) {
       const uint32_t part = static_cast<uint32_t>(p * bpp) * 64u;
 #pragma unroll
       for (int q = 0; q < kStgLd; ++q) {
         const uint32_t o = static_cast<uint32_t>(q * kWave + lane) * 16u;
         st.w[0][q] = __builtin_amdgcn_raw_buffer_load_b128(rS, o, src.s, kNT);
-        // a row past the columns (r < 0) reads past the buffer: zeros
-        const uint32_t x0 = r0 < 0 ? a.x_bytes : static_cast<uint32_t>(r0) * static_cast<uint32_t>(K) * 2u + part;
-        const uint32_t x1 = r1 < 0 ? a.x_bytes : static_cast<uint32_t>(r1) * static_cast<uint32_t>(K) * 2u + part;
-        st.w[1][q] = __builtin_amdgcn_raw_buffer_load_b128(rB, o, x0, 0);
-        st.w[2][q] = __builtin_amdgcn_raw_buffer_load_b128(rB, o, x1, 0);
+        if constexpr (kStageB) {
+          const int r0 = __builtin_amdgcn_readlane(row[0], 0), r1 = __builtin_amdgcn_readlane(row[0], 1);
+          // a row past the columns (r < 0) reads past the buffer: zeros
+          const uint32_t x0 =
+              !s.valid || r0 < 0 ? a.x_bytes : static_cast<uint32_t>(r0) * static_cast<uint32_t>(K) * 2u + part;
+          const uint32_t x1 =
+              !s.valid || r1 < 0 ? a.x_bytes : static_cast<uint32_t>(r1) * static_cast<uint32_t>(K) * 2u + part;
+          st.w[1][q] = __builtin_amdgcn_raw_buffer_load_b128(rB, o, x0, 0);
+          st.w[2][q] = __builtin_amdgcn_raw_buffer_load_b128(rB, o, x1, 0);
+        }
       }
-      bcol = min(lo16, min(s.M - s.cg * kTok, 2) - 1);
+      st.bcol = kStageB && s.valid ? min(lo16, min(s.M - s.cg * kTok, 2) - 1) : 0;
     }
   };
   auto stage_store = [&](const Staged& st) __attribute__((always_inline)) {
-    if constexpr (kStage) {
+    if constexpr (kStageS) {
 #pragma unroll
-      for (int k = 0; k < 3; ++k)
+      for (int k = 0; k < kStgRows; ++k)
 #pragma unroll
         for (int q = 0; q < kStgLd; ++q) stg_w[k * kStgU4 + q * kWave + lane] = st.w[k][q];
+      bcol = st.bcol;
     }
   };
 
@@ -375,7 +388,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     issue(u, cs, u, false);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if constexpr (kStage) {
+  if constexpr (kStageS) {
     stage_store(st0);
 #pragma unroll
     for (int u = 0; u < D; ++u) issue_lds(u, u);
@@ -404,6 +417,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const McSrc<NC> ns = src_of(nxt, nrow);
+    Staged stn;  // the next step's staged operands
 
     // The blocks of this step; the branch on the expert's special-code flag
     // is taken once per step, so the block loop itself has no branches.
@@ -435,6 +449,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
           consume(i % D);
           if (i + D < BPP) issue(i % D, cs, i + D, true);
           else issue(i % D, ns, i + D - BPP, false);
+          if (kStg == 1 && i == BPP / 2) stage_load(nxt, ns, nrow, stn);
           __builtin_amdgcn_sched_barrier(0);  // keep the ring order: one block decoded at a time
         }
       } else {
@@ -460,6 +475,13 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
       else run(std::false_type{});
     } else {
       run(std::false_type{});
+    }
+    if constexpr (kStg == 1) {
+      // every LDS read of this step is issued: the next step's operands
+      // replace them, and its first blocks (already in flight) read theirs
+      stage_store(stn);
+#pragma unroll
+      for (int u = 0; u < D; ++u) issue_lds(u, u);
     }
 
     // Epilogue: fragment (i, c) of lane l is rows t*64 + 16 i + 4 (l/16) + r,
@@ -517,9 +539,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
       if (nxt.valid) lds_barrier();  // work-group uniform
     }
     if (!nxt.valid) break;
-    if constexpr (kStage) {
-      // another item (a grid capped at the resident work-groups): its rows
-      // and scales, with a full wait, then its first blocks' LDS operands
+    if constexpr (kStg == 2) {
       Staged sn;
       stage_load(nxt, ns, nrow, sn);
       stage_store(sn);
@@ -550,11 +570,11 @@ __global__ void special_scan_kernel(const uint8_t* __restrict__ ws, TiledGeom g,
   }
 }
 
-template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false, bool kStage = false>
+template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false, int kStg = 0>
 hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_t s, const KernelTimer& timer) {
   static const int per_cu = [] {  // resident work-groups per CU (a property of the kernel)
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute, kStage>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute, kStg>,
                                                      P * kWave, 0) != hipSuccess ||
         n < 1)
       n = 1;
@@ -566,7 +586,7 @@ hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_
   if constexpr (kRoute) grid += 8;  // work-groups past the items: they write the one-token plan
   McParams q = p;
   q.bpp = p.g.nb / P;
-  gx_launch(mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute, kStage>, dim3(static_cast<unsigned>(grid)),
+  gx_launch(mc_stream_kernel<kGated, P, D, NC, kSpec, BPP, kRoute, kStg>, dim3(static_cast<unsigned>(grid)),
             dim3(P * kWave), 0, s, timer, q);
   return hipGetLastError();
 }
@@ -613,7 +633,7 @@ hipError_t launch_mc_shape(const McParams& p, int P, int D, int NC, int max_item
   if (p.g.nb == kNbGptOss) {
 #define GX_MC_GO(p_, d_, nc_) \
   if (P == p_ && D == d_ && NC == nc_)  \
-    return launch_mc_t<kGated, p_, d_, nc_, false, kNbGptOss / p_>(p, max_items, num_cus, s, timer);
+    return launch_mc_t<kGated, p_, d_, nc_, false, kNbGptOss / p_, false, 1>(p, max_items, num_cus, s, timer);
     GX_MC_SHAPES(GX_MC_GO)
 #undef GX_MC_GO
   }
@@ -655,9 +675,10 @@ hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int n
   if (p.g.nb == kNbGptOss) {
     // the default shape with staged operands (at most 2 tokens: 2 slots per expert)
     if (P == 3 && D == 5 && p.r_T <= 2)
-      return launch_mc_t<true, 3, 5, 1, false, 30, true, true>(p, max_items, num_cus, s, timer);
+      return launch_mc_t<true, 3, 5, 1, false, 30, true, 2>(p, max_items, num_cus, s, timer);
 #define GX_MC_GO(p_, d_) \
-  if (P == p_ && D == d_) return launch_mc_t<true, p_, d_, 1, false, kNbGptOss / p_, true>(p, max_items, num_cus, s, timer);
+  if (P == p_ && D == d_)                                                                                 \
+    return launch_mc_t<true, p_, d_, 1, false, kNbGptOss / p_, true, 1>(p, max_items, num_cus, s, timer);
     GX_MC_ROUTE_SHAPES(GX_MC_GO)
 #undef GX_MC_GO
   }
@@ -747,8 +768,8 @@ hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
   // down at one or two tokens (at most 2 slots per expert): the default
   // shapes with staged operands
   if (!gated && a.T <= 2 && g.nb == kNbGptOss && NC == 1 && P == 3) {
-    if (D == 10) return launch_mc_t<false, 3, 10, 1, false, 30, false, true>(p, max_items, a.num_cus, s, a.timer);
-    if (D == 5) return launch_mc_t<false, 3, 5, 1, false, 30, false, true>(p, max_items, a.num_cus, s, a.timer);
+    if (D == 10) return launch_mc_t<false, 3, 10, 1, false, 30, false, 2>(p, max_items, a.num_cus, s, a.timer);
+    if (D == 5) return launch_mc_t<false, 3, 5, 1, false, 30, false, 2>(p, max_items, a.num_cus, s, a.timer);
   }
   return gated ? launch_mc_shape<true>(p, P, D, NC, max_items, a.num_cus, s, a.timer)
                : launch_mc_shape<false>(p, P, D, NC, max_items, a.num_cus, s, a.timer);
