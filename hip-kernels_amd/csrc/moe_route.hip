@@ -24,6 +24,8 @@
 // rows) instead of LDS permutes: a reduction to lane 0 is 6 VALU steps.
 #include <float.h>
 
+#include <type_traits>
+
 #include "moe_device.h"
 #include "moe_kernels.h"
 #include "moe_stages.h"
@@ -530,12 +532,14 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_kernel(const void* log
 
 // Top-k + plan for T <= 64 tokens with one lane per token (E <= 128, a
 // multiple of 8): wave w sorts the 8 logits of experts 8w..8w+7 of its
-// lane's token (a depth-6 sorting network on 64-bit entries, key << 32 |
-// 0xffff - expert: larger = earlier in the reference's order, 0 = not
-// selectable), keeps the top K, and the lists of the E/8 slices meet in a
-// 4-level tree of bitonic merges through LDS.  Each lane then applies its
-// token's softmax.  Every step is a few dependent instructions on all tokens
-// at once, where one wave per token would chain k wave-wide reductions.
+// lane's token (a depth-6 sorting network), keeps the top K, and the lists
+// of the E/8 slices meet in a 4-level tree of bitonic merges through LDS.
+// Each lane then applies its token's softmax.  Every step is a few
+// dependent instructions on all tokens at once, where one wave per token
+// would chain k wave-wide reductions.  Entries: larger = earlier in the
+// reference's order, 0 = not selectable; fp32 logits: key << 32 | 0xffff -
+// expert; bf16 logits: the key's high half (which holds a bf16 value
+// exactly) | 0xffff - expert, so a compare-exchange is one max and one min.
 constexpr int kLaneTopkSlice = 8;
 constexpr int kLaneTopkMaxT = kWave;
 
@@ -544,12 +548,18 @@ __device__ __forceinline__ void ce_desc(uint64_t& a, uint64_t& b) {
   a = hi;
   b = lo;
 }
+__device__ __forceinline__ void ce_desc(uint32_t& a, uint32_t& b) {
+  const uint32_t hi = max(a, b), lo = min(a, b);
+  a = hi;
+  b = lo;
+}
 
 template <bool F32, int K>
 __global__ __launch_bounds__(kPlanThreads) void topk_plan_lanes_kernel(const void* logits, int T, int E, int variant,
                                                                       int32_t* idx, float* w, PlanBufs p) {
+  using Entry = std::conditional_t<F32, uint64_t, uint32_t>;
   constexpr int kSlices = kPlanThreads / kWave;  // 16: up to 128 experts
-  __shared__ uint64_t s_list[kSlices][kLaneTopkMaxT][K];
+  __shared__ Entry s_list[kSlices][kLaneTopkMaxT][K];
   __shared__ int32_t s_idx[kLaneTopkMaxT * K];
   __shared__ float s_w[kLaneTopkMaxT * K];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -568,11 +578,13 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_lanes_kernel(const voi
       const uint4 a = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(logits) + o);
       unpack_bf16x8(a, v);
     }
-    uint64_t en[kLaneTopkSlice];
+    Entry en[kLaneTopkSlice];
 #pragma unroll
     for (int i = 0; i < kLaneTopkSlice; ++i) {
       const uint32_t key = select_key(sanitize_logit(v[i]));
-      en[i] = key ? (static_cast<uint64_t>(key) << 32) | static_cast<uint32_t>(0xffff - (e0 + i)) : 0ull;
+      const uint32_t ix = static_cast<uint32_t>(0xffff - (e0 + i));
+      if constexpr (F32) en[i] = key ? (static_cast<uint64_t>(key) << 32) | ix : 0ull;
+      else en[i] = key ? (key & 0xffff0000u) | ix : 0u;
     }
     // optimal 19-comparator sorting network for 8 inputs (descending)
     ce_desc(en[0], en[2]); ce_desc(en[1], en[3]); ce_desc(en[4], en[6]); ce_desc(en[5], en[7]);
@@ -582,17 +594,17 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_lanes_kernel(const voi
     ce_desc(en[1], en[4]); ce_desc(en[3], en[6]);
     ce_desc(en[1], en[2]); ce_desc(en[3], en[4]); ce_desc(en[5], en[6]);
 #pragma unroll
-    for (int i = 0; i < K; ++i) s_list[wv][t][i] = i < kLaneTopkSlice ? en[i < kLaneTopkSlice ? i : 0] : 0ull;
+    for (int i = 0; i < K; ++i) s_list[wv][t][i] = i < kLaneTopkSlice ? en[i < kLaneTopkSlice ? i : 0] : Entry{0};
   }
   __syncthreads();
   // merge tree: at width d, wave w merges slice lists 2dw and 2dw + d
   for (int d = 1; d < nsl; d <<= 1) {
     const int a = 2 * d * wv, b = a + d;
     if (b < nsl) {
-      uint64_t c[K];
+      Entry c[K];
 #pragma unroll
       for (int i = 0; i < K; ++i) {
-        const uint64_t x = s_list[a][t][i], y = s_list[b][t][K - 1 - i];
+        const Entry x = s_list[a][t][i], y = s_list[b][t][K - 1 - i];
         c[i] = x > y ? x : y;
       }
 #pragma unroll
@@ -613,10 +625,14 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_lanes_kernel(const voi
       sel_v[s2] = -FLT_MAX;
       sel_i[s2] = -1;
       if (s2 < K) {
-        const uint64_t en = s_list[0][t][s2 < K ? s2 : 0];
+        const Entry en = s_list[0][t][s2 < K ? s2 : 0];
         if (en) {
-          const uint32_t key = static_cast<uint32_t>(en >> 32);
-          sel_v[s2] = __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+          if constexpr (F32) {
+            const uint32_t key = static_cast<uint32_t>(en >> 32);
+            sel_v[s2] = __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+          } else {
+            sel_v[s2] = bf16_of_key(en);
+          }
           sel_i[s2] = 0xffff - static_cast<int>(en & 0xffffu);
         }
       }
