@@ -65,6 +65,7 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
   const int S = T * k;
   const int C = ((S + NW - 1) / NW + kWave - 1) / kWave * kWave;  // slots per wave, a multiple of 64
   const int s0 = min(S, warp * C), s1 = min(S, s0 + C);
+  const int nws = C > 0 ? (S + C - 1) / C : 0;  // waves holding slots: the only nonzero counts
 
   // rank of this lane's slot among the 64 slots' equal experts and the
   // group mask (wave-uniform control flow)
@@ -79,7 +80,7 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
     return __popcll(peers & ((1ull << lane) - 1ull));
   };
 
-  for (int i = tid; i < NW * kMaxExperts; i += NT) (&s_wc[0][0])[i] = 0;
+  for (int i = tid; i < nws * kMaxExperts; i += NT) (&s_wc[0][0])[i] = 0;
   lds_barrier();
   for (int b = s0; b < s1; b += kWave) {
     const int s = b + lane;
@@ -100,7 +101,7 @@ __device__ void build_plan(IdxFn idx, int T, int k, int E, PlanBufs p) {
   if (tid < kMaxExperts) {  // wave-uniform
     if (tid < E) {
 #pragma unroll 4
-      for (int w = 0; w < NW; ++w) {
+      for (int w = 0; w < nws; ++w) {
         const int v = s_wc[w][tid];
         s_wc[w][tid] = c;
         c += v;
