@@ -925,6 +925,34 @@ __global__ __launch_bounds__(256) void quant_fp8x2_kernel(const uint16_t* __rest
 // the last work-group to finish zeroes them for the next launch.
 constexpr int kQueueStride = 32;  // one 128-byte line per counter
 
+// LDS words of the persistent loop, past every ring layout: word[0..1] the
+// taken index (alternating rounds), word[2] the next queue to try.
+constexpr int kWordNext = 2;
+
+// Queue (x0 + k) & 7 was found empty: the next queue of the rotation that
+// still holds entries, as the new k, or 8 for none.  Thread 0 reads every
+// counter in one round trip; a counter at or past its queue's length marks
+// the queue empty for good (counters only grow), so only queues with
+// entries left are tried, where trying each in turn cost an atomic round
+// trip and a tile-list rebuild apiece at the end of the launch.
+__device__ __forceinline__ int next_queue(const int* queue, int* word, int x0, int k, const TileList& L, int nwt) {
+  if (threadIdx.x == 0) {
+    int c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = __hip_atomic_load(&queue[kQueueStride * j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int nk = 8;
+#pragma unroll
+    for (int j = 7; j > 0; --j) {
+      const int x = (x0 + j) & 7;
+      int lf;
+      if (j > k && c[x] < queue_len(L, nwt, x, lf)) nk = j;
+    }
+    word[kWordNext] = nk;
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(word[kWordNext]);
+}
+
 template <bool kGated, int kW>
 __global__ __launch_bounds__(kW * kWave, WgShape<kW>::kPerCU) void grouped_mfma_kernel(GroupedParams a) {
   constexpr int kRingBytes = WgShape<kW>::kRingBytes;
@@ -954,7 +982,9 @@ __global__ __launch_bounds__(kW * kWave, WgShape<kW>::kPerCU) void grouped_mfma_
     const TileList L = make_tile_list(a.offsets, a.E, lane);
     int lenF;
     if (t >= queue_len(L, a.nwt, x, lenF)) {
-      if (!persistent || ++k == 8) break;
+      if (!persistent) break;
+      k = next_queue(a.queue, word, x0, k, L, a.nwt);
+      if (k == 8) break;
       continue;
     }
     TileCoord tc;
@@ -990,7 +1020,8 @@ __global__ __launch_bounds__(kMxW * kWave, 1) void grouped_mx_kernel(GroupedPara
     const TileList L = make_tile_list(a.offsets, a.E, lane);
     int lenF;
     if (t >= queue_len(L, a.nwt, x, lenF)) {
-      if (++k == 8) break;
+      k = next_queue(a.queue, word, x0, k, L, a.nwt);
+      if (k == 8) break;
       continue;
     }
     TileCoord tc;
