@@ -24,6 +24,7 @@
 // rows) instead of LDS permutes: a reduction to lane 0 is 6 VALU steps.
 #include <float.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "moe_device.h"
@@ -409,7 +410,7 @@ __global__ __launch_bounds__(kRouteThreads) void logits_norm_kernel(
 // tree of tree_sum_lane0 in registers (level m adds lane l + m into lane l,
 // m = 32 .. 1); lane p of wave 0 adds the four wave sums in order from 0.
 constexpr int kLdsTT = 8, kLdsEPW = 8;
-template <bool F32>
+template <bool F32, bool kHoldW>
 __global__ __launch_bounds__(kRouteThreads, 2) void logits_lds_kernel(const uint16_t* __restrict__ x,
                                                                       const uint16_t* __restrict__ W,
                                                                       const uint16_t* __restrict__ bias, int T, int E,
@@ -419,71 +420,101 @@ __global__ __launch_bounds__(kRouteThreads, 2) void logits_lds_kernel(const uint
   __shared__ float red[4][kPairs][kWave + 1];  // [wave][pair][lane], padded: conflict-free rows and columns
   const int lane = threadIdx.x & 63;
   const int j = threadIdx.x >> 6;
-  const int t0 = blockIdx.y * kLdsTT, e0 = blockIdx.x * kLdsEPW;
+  const int e0 = blockIdx.x * kLdsEPW;
   const int KV = H >> 3;
-  float acc[kLdsTT][kLdsEPW];
-#pragma unroll
-  for (int t = 0; t < kLdsTT; ++t)
-#pragma unroll
-    for (int e = 0; e < kLdsEPW; ++e) acc[t][e] = 0.0f;
   // rows past T / E read row 0 (their results are not stored)
-  const uint16_t* xr = x + static_cast<size_t>(t0 < T ? t0 : 0) * H;
   const uint16_t* wr = W + static_cast<size_t>(e0 < E ? e0 : 0) * H;
-  const int tn = min(kLdsTT, T - t0), en = min(kLdsEPW, E - e0);
-  auto load = [&](int c, uint4 (&xv)[kLdsTT], uint4 (&wv4)[kLdsEPW]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int t = 0; t < kLdsTT; ++t)
-      xv[t] = *reinterpret_cast<const uint4*>(xr + static_cast<size_t>(t < tn ? t : 0) * H + c * 8);
+  const int en = min(kLdsEPW, E - e0);
+  auto load_w = [&](int c, uint4 (&wv4)[kLdsEPW]) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < kLdsEPW; ++e)
       wv4[e] = *reinterpret_cast<const uint4*>(wr + static_cast<size_t>(e < en ? e : 0) * H + c * 8);
   };
-  auto fma_chunk = [&](const uint4 (&xv)[kLdsTT], const uint4 (&wv4)[kLdsEPW]) __attribute__((always_inline)) {
-    float wf[kLdsEPW][8];
+  // kHoldW (H <= 4096, so a chain has at most two chunks): the lane's chunks
+  // of the 8 router rows, loaded once and held while the work-group walks
+  // its token blocks (blockIdx.y, + gridDim.y, ...); otherwise one token
+  // block per work-group with both operands loaded per chunk.
+  uint4 wh[kHoldW ? 2 : 1][kLdsEPW];
+  if constexpr (kHoldW) {
 #pragma unroll
-    for (int e = 0; e < kLdsEPW; ++e) unpack_bf16x8(wv4[e], wf[e]);
-#pragma unroll
-    for (int t = 0; t < kLdsTT; ++t) {
-      float xf[8];
-      unpack_bf16x8(xv[t], xf);
-#pragma unroll
-      for (int e = 0; e < kLdsEPW; ++e)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[t][e] = __builtin_fmaf(xf[i], wf[e][i], acc[t][e]);
-    }
-  };
-  // Chunks tau, tau + 256, ... in order.
-  for (int c = lane + kWave * j; c < KV; c += kRouteThreads) {
-    uint4 xa[kLdsTT], wa[kLdsEPW];
-    load(c, xa, wa);
-    fma_chunk(xa, wa);
+    for (int q = 0; q < 2; ++q) load_w(min(lane + kWave * j + kRouteThreads * q, KV - 1), wh[q]);
   }
+  const int ntb = (T + kLdsTT - 1) / kLdsTT;
+  for (int tb = blockIdx.y; tb < ntb; tb += kHoldW ? static_cast<int>(gridDim.y) : ntb) {
+    const int t0 = tb * kLdsTT;
+    float acc[kLdsTT][kLdsEPW];
 #pragma unroll
-  for (int t = 0; t < kLdsTT; ++t)
+    for (int t = 0; t < kLdsTT; ++t)
 #pragma unroll
-    for (int e = 0; e < kLdsEPW; ++e) red[j][t * kLdsEPW + e][lane] = acc[t][e];
-  __syncthreads();
-  float cv[kWave];
+      for (int e = 0; e < kLdsEPW; ++e) acc[t][e] = 0.0f;
+    const uint16_t* xr = x + static_cast<size_t>(t0 < T ? t0 : 0) * H;
+    const int tn = min(kLdsTT, T - t0);
+    auto load_x = [&](int c, uint4 (&xv)[kLdsTT]) __attribute__((always_inline)) {
 #pragma unroll
-  for (int l = 0; l < kWave; ++l) cv[l] = red[j][lane][l];
+      for (int t = 0; t < kLdsTT; ++t)
+        xv[t] = *reinterpret_cast<const uint4*>(xr + static_cast<size_t>(t < tn ? t : 0) * H + c * 8);
+    };
+    auto fma_chunk = [&](const uint4 (&xv)[kLdsTT], const uint4 (&wv4)[kLdsEPW]) __attribute__((always_inline)) {
+      float wf[kLdsEPW][8];
 #pragma unroll
-  for (int m = kWave / 2; m >= 1; m >>= 1)
+      for (int e = 0; e < kLdsEPW; ++e) unpack_bf16x8(wv4[e], wf[e]);
 #pragma unroll
-    for (int l = 0; l < m; ++l) cv[l] = cv[l] + cv[l + m];
-  __syncthreads();  // every row read before the sums overwrite column 0
-  red[j][lane][0] = cv[0];
-  __syncthreads();
-  if (j == 0) {
-    const int t = lane / kLdsEPW, e = lane % kLdsEPW;
-    float v = 0.0f;
+      for (int t = 0; t < kLdsTT; ++t) {
+        float xf[8];
+        unpack_bf16x8(xv[t], xf);
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) v = v + red[jj][lane][0];
-    if (t < tn && e < en) {
-      if (bias != nullptr) v = v + bf16_to_f32(bias[e0 + e]);
-      const size_t o = static_cast<size_t>(t0 + t) * E + e0 + e;
-      if constexpr (F32) reinterpret_cast<float*>(logits)[o] = v;
-      else reinterpret_cast<uint16_t*>(logits)[o] = f32_to_bf16(v);
+        for (int e = 0; e < kLdsEPW; ++e)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[t][e] = __builtin_fmaf(xf[i], wf[e][i], acc[t][e]);
+      }
+    };
+    // Chunks tau, tau + 256, ... in order.
+    if constexpr (kHoldW) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int c = lane + kWave * j + kRouteThreads * q;
+        if (c < KV) {
+          uint4 xa[kLdsTT];
+          load_x(c, xa);
+          fma_chunk(xa, wh[q]);
+        }
+      }
+    } else {
+      for (int c = lane + kWave * j; c < KV; c += kRouteThreads) {
+        uint4 xa[kLdsTT], wa[kLdsEPW];
+        load_x(c, xa);
+        load_w(c, wa);
+        fma_chunk(xa, wa);
+      }
     }
+#pragma unroll
+    for (int t = 0; t < kLdsTT; ++t)
+#pragma unroll
+      for (int e = 0; e < kLdsEPW; ++e) red[j][t * kLdsEPW + e][lane] = acc[t][e];
+    __syncthreads();
+    float cv[kWave];
+#pragma unroll
+    for (int l = 0; l < kWave; ++l) cv[l] = red[j][lane][l];
+#pragma unroll
+    for (int m = kWave / 2; m >= 1; m >>= 1)
+#pragma unroll
+      for (int l = 0; l < m; ++l) cv[l] = cv[l] + cv[l + m];
+    __syncthreads();  // every row read before the sums overwrite column 0
+    red[j][lane][0] = cv[0];
+    __syncthreads();
+    if (j == 0) {
+      const int t = lane / kLdsEPW, e = lane % kLdsEPW;
+      float v = 0.0f;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) v = v + red[jj][lane][0];
+      if (t < tn && e < en) {
+        if (bias != nullptr) v = v + bf16_to_f32(bias[e0 + e]);
+        const size_t o = static_cast<size_t>(t0 + t) * E + e0 + e;
+        if constexpr (F32) reinterpret_cast<float*>(logits)[o] = v;
+        else reinterpret_cast<uint16_t*>(logits)[o] = f32_to_bf16(v);
+      }
+    }
+    if constexpr (kHoldW) __syncthreads();  // the sums are read before the next block's chains land in red
   }
 }
 
@@ -943,8 +974,16 @@ hipError_t launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t
     gx_launch(logits_kernel<1, 1, 0, F32>, dim3((a.E + 3) / 4, a.T), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b,
               a.T, a.E, a.H, a.logits);
   } else {
-    gx_launch(logits_lds_kernel<F32>, dim3((a.E + kLdsEPW - 1) / kLdsEPW, (a.T + kLdsTT - 1) / kLdsTT),
-              dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b, a.T, a.E, a.H, a.logits);
+    const int gx = (a.E + kLdsEPW - 1) / kLdsEPW, ntb = (a.T + kLdsTT - 1) / kLdsTT;
+    if (a.H <= 8 * 2 * kRouteThreads) {  // every chain holds at most two chunks: router rows held across blocks
+      // about two work-groups per CU of 256 (the kernel's occupancy), each walking token blocks
+      const int gy = std::min(ntb, std::max(1, 512 / gx));
+      gx_launch(logits_lds_kernel<F32, true>, dim3(gx, gy), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b, a.T, a.E,
+                a.H, a.logits);
+    } else {
+      gx_launch(logits_lds_kernel<F32, false>, dim3(gx, ntb), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b, a.T,
+                a.E, a.H, a.logits);
+    }
   }
   return hipGetLastError();
 }
