@@ -350,6 +350,39 @@ def test_gptoss120b_prefill_zipf_4096(gpu, orc, torch_mod, zipf120):
     exact.set_trace_gate_up(False)
 
 
+def test_gptoss120b_prefill_max_tokens_8192(gpu, orc, torch_mod, zipf120):
+    """The engine's largest prefill (MAX_TOKENS = 8192, engine.cu:860) through
+    the whole layer: router on many tokens, the multi-launch plan of 32,768
+    slots, the grouped products and the combine.  A token's arithmetic does
+    not depend on the batch it rides in, so the 8192-token call must equal
+    its two 4096-token halves bit for bit; 32 sampled tokens are checked
+    against the oracle (routing included), and a second call must repeat
+    the first."""
+    torch = torch_mod
+    w, pre, _, _ = zipf120
+    E, k, H, I, T = 128, 4, 2880, 2880, 8192
+    cfg = gpu.default_config(E, T)
+    cfg.hidden_size, cfg.intermediate_size, cfg.top_k = H, I, k
+    layer = gpu.MoELayer().init(cfg, 0, pre.t["router_w"], pre.t.get("router_b"), pre.t.get("w1_bias"),
+                                pre.t.get("w2_bias"), tiled=pre.tiled)
+    try:
+        x, res = moe_data.make_tokens(8192, T, H)
+        dx, dr = dev(x, torch), dev(res, torch)
+        say("prefill T=8192 full layer")
+        out = host(layer.forward_prenormed(dx, dr))
+        say("prefill T=8192 as two halves of 4096")
+        half = T // 2
+        lo = host(layer.forward_prenormed(dx[:half].contiguous(), dr[:half].contiguous()))
+        hi = host(layer.forward_prenormed(dx[half:].contiguous(), dr[half:].contiguous()))
+        assert np.array_equal(out, np.concatenate([lo, hi]))
+        sel = np.sort(np.random.default_rng(8192).choice(T, 32, replace=False))
+        ref = orc.moe_forward(w, x[sel], res[sel], E, k, H, I)
+        check_layer_out(out[sel], ref, "T=8192 matrix core vs oracle (32 tokens)")
+        assert np.array_equal(out, host(layer.forward_prenormed(dx, dr)))  # run-to-run deterministic
+    finally:
+        layer.destroy()
+
+
 @pytest.mark.parametrize("mode", [1, 2])
 def test_gptoss120b_prefill_block_scaled_error(gpu, orc, torch_mod, zipf120, mode):
     """prefill_block_scaled = 1 (fp4 weights x two e4m3 activation parts,
