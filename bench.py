@@ -662,6 +662,13 @@ def main():
             extra["prefill"]["block_scaled_variants"][str(m)] = dict(
                 (key, v[key]) for key in ("ms_per_layer", "kernel_ms", "gate_up_tflops"))
         log(json.dumps(extra["prefill"]["block_scaled_variants"]))
+        # the same layer at other prompt lengths, up to the engine's MAX_TOKENS (8192)
+        extra["prefill"]["sizes"] = {}
+        for Tp in (1024, 2048, 8192):
+            v = bench_prefill(g, torch, copies[0], T=Tp)
+            extra["prefill"]["sizes"][str(Tp)] = dict(
+                (key, v[key]) for key in ("ms_per_layer", "tokens_per_s", "tflops_layer", "kernel_ms"))
+        log(json.dumps(extra["prefill"]["sizes"]))
         log("router + top-k T=4096 fp32 logits")
         extra["router"] = bench_router(g, torch)
         log(json.dumps(extra["router"]))

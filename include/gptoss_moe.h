@@ -65,7 +65,11 @@ typedef struct gptoss_moe_config {
    * 0 (default): on the matrix cores, fp32 accumulation in the matrix core's
    * order (like prefill).  1: through the exact VALU kernels, whose results
    * are bit-identical to the canonical order (one ascending fma chain per
-   * K-part, parts added in order), at a lower streaming rate. */
+   * K-part, parts added in order), at a lower streaming rate.  The
+   * matrix-core decode kernels take at most 1024 slots (T * top_k); larger
+   * forwards below prefill_min_tokens (only when it is 0 or above 256 at
+   * top-4) run the exact kernels, about 14 ms for 1024 GPT-OSS-120B tokens
+   * against 0.49 ms on the prefill path. */
   int decode_exact;
   /* Prefill expert products (T >= prefill_min_tokens).  0 (default): the
    * bf16 matrix core with the weights decoded in registers; fp32 accumulation.
