@@ -692,19 +692,23 @@ hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int n
 // Default shape for nb blocks and S routed slots, measured on MI355X at the
 // GPT-OSS-120B shape (graph-replayed steps at 1..64 tokens, 12 compiled
 // shapes; most differ by a few percent): three K-parts with a 5-block ring
-// up to 2 tokens and at 8, two parts with a 9-block ring at 4, three parts
-// with a 10-block ring from 16 tokens (1-2 % ahead of six parts with each
+// up to 2 tokens and at 8, two parts with a 9-block ring for down at 4,
+// three parts with a 10-block ring otherwise and from 16 tokens (1-2 % ahead of six parts with each
 // wave's whole 15-block part in flight, in repeated runs at 16, 32 and 64).
 // The same shape serves both products, except the down product of one token
 // (k x 45 items, one per work-group), which takes the 10-block ring (B=1:
 // 24.0 against 24.5 us per layer in three paired runs; from two tokens the
-// shared shape is ahead).
+// shared shape is ahead).  At 9-16 slots (after the staged scales, three
+// passes): gate_up takes three parts with the 10-block ring (16 slots: 26.0
+// against 29.3 us; 12 slots: even), and so does down up to 12 slots (11.4
+// against 12.9 us), while down at 13-16 slots keeps two parts with the
+// 9-block ring (13.8 against 16.1 us).
 void pick_shape(int nb, int S, bool gated, int T, int& P, int& D, int& NC) {
   NC = 1;
   if (nb == kNbGptOss) {
     if (!gated && T == 1) { P = 3; D = 10; }
     else if (S <= 8 || (S > 16 && S <= 32)) { P = 3; D = 5; }
-    else if (S <= 16) { P = 2; D = 9; }
+    else if (S <= 16 && !gated && S > 12) { P = 2; D = 9; }
     else { P = 3; D = 10; }
     return;
   }
