@@ -702,13 +702,16 @@ hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int n
 // passes): gate_up takes three parts with the 10-block ring (16 slots: 26.0
 // against 29.3 us; 12 slots: even), and so does down up to 12 slots (11.4
 // against 12.9 us), while down at 13-16 slots keeps two parts with the
-// 9-block ring (13.8 against 16.1 us).
+// 9-block ring (13.8 against 16.1 us).  gate_up keeps the 10-block ring up
+// to 24 slots (20 slots: 31.0 against 35.8 us, 24: 34.4 against 38.5) and
+// takes the 5-block ring only at 25-32 (32 slots: 40.4 against 41.6 us).
 void pick_shape(int nb, int S, bool gated, int T, int& P, int& D, int& NC) {
   NC = 1;
   if (nb == kNbGptOss) {
+    const bool ring5 = gated ? S <= 8 || (S > 24 && S <= 32) : S <= 8 || (S > 16 && S <= 32);
     if (!gated && T == 1) { P = 3; D = 10; }
-    else if (S <= 8 || (S > 16 && S <= 32)) { P = 3; D = 5; }
-    else if (S <= 16 && !gated && S > 12) { P = 2; D = 9; }
+    else if (ring5) { P = 3; D = 5; }
+    else if (!gated && S > 12 && S <= 16) { P = 2; D = 9; }
     else { P = 3; D = 10; }
     return;
   }
