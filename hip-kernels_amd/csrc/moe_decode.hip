@@ -704,7 +704,8 @@ hipError_t launch_mc_route(const McParams& p, int P, int D, int max_items, int n
 // against 12.9 us), while down at 13-16 slots keeps two parts with the
 // 9-block ring (13.8 against 16.1 us).  gate_up keeps the 10-block ring up
 // to 24 slots (20 slots: 31.0 against 35.8 us, 24: 34.4 against 38.5) and
-// takes the 5-block ring only at 25-32 (32 slots: 40.4 against 41.6 us).
+// takes the 5-block ring only at 25-32 (28 slots: 38.9 against 39.9 us,
+// 32: 40.4 against 41.6).
 void pick_shape(int nb, int S, bool gated, int T, int& P, int& D, int& NC) {
   NC = 1;
   if (nb == kNbGptOss) {
