@@ -20,7 +20,12 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <algorithm>
+#include <climits>
 #include <cstdint>
+#include <cstdio>
+#include <map>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -47,12 +52,14 @@ struct Api {
                               uint16_t*, int, void*);
   int (*layer_set_profiling)(gptoss_moe_layer*, int);
   int (*layer_profile_read)(gptoss_moe_layer*, float*, float*, float*, float*, int*);
+  int (*layer_profile_records)(gptoss_moe_layer*, gptoss_moe_prof_record*, int, int*);
   int (*checkpoint_open)(const char*, gptoss_checkpoint**);
   void (*checkpoint_close)(gptoss_checkpoint*);
   int (*checkpoint_find)(const gptoss_checkpoint*, const char*, gptoss_tensor_info*);
   int (*stack_create)(const gptoss_moe_config*, int, const gptoss_checkpoint*, int, int, gptoss_moe_stack**);
   int (*stack_io)(gptoss_moe_stack*, uint16_t**, uint16_t**, int*, int*);
   int (*stack_bind)(gptoss_moe_stack*, uint16_t*, uint16_t*);
+  int (*stack_layer)(gptoss_moe_stack*, int, gptoss_moe_layer**);
   int (*stack_decode_step)(gptoss_moe_stack*, int, gptoss_layer_hook, void*, int, void*);
   void (*stack_destroy)(gptoss_moe_stack*);
 };
@@ -79,12 +86,14 @@ void load_library(const std::string& path) {
   resolve(h, api.layer_forward_routed, "gptoss_moe_layer_forward_routed");
   resolve(h, api.layer_set_profiling, "gptoss_moe_layer_set_profiling");
   resolve(h, api.layer_profile_read, "gptoss_moe_layer_profile_read");
+  resolve(h, api.layer_profile_records, "gptoss_moe_layer_profile_records");
   resolve(h, api.checkpoint_open, "gptoss_checkpoint_open");
   resolve(h, api.checkpoint_close, "gptoss_checkpoint_close");
   resolve(h, api.checkpoint_find, "gptoss_checkpoint_find");
   resolve(h, api.stack_create, "gptoss_moe_stack_create");
   resolve(h, api.stack_io, "gptoss_moe_stack_io");
   resolve(h, api.stack_bind, "gptoss_moe_stack_bind");
+  resolve(h, api.stack_layer, "gptoss_moe_stack_layer");
   resolve(h, api.stack_decode_step, "gptoss_moe_stack_decode_step");
   resolve(h, api.stack_destroy, "gptoss_moe_stack_destroy");
   if (api.abi_version() != GPTOSS_MOE_ABI_VERSION)
@@ -207,6 +216,161 @@ gptoss_moe_config make_config(int E, int H, int I, int max_tokens, int top_k, in
   return c;
 }
 
+// ---- the module-level profiler (bindings.cpp:421-439, profiler.cu) -------
+// The reference records a HIP event pair per PROF region of the engine and
+// writes them as a Chrome trace or a summary per (category, name).  Here the
+// regions are the MoE launches of every live MoELayer and engine layer: each
+// registers its layer handles, profiler_reset(max_forwards) arms per-launch
+// timing on all of them (and on layers created later) and clears what was
+// recorded, and the save functions read the records back through the C ABI.
+// Launch i of a forward is "moe_route" (the plan for forward_routed),
+// "moe_gate_up", "moe_down" or "moe_combine", in category "moe_decode" or
+// "moe_prefill" (grouped kernels).
+struct ProfSource {
+  gptoss_moe_layer* h;
+  int layer;
+  int device;
+};
+std::mutex g_prof_mu;
+std::map<const void*, std::vector<ProfSource>> g_prof_sources;  // owner -> its layers
+int g_prof_forwards = 0;                                         // armed capacity per layer; 0: off
+
+void prof_register(const void* owner, std::vector<ProfSource> layers) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (g_prof_forwards > 0)
+    for (const ProfSource& p : layers) (void)api.layer_set_profiling(p.h, g_prof_forwards);
+  g_prof_sources[owner] = std::move(layers);
+}
+
+void prof_unregister(const void* owner) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_sources.erase(owner);
+}
+
+struct ProfEvent {
+  const char* name;
+  const char* category;
+  int device, layer;
+  double ts_us;  // host-clock start
+  float dur_ms;
+};
+
+constexpr const char* kLaunchNames[4] = {"moe_route", "moe_gate_up", "moe_down", "moe_combine"};
+
+// Every recorded launch of every registered layer (waits for their events).
+std::vector<ProfEvent> prof_collect() {
+  std::vector<ProfEvent> ev;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  for (const auto& kv : g_prof_sources)
+    for (const ProfSource& p : kv.second) {
+      int n = 0;
+      if (api.layer_profile_records(p.h, nullptr, 0, &n) != GPTOSS_OK || n <= 0) continue;
+      std::vector<gptoss_moe_prof_record> r(static_cast<size_t>(n));
+      if (api.layer_profile_records(p.h, r.data(), n, &n) != GPTOSS_OK) continue;
+      for (const gptoss_moe_prof_record& f : r)
+        for (int i = 0; i < 4; ++i)
+          ev.push_back({kLaunchNames[i], f.prefill ? "moe_prefill" : "moe_decode", p.device, p.layer,
+                        f.host_us + 1000.0 * f.start_ms[i], f.dur_ms[i]});
+    }
+  std::sort(ev.begin(), ev.end(), [](const ProfEvent& a, const ProfEvent& b) { return a.ts_us < b.ts_us; });
+  return ev;
+}
+
+void profiler_reset(int max_forwards) {
+  if (max_forwards < 0) throw py::value_error("max_forwards must be non-negative");
+  py::gil_scoped_release nogil;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_forwards = max_forwards;
+  for (const auto& kv : g_prof_sources)
+    for (const ProfSource& p : kv.second) (void)api.layer_set_profiling(p.h, max_forwards);
+}
+
+// profiler_save_chrome_trace (profiler.cu:215-270): one "X" event per launch,
+// named L<layer>/<launch>, on thread <device>, with ts relative to the first.
+void profiler_save_trace(const std::string& path) {
+  std::vector<ProfEvent> ev;
+  {
+    py::gil_scoped_release nogil;
+    ev = prof_collect();
+  }
+  FILE* f = std::fopen(path.c_str(), "w");
+  if (f == nullptr) {
+    std::fprintf(stderr, "profiler: cannot open %s for writing\n", path.c_str());
+    return;
+  }
+  const double base = ev.empty() ? 0.0 : ev.front().ts_us;
+  std::fprintf(f, "{\"traceEvents\":[\n");
+  std::vector<int> devs;
+  for (const ProfEvent& e : ev)
+    if (std::find(devs.begin(), devs.end(), e.device) == devs.end()) devs.push_back(e.device);
+  std::sort(devs.begin(), devs.end());
+  for (int d : devs)
+    std::fprintf(f, "{\"name\":\"thread_name\",\"ph\":\"M\",\"pid\":0,\"tid\":%d,\"args\":{\"name\":\"GPU %d\"}},\n", d,
+                 d);
+  for (size_t i = 0; i < ev.size(); ++i) {
+    const ProfEvent& e = ev[i];
+    long long dur = static_cast<long long>(e.dur_ms * 1000.0f);
+    if (dur < 1) dur = 1;
+    std::fprintf(f,
+                 "{\"name\":\"L%d/%s\",\"cat\":\"%s\",\"ph\":\"X\",\"ts\":%lld,\"dur\":%lld,\"pid\":0,\"tid\":%d,"
+                 "\"args\":{\"layer\":%d,\"dur_ms\":%.4f}}%s\n",
+                 e.layer, e.name, e.category, static_cast<long long>(e.ts_us - base), dur, e.device, e.layer,
+                 e.dur_ms, i + 1 < ev.size() ? "," : "");
+  }
+  std::fprintf(f, "]}\n");
+  std::fclose(f);
+  std::fprintf(stderr, "profiler: wrote %zu events to %s\n", ev.size(), path.c_str());
+}
+
+// profiler_save_summary_json (profiler.cu:276-360): per (category, name) the
+// count, total, average, minimum and maximum milliseconds and the share of
+// the total, sorted by total descending.
+void profiler_save_summary(const std::string& path) {
+  std::vector<ProfEvent> ev;
+  {
+    py::gil_scoped_release nogil;
+    ev = prof_collect();
+  }
+  struct Agg {
+    std::string name, category;
+    int count = 0;
+    double total = 0, mn = 1e30, mx = 0;
+  };
+  std::vector<Agg> agg;
+  double all = 0;
+  for (const ProfEvent& e : ev) {
+    auto it = std::find_if(agg.begin(), agg.end(),
+                           [&](const Agg& a) { return a.name == e.name && a.category == e.category; });
+    if (it == agg.end()) {
+      agg.push_back(Agg{e.name, e.category});
+      it = agg.end() - 1;
+    }
+    it->count += 1;
+    it->total += e.dur_ms;
+    it->mn = std::min(it->mn, static_cast<double>(e.dur_ms));
+    it->mx = std::max(it->mx, static_cast<double>(e.dur_ms));
+    all += e.dur_ms;
+  }
+  std::sort(agg.begin(), agg.end(), [](const Agg& a, const Agg& b) { return a.total > b.total; });
+  FILE* f = std::fopen(path.c_str(), "w");
+  if (f == nullptr) {
+    std::fprintf(stderr, "profiler: cannot open %s for writing\n", path.c_str());
+    return;
+  }
+  std::fprintf(f, "{\n  \"total_events\": %zu,\n  \"total_ms\": %.4f,\n  \"kernels\": [\n", ev.size(), all);
+  for (size_t i = 0; i < agg.size(); ++i) {
+    const Agg& a = agg[i];
+    std::fprintf(f,
+                 "    {\"name\":\"%s\",\"category\":\"%s\",\"count\":%d,\"total_ms\":%.4f,\"avg_ms\":%.4f,"
+                 "\"min_ms\":%.4f,\"max_ms\":%.4f,\"pct\":%.2f}%s\n",
+                 a.name.c_str(), a.category.c_str(), a.count, a.total, a.total / a.count, a.mn, a.mx,
+                 all > 0 ? 100.0 * a.total / all : 0.0, i + 1 < agg.size() ? "," : "");
+  }
+  std::fprintf(f, "  ]\n}\n");
+  std::fclose(f);
+  std::fprintf(stderr, "profiler: wrote summary (%zu kernels) to %s\n", agg.size(), path.c_str());
+}
+
 // ---- MoELayer: the operator of one layer -----------------------------------
 class PyMoELayer {
  public:
@@ -230,6 +394,7 @@ class PyMoELayer {
       h_ = nullptr;
       raise(s, "MoELayer init");
     }
+    prof_register(this, {ProfSource{h_, layer, device}});
   }
   ~PyMoELayer() { close(); }
   PyMoELayer(const PyMoELayer&) = delete;
@@ -238,6 +403,7 @@ class PyMoELayer {
   void close() {
     if (h_) {
       py::gil_scoped_release nogil;
+      prof_unregister(this);
       api.layer_destroy(h_);
       h_ = nullptr;
     }
@@ -380,6 +546,12 @@ class PyInferenceEngine {
     cfg_ = cfg;
     device_ = device;
     num_layers_ = n;
+    std::vector<ProfSource> layers;
+    for (int l = 0; l < n; ++l) {
+      gptoss_moe_layer* h = nullptr;
+      if (api.stack_layer(stack_, l, &h) == GPTOSS_OK && h != nullptr) layers.push_back(ProfSource{h, l, device});
+    }
+    prof_register(this, std::move(layers));
   }
 
   bool is_initialized() const { return stack_ != nullptr; }
@@ -448,6 +620,7 @@ class PyInferenceEngine {
   }
   void shutdown_impl() {
     if (stack_ != nullptr) {
+      prof_unregister(this);
       api.stack_destroy(stack_);
       stack_ = nullptr;
     }
@@ -591,8 +764,16 @@ PYBIND11_MODULE(gptoss, m) {
         return "<gptoss.ModelConfig layers=36 hidden=2880 q_heads=64 kv_heads=8 experts=128 active=4 vocab=201088>";
       });
 
-  // Per-launch timing is always compiled in (MoELayer.set_profiling / profile_read).
+  // Per-launch timing is always compiled in: the reference's profiler functions
+  // (bindings.cpp:421-439) exist whenever profiler_enabled() returns True.
   m.def("profiler_enabled", []() { return true; }, "Returns True: per-launch timing is built in.");
+  m.def("profiler_reset", &profiler_reset, py::arg("max_forwards") = 1024,
+        "Clear all profiler records and time the MoE launches of the next max_forwards forwards of every layer "
+        "(0 stops recording). Recording starts here; forwards replayed from a hipGraph are not timed.");
+  m.def("profiler_save_trace", &profiler_save_trace, py::arg("path"),
+        "Save the recorded MoE launches to Chrome Trace Format JSON.");
+  m.def("profiler_save_summary", &profiler_save_summary, py::arg("path"),
+        "Save aggregated launch timing (per category and name) to JSON.");
   m.attr("__version__") = "0.1.0";
   m.attr("MODEL_NAME") = "gpt-oss-120b";
   m.attr("ABI_VERSION") = GPTOSS_MOE_ABI_VERSION;

@@ -7,6 +7,7 @@
 // the host, so a forward can be captured in a hipGraph.
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -298,6 +299,8 @@ struct gptoss_moe_layer {
   bool trace_gu = false;
   // per-launch timing (gptoss_moe_layer_set_profiling): 4 events per recorded forward
   std::vector<hipEvent_t> prof_events;
+  std::vector<double> prof_host_us;  // host steady-clock time at which each recorded forward was enqueued
+  std::vector<int> prof_tokens;      // and its token count
   int prof_capacity = 0;
   int prof_count = 0;
 
@@ -472,7 +475,12 @@ static int layer_init(gptoss_moe_layer* L, const gptoss_moe_config* cfg, int dev
   L->special1 = static_cast<int32_t*>(p);
   if ((rc = L->alloc(&p, E * 4, "special2")) != GPTOSS_OK) return (L->release(), rc);
   L->special2 = static_cast<int32_t*>(p);
-  hipError_t err = hipMemset(L->sc.gqueue, 0, grouped_queue_ints() * 4);
+  // The work queue at the workspace's start reads zero between forwards.  A
+  // shared workspace may have another layer's forward in flight on any stream
+  // of the device: wait for all of it before zeroing, so the zeroing never
+  // lands inside a running grouped launch.
+  hipError_t err = hipDeviceSynchronize();
+  if (err == hipSuccess) err = hipMemset(L->sc.gqueue, 0, grouped_queue_ints() * 4);
   if (err == hipSuccess) err = launch_special_scan(L->w1s, 2 * I, H, E, L->special1, nullptr);
   if (err == hipSuccess) err = launch_special_scan(L->w2s, H, I, E, L->special2, nullptr);
   if (err == hipSuccess) err = hipDeviceGetAttribute(&L->num_cus, hipDeviceAttributeMultiprocessorCount, device_id);
@@ -588,7 +596,7 @@ static Scratch layer_scratch(const gptoss_moe_layer* L) {
 // w: routing weights [T][k].
 static int layer_experts(gptoss_moe_layer* L, const Scratch& S, const uint16_t* normed, const uint16_t* residual,
                          const float* w, uint16_t* out, int T, hipStream_t s, const ProfForward& pf,
-                         bool route_in_w1 = false) {
+                         bool own_routing, bool route_in_w1 = false) {
   const gptoss_moe_config& c = L->cfg;
   ExpertArgs ea{};
   ea.x = normed;
@@ -617,6 +625,7 @@ static int layer_experts(gptoss_moe_layer* L, const Scratch& S, const uint16_t* 
   ea.special2 = L->special2;
   ea.special_any1 = L->special_any1;
   ea.special_any2 = L->special_any2;
+  ea.distinct_slots = own_routing ? 1 : 0;
   ea.num_cus = L->num_cus;
   for (int i = 0; i < 6; ++i) ea.mc_shape[i] = L->mc_shape[i];
   if (route_in_w1) {  // the gate_up launch selects the experts from the router's logits
@@ -691,12 +700,18 @@ static int layer_experts(gptoss_moe_layer* L, const Scratch& S, const uint16_t* 
 
 // Forwards being captured into a graph are not timed (events inside a graph
 // cannot be timed on this runtime) and leave the profiling slots unused.
-static ProfForward next_prof(gptoss_moe_layer* L, hipStream_t s) {
+static ProfForward next_prof(gptoss_moe_layer* L, hipStream_t s, int T) {
   ProfForward pf;
   if (L->prof_count < L->prof_capacity) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     const bool capturing = hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
-    if (!capturing) pf.ev = &L->prof_events[kProfEvents * static_cast<size_t>(L->prof_count++)];
+    if (!capturing) {
+      const int i = L->prof_count++;
+      pf.ev = &L->prof_events[kProfEvents * static_cast<size_t>(i)];
+      L->prof_host_us[i] = std::chrono::duration<double, std::micro>(
+                               std::chrono::steady_clock::now().time_since_epoch()).count();
+      L->prof_tokens[i] = T;
+    }
   }
   return pf;
 }
@@ -735,11 +750,11 @@ static int layer_forward_core(gptoss_moe_layer* L, const Scratch& S, const uint1
                            decode_route_in_w1(T, c.top_k, c.num_experts, c.hidden_size, c.intermediate_size,
                                               L->mc_shape);
   ra.logits_only = route_in_w1 ? 1 : 0;
-  const ProfForward pf = next_prof(L, s);
+  const ProfForward pf = next_prof(L, s, T);
   ra.timer = pf.timer(0);
   HIP_TRY(launch_route(ra, s), "route launch");
-  if (delta != nullptr) return layer_experts(L, S, S.normed, sum_out, S.w, out, T, s, pf, route_in_w1);
-  return layer_experts(L, S, normed, residual, S.w, out, T, s, pf, route_in_w1);
+  if (delta != nullptr) return layer_experts(L, S, S.normed, sum_out, S.w, out, T, s, pf, true, route_in_w1);
+  return layer_experts(L, S, normed, residual, S.w, out, T, s, pf, true, route_in_w1);
 }
 
 static int check_forward_args(gptoss_moe_layer* L, const void* in, const void* out, int T) {
@@ -811,10 +826,10 @@ int gptoss_moe_layer_forward_routed(gptoss_moe_layer* L, const uint16_t* normed,
   if (sd.err != hipSuccess) return hip_fail(sd.err, "hipSetDevice");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const gptoss_moe_config& c = L->cfg;
-  const ProfForward pf = next_prof(L, s);
+  const ProfForward pf = next_prof(L, s, T);
   const Scratch S = layer_scratch(L);
   HIP_TRY(launch_plan(idx, T, c.top_k, c.num_experts, S.plan(), s, pf.timer(0)), "plan launch");
-  return layer_experts(L, S, normed, residual, w, out, T, s, pf);
+  return layer_experts(L, S, normed, residual, w, out, T, s, pf, false);
 }
 
 int gptoss_moe_layer_forward_prenormed_noalloc(gptoss_moe_layer* L, const uint16_t* normed, const uint16_t* residual,
@@ -898,6 +913,10 @@ int gptoss_moe_layer_set_profiling(gptoss_moe_layer* L, int max_forwards) {
   ScopedDevice sd(L->device);
   for (hipEvent_t e : L->prof_events) (void)hipEventDestroy(e);
   L->prof_events.assign(kProfEvents * static_cast<size_t>(max_forwards), nullptr);
+  L->prof_host_us.assign(static_cast<size_t>(max_forwards), 0.0);
+  L->prof_tokens.assign(static_cast<size_t>(max_forwards), 0);
+  L->prof_capacity = 0;
+  L->prof_count = 0;
   for (auto& e : L->prof_events) HIP_TRY(hipEventCreate(&e), "hipEventCreate");
   L->prof_capacity = max_forwards;
   L->prof_count = 0;
@@ -923,6 +942,30 @@ int gptoss_moe_layer_profile_read(gptoss_moe_layer* L, float* route_ms, float* w
   if (w2_ms) *w2_ms = static_cast<float>(sum[2]);
   if (combine_ms) *combine_ms = static_cast<float>(sum[3]);
   if (n_forwards) *n_forwards = L->prof_count;
+  return ok();
+}
+
+int gptoss_moe_layer_profile_records(gptoss_moe_layer* L, gptoss_moe_prof_record* records, int capacity,
+                                     int* n_records) {
+  if (L == nullptr || !L->initialized) return fail(GPTOSS_ERR_STATE, "layer not initialised");
+  if (capacity < 0 || (capacity > 0 && records == nullptr))
+    return fail(GPTOSS_ERR_INVALID, "records: capacity=%d with %s buffer", capacity, records ? "a" : "no");
+  ScopedDevice sd(L->device);
+  const int n = L->prof_count < capacity ? L->prof_count : capacity;
+  const gptoss_moe_config& c = L->cfg;
+  for (int i = 0; i < n; ++i) {
+    hipEvent_t* ev = &L->prof_events[kProfEvents * static_cast<size_t>(i)];
+    HIP_TRY(hipEventSynchronize(ev[kProfEvents - 1]), "hipEventSynchronize");
+    gptoss_moe_prof_record& r = records[i];
+    r.host_us = L->prof_host_us[i];
+    r.num_tokens = L->prof_tokens[i];
+    r.prefill = c.prefill_min_tokens > 0 && r.num_tokens >= c.prefill_min_tokens ? 1 : 0;
+    for (int j = 0; j < 4; ++j) {
+      HIP_TRY(hipEventElapsedTime(&r.start_ms[j], ev[0], ev[2 * j]), "hipEventElapsedTime");
+      HIP_TRY(hipEventElapsedTime(&r.dur_ms[j], ev[2 * j], ev[2 * j + 1]), "hipEventElapsedTime");
+    }
+  }
+  if (n_records) *n_records = L->prof_count;
   return ok();
 }
 

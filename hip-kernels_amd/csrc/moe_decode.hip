@@ -773,9 +773,11 @@ hipError_t launch_mc(const ExpertArgs& a, bool gated, hipStream_t s) {
   if (gated ? a.special_any1 : a.special_any2)  // weights with e8m0 code 0 or 255: the checking variant
     return gated ? launch_mc_t<true, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s, a.timer)
                  : launch_mc_t<false, 1, 1, 1, true, 0>(p, max_items, a.num_cus, s, a.timer);
-  // down at one or two tokens (at most 2 slots per expert): the default
-  // shapes with staged operands
-  if (!gated && a.T <= 2 && g.nb == kNbGptOss && NC == 1 && P == 3) {
+  // down at one or two tokens whose experts are distinct (so at most 2 slots
+  // per expert: the staged rows cover columns 0 and 1 only): the default
+  // shapes with staged operands.  Caller-given indices may repeat an expert
+  // within a token and take the per-lane B loads.
+  if (!gated && a.T <= 2 && a.distinct_slots && g.nb == kNbGptOss && NC == 1 && P == 3) {
     if (D == 10) return launch_mc_t<false, 3, 10, 1, false, 30, false, 2>(p, max_items, a.num_cus, s, a.timer);
     if (D == 5) return launch_mc_t<false, 3, 5, 1, false, 30, false, 2>(p, max_items, a.num_cus, s, a.timer);
   }

@@ -157,6 +157,8 @@ struct ExpertArgs {
   const int32_t* special1;    // [E] W1 scales hold code 0 or 255 (launch_special_scan), or null
   const int32_t* special2;    // [E] same for W2
   int special_any1, special_any2;  // any flag set (read back at layer init)
+  int distinct_slots;         // 1: each token's k experts are distinct (this library's top-k), so an
+                              // expert holds at most T slots; 0: caller-given indices, unchecked
   int num_cus;                // compute units of the device (persistent grid size)
   int mc_shape[6];            // {P, D, NC} launch shape overrides of gate_up, then down; 0 = automatic
   KernelTimer timer;          // of the next launch_w1* / launch_w2* / launch_combine_slots

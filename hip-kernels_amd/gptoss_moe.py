@@ -80,6 +80,11 @@ class TensorInfo(ctypes.Structure):
                 ("shape", ctypes.c_int64 * 8), ("nbytes", ctypes.c_uint64), ("data", _P), ("shard", _I)]
 
 
+class ProfRecord(ctypes.Structure):
+    _fields_ = [("host_us", ctypes.c_double), ("num_tokens", _I), ("prefill", _I),
+                ("start_ms", _F * 4), ("dur_ms", _F * 4)]
+
+
 def _sig(name, args, res=_I):
     f = getattr(_lib, name)
     f.argtypes = args
@@ -125,6 +130,7 @@ _sig("gptoss_moe_layer_set_trace_gate_up", [_P, _I])
 _sig("gptoss_moe_layer_set_profiling", [_P, _I])
 _sig("gptoss_moe_layer_profile_read", [_P, ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_F),
                                         ctypes.POINTER(_F), ctypes.POINTER(_I)])
+_sig("gptoss_moe_layer_profile_records", [_P, ctypes.POINTER(ProfRecord), _I, ctypes.POINTER(_I)])
 _sig("gptoss_moe_route_scratch_bytes", [_I, _I, _I], _SZ)
 _sig("gptoss_moe_route", [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P])
 _sig("gptoss_topk_softmax_forward", [_P, _I, _P, _P, _P, _I, _I, _I, _P])
@@ -413,6 +419,16 @@ class MoELayer:
         check(_lib.gptoss_moe_layer_profile_read(self._h, ctypes.byref(r), ctypes.byref(a), ctypes.byref(b),
                                                  ctypes.byref(c), ctypes.byref(n)))
         return r.value, a.value, b.value, c.value, n.value
+
+    def profile_records(self):
+        """Per recorded forward: dict(host_us, num_tokens, prefill, start_ms[4],
+        dur_ms[4]) for the route (or plan), gate_up, down and combine launches."""
+        n = _I()
+        check(_lib.gptoss_moe_layer_profile_records(self._h, None, 0, ctypes.byref(n)))
+        recs = (ProfRecord * max(n.value, 1))()
+        check(_lib.gptoss_moe_layer_profile_records(self._h, recs, n.value, ctypes.byref(n)))
+        return [dict(host_us=r.host_us, num_tokens=r.num_tokens, prefill=r.prefill,
+                     start_ms=list(r.start_ms), dur_ms=list(r.dur_ms)) for r in recs[:n.value]]
 
     def trace(self) -> Trace:
         t = MoeTrace()

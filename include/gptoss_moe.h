@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GPTOSS_MOE_ABI_VERSION 6
+#define GPTOSS_MOE_ABI_VERSION 7
 
 enum {
   GPTOSS_OK = 0,
@@ -141,8 +141,11 @@ size_t gptoss_moe_layer_workspace_bytes(const gptoss_moe_config* cfg);
  * forwards are ordered on one stream may share one workspace, whatever their
  * configs (each needs the bytes of its own); forwards that can overlap in time
  * need separate workspaces.  The first 1152 bytes hold a work queue that must
- * read zero whenever no forward is running: init zeroes it and every forward
- * leaves it zero, so nothing else may write there.  The workspace must
+ * read zero whenever no forward is running: init zeroes it (after waiting for
+ * all work already queued on the device, so a forward in flight on another
+ * stream is not disturbed) and every forward leaves it zero, so nothing else
+ * may write there; a forward enqueued on it by another host thread while an
+ * init runs races with that zeroing.  The workspace must
  * outlive the layer; a trace (gptoss_moe_layer_trace) then shows the last
  * forward of any layer on it. */
 int gptoss_moe_layer_init_with_workspace(gptoss_moe_layer* layer, const gptoss_moe_config* cfg, int device_id,
@@ -326,6 +329,24 @@ int gptoss_moe_layer_set_trace_gate_up(gptoss_moe_layer* layer, int enable);
 int gptoss_moe_layer_set_profiling(gptoss_moe_layer* layer, int max_forwards);
 int gptoss_moe_layer_profile_read(gptoss_moe_layer* layer, float* route_ms, float* w1_ms,
                                   float* w2_ms, float* combine_ms, int* n_forwards);
+/* One recorded forward, for per-launch traces and summaries (the records
+ * behind the reference's profiler_save_chrome_trace / _summary_json,
+ * src/engine/profiler.cu:215-360): host_us is the host steady-clock time
+ * (microseconds) at which the forward was enqueued; launch i (0 route, or the
+ * plan for forward_routed; 1 gate_up; 2 down; 3 combine) started start_ms[i]
+ * after launch 0 and ran dur_ms[i]. */
+typedef struct gptoss_moe_prof_record {
+  double host_us;
+  int num_tokens;
+  int prefill;       /* 1: the grouped prefill kernels ran (num_tokens >= prefill_min_tokens) */
+  float start_ms[4];
+  float dur_ms[4];
+} gptoss_moe_prof_record;
+/* Waits for the events of the first min(capacity, recorded) forwards since the
+ * last set_profiling and writes their records; *n_records (may be NULL) gets
+ * the number recorded. */
+int gptoss_moe_layer_profile_records(gptoss_moe_layer* layer, gptoss_moe_prof_record* records,
+                                     int capacity, int* n_records);
 
 /* ---- Stage entry points (the reference's kernel launchers) --------------- */
 

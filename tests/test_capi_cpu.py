@@ -32,7 +32,7 @@ def test_exports_every_declared_symbol(g):
 
 
 def test_abi_version_and_defaults(g):
-    assert g.lib.gptoss_abi_version() == 6
+    assert g.lib.gptoss_abi_version() == 7
     cfg = g.default_config(128, 64)
     assert (cfg.hidden_size, cfg.num_experts, cfg.top_k, cfg.intermediate_size) == (2880, 128, 4, 2880)
     assert abs(cfg.swiglu_alpha - 1.702) < 1e-6 and cfg.swiglu_limit == 7.0

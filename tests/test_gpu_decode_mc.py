@@ -142,9 +142,9 @@ def test_mc_gptoss120b_decode(gpu, orc, torch_mod, pair120, T):
     x, res = moe_data.make_tokens(700 + T, T, H120)
     say("120B matrix-core decode T", T)
     out_mc, out_ex = _stagewise_vs_exact(gpu, orc, torch, ex, mc, x, res, T, f"120B mc T={T}")
-    ref = orc.moe_forward(w, x[:1], res[:1], E120, K120, H120, I120)
-    assert np.array_equal(out_ex[:1], ref)
-    check_layer_out(out_mc[:1], ref, f"120B mc T={T} token 0 vs oracle")
+    ref = orc.moe_forward(w, x, res, E120, K120, H120, I120)  # every token
+    assert np.array_equal(out_ex, ref)
+    check_layer_out(out_mc, ref, f"120B mc T={T} all tokens vs oracle")
     out2 = host(mc.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
     assert np.array_equal(out_mc, out2)  # run-to-run deterministic
 
@@ -222,6 +222,26 @@ def test_mc_special_scales(gpu, orc, torch_mod):
     c = moe_data.mfma_stats(out_mc, out_ex)
     say("mc special out", c)
     assert c["nan_ok"] and c["inf_ok"]
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_mc_repeated_expert_in_token(gpu, orc, torch_mod, pair120, T):
+    """forward_routed with an expert repeated within a token (three slots of
+    one expert at one token, four over two tokens): the one- and two-token
+    down launch stages the input rows of two slots per expert only, so such
+    a routing takes the per-lane loads and every slot's output is its own.
+    Checked against the exact path and the oracle."""
+    torch = torch_mod
+    w, ex, mc = pair120
+    idx = np.array([[3, 3, 3, 9], [3, 9, 9, 3]], np.int32)[:T]
+    wt = np.array([[0.4, 0.3, 0.2, 0.1], [0.1, 0.2, 0.3, 0.4]], np.float32)[:T]
+    x, res = moe_data.make_tokens(880 + T, T, H120)
+    dx, dr, di, dw = dev(x, torch), dev(res, torch), dev(idx, torch), dev(wt, torch)
+    out_mc = host(mc.layer.forward_routed(dx, di, dw, residual=dr))
+    out_ex = host(ex.layer.forward_routed(dx, di, dw, residual=dr))
+    ref = orc.moe_forward_routed(w, x, res, idx, wt, E120, K120, H120, I120)
+    assert np.array_equal(out_ex, ref)
+    check_layer_out(out_mc, ref, f"mc repeated expert T={T} vs oracle")
 
 
 @pytest.mark.parametrize("T", [1, 8])

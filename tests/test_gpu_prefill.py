@@ -38,7 +38,7 @@ MEAN_REL_TOL = 1e-3
 FLIP_FRAC = 2e-3        # fraction of single-rounding values allowed to differ
 REORDER_ABS = 2.0 ** -9  # fp32 reordering allowance beyond one bf16 step
 OUT_OVER_FRAC = 2e-3    # fraction of layer outputs allowed past 2e-2 (whole-step moves)
-ROW_STEPS = 4.0         # and by how much: bf16 steps at the token's largest output
+ROW_STEPS = 1.0         # and by how much: bf16 steps at the token's largest output (measured <= 1.0)
 # The block-scaled product (prefill_block_scaled = 1) sums each group of 8
 # products aligned to the group's largest, about 14 bits below it (measured on
 # gfx950), not in fp32: more single-rounding values land one step away.

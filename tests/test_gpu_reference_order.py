@@ -12,10 +12,12 @@ in for hipBLASLt's own (not vendored, so not restated).
 Both decode paths of this build (the matrix-core default and the exact
 kernels) are measured against it at BASELINE config 0 (E=32, T=1) and config
 2 (E=128, B=1 and B=8).  Asserted: expert indices and routing weights bit-exact
-and mean-rel <= 1e-3.  Reported, not asserted: max-abs
-and the fraction of outputs beyond 2e-2, which at these output magnitudes
-(|out| up to ~140, one bf16 step 0.125-0.5) count the outputs whose bf16
-rounding lands one step away in another summation order.
+and mean-rel <= 1e-3; no output further than one bf16
+step of its token's largest output, and at most 2 % of outputs beyond 2e-2
+(measured <= 1.2 %).  At these output magnitudes (|out| up to ~140, one bf16
+step 0.125-0.5) the outputs beyond 2e-2 are those whose bf16 rounding lands
+one step away in another summation order, so max-abs itself is reported, not
+asserted.
 """
 import numpy as np
 import pytest
@@ -26,6 +28,8 @@ from test_gpu_parity import DeviceLayer, _trace_arrays, dev, host, say
 pytestmark = pytest.mark.gpu
 
 MEAN_REL_TOL = 1e-3
+ROW_STEPS = 1.0
+OVER_FRAC = 2e-2
 H = I = 2880
 K_TOP = 4
 
@@ -56,7 +60,7 @@ def layer120(gpu, torch_mod):
 
 def _stats(got, ref):
     c = moe_data.mfma_stats(got, ref)
-    return {k: c[k] for k in ("max_abs", "mean_rel", "mismatch_frac", "over_abs_frac", "max_ulps")}
+    return {k: c[k] for k in ("max_abs", "mean_rel", "mismatch_frac", "over_abs_frac", "max_ulps", "row_steps")}
 
 
 @pytest.mark.parametrize("E,T", [(32, 1), (128, 1), (128, 8)])
@@ -79,5 +83,9 @@ def test_decode_vs_reference_order(gpu, orc, torch_mod, layer20, layer120, E, T)
         say(f"E={E} T={T} {name} path vs reference order", s_r)
         say(f"E={E} T={T} {name} path vs canonical order", s_c)
         assert s_r["mean_rel"] <= MEAN_REL_TOL, (name, s_r)
+        # whole-step moves only: at most one bf16 step of the token's largest
+        # output, on a bounded fraction of outputs (measured <= 1.2 %)
+        assert s_r["row_steps"] <= ROW_STEPS, (name, s_r)
+        assert s_r["over_abs_frac"] <= OVER_FRAC, (name, s_r)
         if name == "exact":
             assert s_c["mismatch_frac"] == 0.0, s_c  # the exact kernels are the canonical order

@@ -24,7 +24,7 @@ def gptoss():
 
 def test_module_attributes_and_config(gptoss):
     assert gptoss.__version__ == "0.1.0" and gptoss.MODEL_NAME == "gpt-oss-120b"
-    assert gptoss.ABI_VERSION == 6
+    assert gptoss.ABI_VERSION == 7
     assert gptoss.profiler_enabled() is True
     C = gptoss.ModelConfig
     assert (C.num_layers, C.hidden_size, C.num_q_heads, C.num_kv_heads, C.head_dim) == (36, 2880, 64, 8, 64)
@@ -39,6 +39,25 @@ def test_module_attributes_and_config(gptoss):
     assert C().num_layers == 36 and "layers=36" in repr(C())
     with pytest.raises(AttributeError):
         C.num_layers = 3
+
+
+def test_profiler_contract_cpu(gptoss, tmp_path):
+    """bindings.cpp:421-439: with profiler_enabled() True the module has
+    profiler_save_trace, profiler_save_summary and profiler_reset; with no
+    layer recorded both files are well-formed and empty."""
+    import json
+    assert gptoss.profiler_enabled() is True
+    gptoss.profiler_reset()
+    gptoss.profiler_save_trace(str(tmp_path / "t.json"))
+    gptoss.profiler_save_summary(str(tmp_path / "s.json"))
+    assert json.load(open(tmp_path / "t.json")) == {"traceEvents": []}
+    s = json.load(open(tmp_path / "s.json"))
+    assert s["total_events"] == 0 and s["kernels"] == []
+    with pytest.raises(ValueError):
+        gptoss.profiler_reset(-1)
+    # an unwritable path is reported on stderr and does not raise (profiler.cu:221-224)
+    gptoss.profiler_save_summary(str(tmp_path / "missing_dir" / "s.json"))
+    gptoss.profiler_reset(0)
 
 
 def test_engine_errors(gptoss, tmp_path):
@@ -158,3 +177,47 @@ def test_engine_decode_step_matches_c_abi(gptoss, gpu, model):
     eng.shutdown()
     assert not eng.is_initialized
     st.destroy()
+
+
+@pytest.mark.gpu
+def test_profiler_records_moe_launches(gptoss, model, tmp_path):
+    """profiler_reset arms every live layer; the trace holds one event per
+    launch (route, gate_up, down, combine) of every eager forward, named
+    L<layer>/<launch> as the reference's trace names its regions, and the
+    summary aggregates them per (category, name)."""
+    import json
+    import torch
+    pl = gptoss.MoELayer(model, 2, max_tokens=160)
+    gptoss.profiler_reset(8)
+    for T in (1, 7, 150):
+        x, r = moe_data.make_tokens(700 + T, T, H)
+        pl.forward_prenormed(_dev(x, torch), _dev(r, torch))
+    torch.cuda.synchronize()
+    gptoss.profiler_save_trace(str(tmp_path / "trace.json"))
+    gptoss.profiler_save_summary(str(tmp_path / "summary.json"))
+    ev = [e for e in json.load(open(tmp_path / "trace.json"))["traceEvents"] if e["ph"] == "X"]
+    assert len(ev) == 12
+    names = sorted({e["name"] for e in ev})
+    assert names == ["L2/moe_combine", "L2/moe_down", "L2/moe_gate_up", "L2/moe_route"]
+    assert all(e["dur"] >= 1 and e["args"]["layer"] == 2 and e["args"]["dur_ms"] > 0 for e in ev)
+    assert sum(e["cat"] == "moe_prefill" for e in ev) == 4 and sum(e["cat"] == "moe_decode" for e in ev) == 8
+    # launches of one forward follow each other
+    ts = [e["ts"] for e in ev]
+    assert ts == sorted(ts)
+    s = json.load(open(tmp_path / "summary.json"))
+    assert s["total_events"] == 12
+    cnt = {(k["category"], k["name"]): k["count"] for k in s["kernels"]}
+    assert cnt[("moe_decode", "moe_gate_up")] == 2 and cnt[("moe_prefill", "moe_down")] == 1
+    tot = [k["total_ms"] for k in s["kernels"]]
+    assert tot == sorted(tot, reverse=True) and abs(sum(k["pct"] for k in s["kernels"]) - 100.0) < 0.1
+    for k in s["kernels"]:
+        assert k["min_ms"] <= k["avg_ms"] <= k["max_ms"]
+    # reset clears; a closed layer leaves the registry
+    gptoss.profiler_reset(8)
+    gptoss.profiler_save_summary(str(tmp_path / "empty.json"))
+    assert json.load(open(tmp_path / "empty.json"))["total_events"] == 0
+    pl.forward_prenormed(_dev(moe_data.make_tokens(9, 2, H)[0], torch))
+    pl.close()
+    gptoss.profiler_save_summary(str(tmp_path / "closed.json"))
+    assert json.load(open(tmp_path / "closed.json"))["total_events"] == 0
+    gptoss.profiler_reset(0)
