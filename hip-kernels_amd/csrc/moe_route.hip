@@ -938,7 +938,168 @@ hipError_t launch_plan_kernel(const int32_t* idx, int T, int k, int E, PlanBufs 
   return hipGetLastError();
 }
 
+// Logits on the matrix cores (many tokens; the reference routes T > 1
+// through hipBLASLt, cuda_utils.h:226-308, moe_layer.cu:1174-1185): bf16
+// products, fp32 sums in v_mfma_f32_16x16x32_bf16's order, + bias.
+//
+// A work-group computes kMmTT = 32 tokens x kMmEE = 64 experts; wave w owns
+// experts 16 w .. 16 w + 15 for all 32 tokens over the whole K, so a logit is
+// four chains of products (blocks j, j + 4, ...) in block order, added
+// pairwise, plus the bias: a token's logits depend on its own row only
+// (batch-invariant), and every run gives the same bits.  The grid
+// gives the expert slices of eight token blocks to one XCD, so a token row
+// is read from HBM once per XCD.
+//
+// K goes in chunks of kMmKB blocks (128 elements, 256 bytes of each row).
+// The work-group loads a chunk's rows (32 token rows, 64 router rows) with
+// coalesced 16-byte loads, 16 lanes per row, into a ring of kMmP chunks of
+// registers, so kMmP chunks are in flight behind the one being multiplied;
+// each chunk is written to one of two LDS stages with the 16-byte piece c of
+// row r at position c ^ (r % 16), so that the operand reads (16 rows at one
+// piece) hit distinct banks.  One barrier per chunk.  Loads past the last
+// chunk read past the buffer end (zeros, no memory access); blocks of the
+// last chunk past K are loaded but not multiplied.
+//
+// Measured on MI355X at 4096 tokens x 128 experts x 2880 (bench leg
+// `router`): 16.8 us for the logits, against 71 us for the gemv tree.  The
+// kernel is bound by what the CUs pull from L2 (553 KiB per work-group): the
+// operands loaded straight in the fragment layout (16 rows x 64 bytes per
+// load) ran at 19-21 us whatever the ring depth, and a split of K into 8
+// ranges with a second pass adding the partial sums at 20 us.
+constexpr int kMmTT = 32, kMmEE = 64, kMmKB = 4, kMmP = 4;
+constexpr int kMmRows = kMmTT + kMmEE;                 // rows of a chunk: tokens, then router rows
+constexpr int kMmRowB = kMmKB * 64;                    // bytes of a row in a chunk
+constexpr int kMmLpr = kMmRowB / 16;                   // lanes per row in a load (= pieces per row)
+constexpr int kMmRpl = kWave / kMmLpr;                 // rows per load
+constexpr int kMmLoads = kMmRows * kMmRowB / 1024 / 4;  // 16-byte loads per lane and chunk (a wave's share)
+constexpr int kMmStage = kMmRows * kMmRowB;            // bytes of a chunk in LDS
+template <bool F32>
+__global__ __launch_bounds__(kRouteThreads, 2) void logits_mfma_kernel(const uint16_t* __restrict__ x,
+                                                                       const uint16_t* __restrict__ W,
+                                                                       const uint16_t* __restrict__ bias, int T, int E,
+                                                                       int H, void* __restrict__ logits) {
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  static_assert(kMmLpr == 16 && kMmLoads * 4 * 1024 == kMmStage && kMmTT % kMmRpl == 0,
+                "16 pieces per row (the swizzle); four waves share a chunk; a load's rows are all token rows or "
+                "all router rows");
+  __shared__ __attribute__((aligned(16))) uint8_t stage[2][kMmStage];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int neh = (E + kMmEE - 1) / kMmEE;
+  const int id = static_cast<int>(blockIdx.x);
+  const int eh = (id >> 3) % neh;                  // expert slice
+  const int tb = (id / (8 * neh)) * 8 + (id & 7);  // token block: the same id % 8 (XCD) for all slices
+  const int t0 = tb * kMmTT, e0 = eh * kMmEE;
+  if (t0 >= T) return;  // the grid is rounded up to whole groups of eight token blocks
+  const int nb = H >> 5;
+  const int nch = (nb + kMmKB - 1) / kMmKB;
+  const int rowb = H * 2;  // bytes per row
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(W), 0, E * rowb, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, T * rowb, 0x00020000);
+  // The wave's loads of a chunk: load i covers chunk rows R = kMmRpl (kMmLoads w
+  // + i) + l / kMmLpr, piece l % kMmLpr of the row's kMmRowB bytes.  Rows past
+  // T / E read the last row (their sums are not stored).
+  int goff[kMmLoads], loff[kMmLoads];
+#pragma unroll
+  for (int i = 0; i < kMmLoads; ++i) {
+    const int R = kMmRpl * (kMmLoads * w + i) + lane / kMmLpr, c = lane % kMmLpr;
+    const int row = R < kMmTT ? min(t0 + R, T - 1) : min(e0 + R - kMmTT, E - 1);
+    goff[i] = row * rowb + 16 * c;
+    loff[i] = R * kMmRowB + 16 * (c ^ (R & 15));
+  }
+  uint4 ring[kMmP][kMmLoads];
+  auto load = [&](int ch, int slot) __attribute__((always_inline)) {
+    const int so = ch < nch ? ch * kMmRowB : 0x40000000;  // past the last chunk: out of range
+#pragma unroll
+    for (int i = 0; i < kMmLoads; ++i) {
+      const bool ux = kMmRpl * (kMmLoads * w + i) < kMmTT;  // wave-uniform: token rows or router rows
+      ring[slot][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ux ? xrs : wrs, goff[i], so, 0));
+    }
+  };
+  auto store = [&](int slot, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kMmLoads; ++i) *reinterpret_cast<uint4*>(stage[st] + loff[i]) = ring[slot][i];
+  };
+  // acc[f][j]: the products of blocks j, j + 4, ... (four chains per logit,
+  // summed pairwise at the end: each chain adds a quarter of the blocks, so
+  // the fp32 error of a logit is about a quarter of one chain's)
+  f32x4_t acc[2][kMmKB];
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int j = 0; j < kMmKB; ++j) acc[f][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const int r16 = lane & 15, q = lane >> 4;
+  auto compute = [&](int st, int ch) __attribute__((always_inline)) {
+    const uint8_t* sp = stage[st];
+#pragma unroll
+    for (int j = 0; j < kMmKB; ++j) {
+      if (kMmKB * ch + j >= nb) break;  // the last chunk's blocks past K
+      // piece 4 j + q of the lane's row at its swizzled position (the rows
+      // read here are 16-aligned, so the swizzle is r16)
+      const int pz = 16 * ((4 * j + q) ^ r16);
+      const gx_bf16x8 a = *reinterpret_cast<const gx_bf16x8*>(sp + (kMmTT + 16 * w + r16) * kMmRowB + pz);
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const gx_bf16x8 b = *reinterpret_cast<const gx_bf16x8*>(sp + (16 * f + r16) * kMmRowB + pz);
+        acc[f][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[f][j], 0, 0, 0);
+      }
+    }
+  };
+  // chunk 0 into stage 0; chunks 1 .. kMmP in flight
+  load(0, 0);
+  store(0, 0);
+#pragma unroll
+  for (int p = 1; p <= kMmP; ++p) load(p, p % kMmP);
+  __syncthreads();
+  for (int c0 = 0; c0 < nch; c0 += kMmP) {
+#pragma unroll
+    for (int u = 0; u < kMmP; ++u) {
+      const int c = c0 + u;  // chunk c in stage c % 2; chunk c + 1 in ring slot (c + 1) % kMmP
+      compute(u & 1, c);
+      store((u + 1) % kMmP, (u + 1) & 1);
+      load(c + 1 + kMmP, (u + 1) % kMmP);
+      __syncthreads();
+    }
+  }
+  // acc[f][j][r]: expert 16 w + 4 (l / 16) + r, token 16 f + l % 16
+  const int eb = e0 + 16 * w + 4 * q;
+  float bv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) bv[r] = bias != nullptr && eb + r < E ? bf16_to_f32(bias[eb + r]) : 0.0f;
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int t = t0 + 16 * f + r16;
+    if (t >= T) continue;
+    static_assert(kMmKB == 4, "four chains");
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = ((acc[f][0][r] + acc[f][1][r]) + (acc[f][2][r] + acc[f][3][r])) + bv[r];
+    const size_t o = static_cast<size_t>(t) * E + eb;
+    if (eb + 4 <= E && (E & 3) == 0) {
+      if constexpr (F32) *reinterpret_cast<float4*>(reinterpret_cast<float*>(logits) + o) = make_float4(v[0], v[1], v[2], v[3]);
+      else *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(logits) + o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (eb + r < E) {
+          if constexpr (F32) reinterpret_cast<float*>(logits)[o + r] = v[r];
+          else reinterpret_cast<uint16_t*>(logits)[o + r] = f32_to_bf16(v[r]);
+        }
+    }
+  }
+}
+
 constexpr int kNormFusedMaxT = 4;  // tokens up to which the residual RMSNorm runs inside the router
+// Tokens above which the router's logits come from the matrix cores; up to
+// it every logit follows the reference's gemv_bf16 tree (its T = 1 path).
+constexpr int kMmMinT = 64;
+
+// The matrix-core router applies: many tokens, whole 32-element blocks, and
+// every offset inside a 32-bit buffer range.
+bool mm_router_ok(const RouteArgs& a) {
+  return a.T > kMmMinT && a.H % 32 == 0 &&
+         static_cast<size_t>(a.T) * a.H * 2 < (size_t{1} << 30) && static_cast<size_t>(a.E) * a.H * 2 < (size_t{1} << 30);
+}
 
 template <bool F32>
 hipError_t launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t) {
@@ -973,6 +1134,11 @@ hipError_t launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t
   } else if (a.T <= 8) {
     gx_launch(logits_kernel<1, 1, 0, F32>, dim3((a.E + 3) / 4, a.T), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b,
               a.T, a.E, a.H, a.logits);
+  } else if (mm_router_ok(a)) {  // many tokens: the matrix cores
+    const int neh = (a.E + kMmEE - 1) / kMmEE, ntb = (a.T + kMmTT - 1) / kMmTT;
+    const int grid = ((ntb + 7) / 8) * 8 * neh;
+    gx_launch(logits_mfma_kernel<F32>, dim3(grid), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b, a.T, a.E, a.H,
+              a.logits);
   } else {
     const int gx = (a.E + kLdsEPW - 1) / kLdsEPW, ntb = (a.T + kLdsTT - 1) / kLdsTT;
     if (a.H <= 8 * 2 * kRouteThreads) {  // every chain holds at most two chunks: router rows held across blocks

@@ -357,7 +357,14 @@ int gptoss_moe_layer_profile_records(gptoss_moe_layer* layer, gptoss_moe_prof_re
  * bf16 logits or kept in fp32).  `scratch` is reserved: it must be non-NULL
  * (gptoss_moe_route_scratch_bytes bytes of device memory, 256 today) and is
  * neither read nor written; routing exchanges no values between
- * work-groups, so no workspace is needed. */
+ * work-groups, so no workspace is needed.
+ * Up to 64 tokens every logit follows the reference's gemv_bf16 tree (its
+ * T = 1 path, gemv_bf16.cu:57-129), bit-exact against the oracle.  Above 64
+ * (when hidden % 32 == 0) the logits come from the matrix cores: fp32 sums of
+ * exact bf16 products in the instruction's order, block by block, then the
+ * bias, as the reference's hipBLASLt path for T > 1 sums in its own order;
+ * within the fp32 error bound of the exact sum, deterministic, and
+ * independent of the other tokens in the call. */
 size_t gptoss_moe_route_scratch_bytes(int num_tokens, int num_experts, int top_k);
 int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
                      int num_tokens, int num_experts, int hidden, int top_k, int logits_fp32,

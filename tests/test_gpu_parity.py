@@ -130,15 +130,37 @@ def test_topk_softmax(gpu, orc, torch_mod, T, k, fp32):
     assert np.array_equal(host(tpe), hist)
 
 
+MM_MIN_T = 64  # above this many tokens (and H % 32 == 0) the router runs on the matrix cores
+
+
+def _mm_router_bound(orc, x, W, b):
+    """fp64 logits and the fp32 error bound of any summation order: the K
+    exact bf16 products and the bias, (K + 2) u (sum |x w| + |b|)."""
+    xf = orc.bf16_to_f32(x).astype(np.float64)
+    wf = orc.bf16_to_f32(W).astype(np.float64)
+    bf = orc.bf16_to_f32(b).astype(np.float64)
+    exact = xf @ wf.T + bf
+    mag = np.abs(xf) @ np.abs(wf).T + np.abs(bf)
+    return exact, (x.shape[1] + 2) * 2.0 ** -24 * mag
+
+
 @pytest.mark.parametrize("T,fp32,E,H", [(1, False, 128, 2880), (8, False, 128, 2880), (64, False, 128, 2880),
                                          (9, True, 128, 2880), (4096, True, 128, 2880), (100, False, 20, 512),
-                                         (300, True, 36, 4104), (130, True, 256, 2880)])
+                                         (300, True, 36, 4104), (130, True, 256, 2880), (65, True, 128, 2880),
+                                         (1000, False, 128, 2880)])
 def test_route_router_topk(gpu, orc, torch_mod, T, fp32, E, H):
-    """Router GEMV (gemv_bf16 tree) + top-k; T=4096 fp32 is BASELINE config 1:
-    logits bit-exact, indices bit-exact, weights bit-exact.  The many-token
-    cases also cover partial 8 x 8 blocks (T, E not multiples of 8), a short
-    hidden size (chains past the last chunk stay 0), three chunks per chain
-    (H = 4104) and 256 experts."""
+    """Router + top-k; T=4096 fp32 is BASELINE config 1.
+    Up to 64 tokens (and for H % 32 != 0: H = 4104, three chunks per chain)
+    the logits follow the gemv_bf16 tree bit for bit, and so do the indices
+    and weights.  Above 64 tokens they come from the matrix cores: asserted
+    within the fp32 error bound of the exact (fp64) sum, deterministic, and a
+    token's logits independent of the other tokens in the call; the indices
+    and weights are exactly the oracle's top-k softmax of those logits, and
+    against the oracle's own (tree) logits the indices differ only where
+    two candidates for the k-th place lie within the bound of each other
+    (none in these cases) with weights within 1e-6 (the config-1 bar).  The
+    many-token cases also cover partial tiles (T, E not multiples of the
+    tiles), a short hidden size and 256 experts."""
     torch = torch_mod
     k = 4
     rng = np.random.default_rng(T + E + H)
@@ -149,18 +171,50 @@ def test_route_router_topk(gpu, orc, torch_mod, T, fp32, E, H):
     logits, idx, w = gpu.route(dev(x, torch), dev(W, torch), dev(b, torch), k, logits_fp32=fp32)
     ref_l = orc.router(x, W, b, logits_fp32=fp32)
     got_l = host(logits)
-    if fp32:
-        assert np.array_equal(got_l.view(np.uint32), ref_l.view(np.uint32))
-        lf = ref_l
+    lf_ref = ref_l if fp32 else orc.bf16_to_f32(ref_l)
+    ridx, rw = orc.topk_softmax(lf_ref, k)
+    if T <= MM_MIN_T or H % 32:
+        if fp32:
+            assert np.array_equal(got_l.view(np.uint32), ref_l.view(np.uint32))
+        else:
+            assert np.array_equal(got_l, ref_l)
+        assert np.array_equal(host(idx), ridx)
+        assert np.array_equal(host(w).view(np.uint32), rw.view(np.uint32))
     else:
-        assert np.array_equal(got_l, ref_l)
-        lf = orc.bf16_to_f32(ref_l)
-    ridx, rw = orc.topk_softmax(lf, k)
-    assert np.array_equal(host(idx), ridx)
-    assert np.array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+        exact, bound = _mm_router_bound(orc, x, W, b)
+        lg = got_l.astype(np.float64) if fp32 else orc.bf16_to_f32(got_l).astype(np.float64)
+        # bf16 logits: one rounding of the fp32 value on top
+        tol = bound if fp32 else bound + np.abs(exact) * 2.0 ** -8 + 2.0 ** -133
+        err = np.abs(lg - exact)
+        say("mm router logits", dict(max_err=float(err.max()), max_err_over_bound=float((err / tol).max())))
+        assert np.all(err <= tol)
+        # selection and weights: exactly the top-k softmax of the GPU's logits
+        gidx, gw = orc.topk_softmax(lg.astype(np.float32), k)
+        assert np.array_equal(host(idx), gidx)
+        assert np.array_equal(host(w).view(np.uint32), gw.view(np.uint32))
+        # against the oracle's tree logits: a token's selection can differ
+        # only if its k-th and (k+1)-th exact logits lie within twice the bound
+        srt = np.sort(exact, axis=1)[:, ::-1]
+        tie = (srt[:, k - 1] - srt[:, k]) <= 2 * tol.max(axis=1)
+        diff = np.any(host(idx) != ridx, axis=1)
+        say("mm router vs tree selection", dict(tokens=T, near_ties=int(tie.sum()), differing=int(diff.sum())))
+        assert not np.any(diff & ~tie)
+        same = ~diff
+        if fp32:  # config 1's bar: weights within 1e-6
+            assert np.max(np.abs(host(w)[same] - rw[same]), initial=0.0) <= 1e-6
+        else:  # bf16 logits: where the selected logits are the same bits, so are the weights
+            sel_eq = np.all(np.take_along_axis(got_l, ridx, 1) == np.take_along_axis(ref_l, ridx, 1), axis=1) & same
+            assert np.array_equal(host(w)[sel_eq].view(np.uint32), rw[sel_eq].view(np.uint32))
+        # deterministic, and independent of the other tokens: the first
+        # tokens alone give the same bits
+        logits2, idx2, _ = gpu.route(dev(x, torch), dev(W, torch), dev(b, torch), k, logits_fp32=fp32)
+        assert np.array_equal(host(logits2).view(np.uint8), got_l.view(np.uint8))
+        h = max(MM_MIN_T + 1, T // 2)
+        logits3, _, _ = gpu.route(dev(x[:h], torch), dev(W, torch), dev(b, torch), k, logits_fp32=fp32)
+        assert np.array_equal(host(logits3).view(np.uint8), got_l[:h].view(np.uint8))
     # repeat: nothing carries over between calls
     logits2, idx2, w2 = gpu.route(dev(x, torch), dev(W, torch), dev(b, torch), k, logits_fp32=fp32)
-    assert np.array_equal(host(idx2), ridx)
+    assert np.array_equal(host(idx2), host(idx))
 
 
 # 6144 x 4 slots: the largest plan whose indices are staged in LDS; 8192 x 4:
