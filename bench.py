@@ -185,6 +185,51 @@ def profiled_traffic(name: str):
     return None
 
 
+def profiled_value(name: str, key: str):
+    """A `key: value` figure of a committed profiles/ summary, or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            for line in f:
+                if line.startswith(key + ":"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def bench_launch_floor(torch, kernels=(1, 4, 5), replays=50):
+    """The floor a chain of dependent launches sets: n one-wave elementwise
+    kernels (torch's add_ on 64 floats), each reading the previous one's
+    output, captured in one hipGraph and replayed back to back.  A decode
+    layer is four such dependent launches at one token (router, gate_up with
+    the routing, down, combine) and five from three tokens."""
+    res = {}
+    x = torch.zeros(64, device="cuda")
+    for n in kernels:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(n):
+                x.add_(1.0)
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(n):
+                x.add_(1.0)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / replays
+        res[str(n)] = {"us_per_graph": us, "us_per_kernel": us / n}
+    return {"dependent_kernels": res, "kernel": "torch add_ on 64 floats (one work-group)", "replays": replays}
+
+
 def copy_calibration(torch, mib: int = 256, reps: int = 4):
     """A plain device-to-device copy of `mib` MiB, `reps` times: the known-size
     workload that scales the profiler's FETCH_SIZE / WRITE_SIZE counters."""
@@ -298,7 +343,9 @@ def bench_router(g, torch, T: int = 4096, reps: int = 20):
                                             scratch=scratch), per_graph=10, replays=reps // 10 or 1)
     nbytes = T * H * 2 + E * H * 2 + E * 2 + T * E * 4 + 2 * T * K_TOP * 4
     return dict(tokens=T, logits="fp32", us=ms * 1e3, tokens_per_s=T / (ms / 1e3), algorithmic_bytes=nbytes,
-                gbs=nbytes / (ms / 1e3) / 1e9)
+                gbs=nbytes / (ms / 1e3) / 1e9,
+                logits_order="matrix cores above 64 tokens (four fp32 chains per logit, then the bias)",
+                tflops=2.0 * T * E * H / (ms / 1e3) / 1e12)
 
 
 def bench_residual(g, torch, wc, T: int, steps: int = 64):
@@ -598,7 +645,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true",
                     help="decode sweep only (skip the exact-path, prefill, router and 36-layer stack legs)")
     ap.add_argument("--stack-layers", type=int, default=36)
-    ap.add_argument("--leg", choices=("prefill", "router", "stack"),
+    ap.add_argument("--leg", choices=("prefill", "router", "stack", "floor"),
                     help="only run this leg of the bench and print its JSON (profiler runs)")
     args = ap.parse_args()
 
@@ -619,6 +666,8 @@ def main():
             res = bench_prefill(g, torch, wc)
         elif args.leg == "router":
             res = bench_router(g, torch)
+        elif args.leg == "floor":
+            res = bench_launch_floor(torch)
         else:
             res = bench_stack(g, torch, layers=args.stack_layers)
         print(json.dumps({"leg": args.leg, **res}), flush=True)
@@ -645,6 +694,16 @@ def main():
                                  "copy-calibrated)" if traffic else None,
                   algorithmic_bytes_per_launch=head["w1_algorithmic_bytes"],
                   avg_launch_us=head["kernel_us"]["w1"])
+        # the same fraction from the committed rocprofv3 kernel statistics of
+        # this workload (the events above add ~4 us of stamping per dispatch)
+        pb = profiled_value("mc_decode_b64_kernel_stats.md", "gate_up_algorithmic_bytes_per_launch")
+        pa = profiled_value("mc_decode_b64_kernel_stats.md", "rocprof_gate_up_avg_us")
+        pg = profiled_value("mc_decode_b64_kernel_stats.md", "rocprof_gate_up_graph_timed_us")
+        if headline_b == 64 and pb and pa:
+            rf["frac_rocprof"] = pb / (pa * 1e-6) / 1e9 / HBM_PEAK_GBS
+            rf["frac_rocprof_graph_replay"] = pb / (pg * 1e-6) / 1e9 / HBM_PEAK_GBS if pg else None
+            rf["rocprof_source"] = ("profiles/mc_decode_b64_kernel_stats.md (average over all dispatches; "
+                                    "graph-replayed dispatches)")
     extra = {}
     if not args.no_extra:
         # the exact (bit-identical to the oracle) decode kernels at the headline batch
@@ -672,6 +731,9 @@ def main():
         log("router + top-k T=4096 fp32 logits")
         extra["router"] = bench_router(g, torch)
         log(json.dumps(extra["router"]))
+        log("launch floor: dependent one-wave kernels in a hipGraph")
+        extra["launch_floor"] = bench_launch_floor(torch)
+        log(json.dumps(extra["launch_floor"]))
         log("residual add + RMSNorm in front of the MoE (B=1, 4, 64)")
         extra["residual_norm"] = [bench_residual(g, torch, copies[0], T) for T in (1, 4, 64)]
         log(json.dumps(extra["residual_norm"]))
