@@ -197,37 +197,39 @@ def profiled_value(name: str, key: str):
     return None
 
 
-def bench_launch_floor(torch, kernels=(1, 4, 5), replays=50):
-    """The floor a chain of dependent launches sets: n one-wave elementwise
-    kernels (torch's add_ on 64 floats), each reading the previous one's
-    output, captured in one hipGraph and replayed back to back.  A decode
-    layer is four such dependent launches at one token (router, gate_up with
-    the routing, down, combine) and five from three tokens."""
+def bench_launch_floor(torch, chain: int = 200, sizes=(64, 1 << 20)):
+    """The floor a chain of dependent launches sets: `chain` elementwise
+    kernels (torch's add_), each reading the previous one's output, captured
+    in one hipGraph and timed over one replay (after a warm one), as the
+    decode steps are.  64 floats is one work-group; 2^20 floats spreads over
+    the whole chip, as the decode launches do.  A decode layer is four
+    dependent launches at one token (router, gate_up with the routing, down,
+    combine) and five from three tokens."""
     res = {}
-    x = torch.zeros(64, device="cuda")
-    for n in kernels:
-        s = torch.cuda.Stream()
+    s = torch.cuda.Stream()
+    for n in sizes:
+        x = torch.zeros(n, device="cuda")
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            for _ in range(n):
+            for _ in range(3):
                 x.add_(1.0)
         torch.cuda.current_stream().wait_stream(s)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(n):
+        with torch.cuda.graph(graph, stream=s):
+            for _ in range(chain):
                 x.add_(1.0)
-        for _ in range(3):
-            graph.replay()
+        graph.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(replays):
+        with torch.cuda.stream(s):
+            e0.record(s)
             graph.replay()
-        e1.record()
+            e1.record(s)
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1000.0 / replays
-        res[str(n)] = {"us_per_graph": us, "us_per_kernel": us / n}
-    return {"dependent_kernels": res, "kernel": "torch add_ on 64 floats (one work-group)", "replays": replays}
+        us = e0.elapsed_time(e1) * 1000.0 / chain
+        res[str(n)] = {"us_per_kernel": us, "us_per_4": 4 * us, "us_per_5": 5 * us}
+        del graph
+    return {"dependent_kernels_by_floats": res, "kernel": "torch add_ (fp32)", "chain": chain}
 
 
 def copy_calibration(torch, mib: int = 256, reps: int = 4):

@@ -13,8 +13,12 @@
 //                      LDS transpose;
 //   topk_plan_kernel   (T <= kTopkPlanMaxT) one work-group of 16 waves selects
 //                      every token's top-k and builds the plan from LDS;
-//   topk_kernel +      (larger T) top-k spread over the device, then the plan
-//   plan_kernel        from the selections.
+//   logits_mfma_kernel (T > 64) the logits on the matrix cores, operands
+//                      staged in LDS by direct loads;
+//   topk16_kernel +    (larger T) top-k spread over the device, sixteen lanes
+//   plan_kernel        a token (topk_kernel, a wave a token, when E % 4 != 0
+//                      or the logits are unaligned), then the plan from the
+//                      selections.
 //
 // Kernel boundaries order the stages: no values cross work-groups inside a
 // launch, so there are no tickets, exchange buffers or cache maintenance.
@@ -530,6 +534,108 @@ __global__ __launch_bounds__(kRouteThreads) void topk_kernel(const void* logits,
   topk_token<NV, !F32>(v, k, variant, idx + static_cast<size_t>(t) * k, w + static_cast<size_t>(t) * k, tpe, lane);
 }
 
+// Top-k softmax of every token, kTopkGroup = 16 lanes per token (four tokens
+// a wave).  Lane g of a token holds experts 64 c + 4 g .. 64 c + 4 g + 3, one
+// 16-byte (fp32) or 8-byte (bf16) load per c.  A round takes the largest of
+// the lanes' 64-bit words select_key << 32 | ~expert (value descending, and
+// among equal values the smallest expert: the order of select_topk), which the
+// sixteen lanes agree on through four DPP exchanges (lane pairs, quads, the
+// mirrored halves of eight lanes, of sixteen); words are distinct, so the
+// winner clears itself by equality, and a round whose largest word is 0 (no
+// finite logit left) yields the padding (-FLT_MAX, -1).  The selected value
+// comes back from its key (-0 as +0, which no slot weight can tell apart:
+// both give exp(0) against either as the maximum).  Same slots as
+// topk_kernel.
+//
+// Work-group b takes 16 tokens of the 32-token block (b / 16) * 8 + b % 8,
+// half (b / 8) % 2: the block whose logits the matrix-core router kernel
+// wrote on the same XCD (b % 8), so they are read where they were written
+// (measured 1.1 us less after that kernel at 4096 tokens).  Requires E % 4 ==
+// 0, E <= 256 and logits aligned to the load width (the launcher checks).
+constexpr int kTopkGroup = 16;
+template <int Ctrl>
+__device__ __forceinline__ uint64_t max_dpp_u64(uint64_t x) {
+  const uint32_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(x)), Ctrl, 0xf, 0xf, true));
+  const uint32_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(x >> 32)), Ctrl, 0xf, 0xf, true));
+  const uint64_t y = (static_cast<uint64_t>(hi) << 32) | lo;
+  return y > x ? y : x;
+}
+
+template <bool F32, int NC>
+__global__ __launch_bounds__(kRouteThreads) void topk16_kernel(const void* logits, int T, int E, int k, int variant,
+                                                              int32_t* idx, float* w, int32_t* tpe) {
+  const int b = static_cast<int>(blockIdx.x);
+  const int tb = (b >> 4) * 8 + (b & 7);
+  const int tblk = tb * 32 + ((b >> 3) & 1) * (kRouteThreads / kTopkGroup);
+  if (tblk >= T) return;  // work-group-uniform
+  const int t = tblk + static_cast<int>(threadIdx.x) / kTopkGroup;
+  const int g = static_cast<int>(threadIdx.x) % kTopkGroup;
+  const int tl = min(t, T - 1);  // lanes of tokens past T load a real row and write nothing
+  uint64_t key[4 * NC];
+  if constexpr (F32) {
+    float4 r[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      r[c] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(logits) + static_cast<size_t>(tl) * E +
+                                              min(64 * c + 4 * g, E - 4));
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float f[4] = {r[c].x, r[c].y, r[c].z, r[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 64 * c + 4 * g + i;
+        const uint32_t sk = e < E ? select_key(sanitize_logit(f[i])) : 0u;
+        key[4 * c + i] = sk == 0u ? 0ull : (static_cast<uint64_t>(sk) << 32) | static_cast<uint32_t>(~e);
+      }
+    }
+  } else {
+    uint2 r[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      r[c] = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(logits) + static_cast<size_t>(tl) * E +
+                                             min(64 * c + 4 * g, E - 4));
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float f[4] = {__uint_as_float(r[c].x << 16), __uint_as_float(r[c].x & 0xffff0000u),
+                          __uint_as_float(r[c].y << 16), __uint_as_float(r[c].y & 0xffff0000u)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 64 * c + 4 * g + i;
+        const uint32_t sk = e < E ? select_key(sanitize_logit(f[i])) : 0u;
+        key[4 * c + i] = sk == 0u ? 0ull : (static_cast<uint64_t>(sk) << 32) | static_cast<uint32_t>(~e);
+      }
+    }
+  }
+  float sel_v[kMaxTopK];
+  int sel_i[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    sel_v[s] = -FLT_MAX;
+    sel_i[s] = -1;
+    if (s < k) {
+      uint64_t best = key[0];
+#pragma unroll
+      for (int j = 1; j < 4 * NC; ++j) best = key[j] > best ? key[j] : best;
+      best = max_dpp_u64<0xB1>(best);   // quad_perm [1,0,3,2]
+      best = max_dpp_u64<0x4E>(best);   // quad_perm [2,3,0,1]
+      best = max_dpp_u64<0x141>(best);  // row_half_mirror
+      best = max_dpp_u64<0x140>(best);  // row_mirror
+      const uint32_t kv = static_cast<uint32_t>(best >> 32);
+      if (kv != 0u) {
+        sel_v[s] = __uint_as_float((kv & 0x80000000u) ? (kv & 0x7fffffffu) : ~kv);
+        sel_i[s] = static_cast<int>(~static_cast<uint32_t>(best));
+      }
+#pragma unroll
+      for (int j = 0; j < 4 * NC; ++j) key[j] = key[j] == best ? 0ull : key[j];
+    }
+  }
+  if (g != 0 || t >= T) return;
+  write_slots(sel_v, sel_i, k, variant, idx + static_cast<size_t>(t) * k, w ? w + static_cast<size_t>(t) * k : nullptr,
+              tpe);
+}
+
 // Top-k of all T <= kTopkPlanMaxT tokens (16 waves, tokens w, w + 16, ...),
 // then the plan from the selections.  Each wave loads all its tokens' logits
 // before it stores anything (gfx9 counts stores in vmcnt, so a load issued
@@ -942,47 +1048,67 @@ hipError_t launch_plan_kernel(const int32_t* idx, int T, int k, int E, PlanBufs 
 // through hipBLASLt, cuda_utils.h:226-308, moe_layer.cu:1174-1185): bf16
 // products, fp32 sums in v_mfma_f32_16x16x32_bf16's order, + bias.
 //
-// A work-group computes kMmTT = 32 tokens x kMmEE = 64 experts; wave w owns
-// experts 16 w .. 16 w + 15 for all 32 tokens over the whole K, so a logit is
-// four chains of products (blocks j, j + 4, ...) in block order, added
-// pairwise, plus the bias: a token's logits depend on its own row only
-// (batch-invariant), and every run gives the same bits.  The grid
-// gives the expert slices of eight token blocks to one XCD, so a token row
-// is read from HBM once per XCD.
+// A work-group computes kMmTT = 32 tokens x kMmEE = 64 experts.  K goes in
+// chunks of kMmKB = 4 blocks (128 elements, 256 bytes of each row), and wave
+// j owns chain j: block j of every chunk, for the whole 32 x 64 tile.  So a
+// logit is four chains of products (blocks j, j + 4, ...) in block order,
+// added pairwise at the end, plus the bias: a token's logits depend on its
+// own row only (batch-invariant), and every run gives the same bits.  The
+// grid gives the expert slices of eight token blocks to one XCD, so a token
+// row is read from HBM once per XCD.
 //
-// K goes in chunks of kMmKB blocks (128 elements, 256 bytes of each row).
-// The work-group loads a chunk's rows (32 token rows, 64 router rows) with
-// coalesced 16-byte loads, 16 lanes per row, into a ring of kMmP chunks of
-// registers, so kMmP chunks are in flight behind the one being multiplied;
-// each chunk is written to one of two LDS stages with the 16-byte piece c of
-// row r at position c ^ (r % 16), so that the operand reads (16 rows at one
-// piece) hit distinct banks.  One barrier per chunk.  Loads past the last
-// chunk read past the buffer end (zeros, no memory access); blocks of the
-// last chunk past K are loaded but not multiplied.
+// A chunk's rows (32 token rows, 64 router rows: 24 KiB) go straight from
+// memory into one of kMmS = 6 LDS stages (buffer_load ... lds, 16 bytes a
+// lane: each load fills 1 KiB of the stage, four rows), with the 16-byte
+// piece c of row r at slot c ^ (r % 16), so the operand reads (16 rows at
+// one piece) hit distinct banks; five chunks are in flight behind the one
+// being multiplied.  Each piece is read once, by the wave of its chain: the
+// LDS moves 24 KiB in and 24 KiB out per chunk, and no registers hold the
+// ring.  One barrier per chunk, after the wave's own wait for the chunk.
+// Loads past the last chunk read past the buffer end (zeros, no memory
+// access); blocks of the last chunk past K are loaded but not multiplied.
+// The four chains meet in LDS at the end.
 //
-// Measured on MI355X at 4096 tokens x 128 experts x 2880 (bench leg
-// `router`): 16.8 us for the logits, against 71 us for the gemv tree.  The
-// kernel is bound by what the CUs pull from L2 (553 KiB per work-group): the
-// operands loaded straight in the fragment layout (16 rows x 64 bytes per
-// load) ran at 19-21 us whatever the ring depth, and a split of K into 8
-// ranges with a second pass adding the partial sums at 20 us.
-constexpr int kMmTT = 32, kMmEE = 64, kMmKB = 4, kMmP = 4;
+// Measured on MI355X at 4096 tokens x 128 experts x 2880 (harness, back-to-
+// back launches): 10.3-10.5 us for the logits (the gemv tree: 71 us).  The
+// earlier forms, with the same bits: a register ring stored to two LDS
+// stages by four waves that each read their operands for all four chains
+// (a tile's router rows read by two waves, its token rows by four, and a
+// wait on every read before each product): 16.0-16.7 us; the same with the
+// reads of a chunk issued together: 13.5 us; eight waves: 12.5 us.  The
+// work-group's chain of chunks sets the time (9.3 us at 256 tokens, where
+// the chip is nearly idle): five chunks in flight per CU and their latency.
+constexpr int kMmTT = 32, kMmEE = 64, kMmKB = 4, kMmS = 6;
+constexpr int kMmWaves = kMmKB;                        // wave j: chain j (block j of every chunk)
+constexpr int kMmThreads = kWave * kMmWaves;
 constexpr int kMmRows = kMmTT + kMmEE;                 // rows of a chunk: tokens, then router rows
 constexpr int kMmRowB = kMmKB * 64;                    // bytes of a row in a chunk
 constexpr int kMmLpr = kMmRowB / 16;                   // lanes per row in a load (= pieces per row)
 constexpr int kMmRpl = kWave / kMmLpr;                 // rows per load
-constexpr int kMmLoads = kMmRows * kMmRowB / 1024 / 4;  // 16-byte loads per lane and chunk (a wave's share)
+constexpr int kMmLoads = kMmRows * kMmRowB / 1024 / kMmWaves;  // 1 KiB loads per wave and chunk
 constexpr int kMmStage = kMmRows * kMmRowB;            // bytes of a chunk in LDS
+constexpr int kMmTE = kMmEE / 16, kMmTF = kMmTT / 16;  // 16 x 16 tiles of a work-group: experts, tokens
+
+// s_waitcnt vmcnt(N), the other counters untouched.
+template <int N>
+__device__ __forceinline__ void mm_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
 template <bool F32>
-__global__ __launch_bounds__(kRouteThreads, 2) void logits_mfma_kernel(const uint16_t* __restrict__ x,
-                                                                       const uint16_t* __restrict__ W,
-                                                                       const uint16_t* __restrict__ bias, int T, int E,
-                                                                       int H, void* __restrict__ logits) {
+__global__ __launch_bounds__(kMmThreads) void logits_mfma_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ W,
+                                                                 const uint16_t* __restrict__ bias, int T, int E,
+                                                                 int H, void* __restrict__ logits) {
   typedef float f32x4_t __attribute__((ext_vector_type(4)));
-  static_assert(kMmLpr == 16 && kMmLoads * 4 * 1024 == kMmStage && kMmTT % kMmRpl == 0,
-                "16 pieces per row (the swizzle); four waves share a chunk; a load's rows are all token rows or "
-                "all router rows");
-  __shared__ __attribute__((aligned(16))) uint8_t stage[2][kMmStage];
+  typedef __attribute__((address_space(3))) void lds_void_t;
+  static_assert(kMmLpr == 16 && kMmLoads * kMmWaves * 1024 == kMmStage && kMmTT % kMmRpl == 0,
+                "16 pieces per row (the swizzle); the waves share a chunk's loads; a load's rows are all token rows "
+                "or all router rows");
+  static_assert(kMmS * kMmStage <= 160 * 1024 && kMmWaves * kMmTE * kMmTF * 1024 <= kMmS * kMmStage,
+                "the ring fits the LDS; the chains' exchange fits the ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[kMmS * kMmStage];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int neh = (E + kMmEE - 1) / kMmEE;
@@ -996,84 +1122,104 @@ __global__ __launch_bounds__(kRouteThreads, 2) void logits_mfma_kernel(const uin
   const int rowb = H * 2;  // bytes per row
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(W), 0, E * rowb, 0x00020000);
   const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, T * rowb, 0x00020000);
-  // The wave's loads of a chunk: load i covers chunk rows R = kMmRpl (kMmLoads w
-  // + i) + l / kMmLpr, piece l % kMmLpr of the row's kMmRowB bytes.  Rows past
-  // T / E read the last row (their sums are not stored).
-  int goff[kMmLoads], loff[kMmLoads];
+  // Load i of wave w fills the chunk's KiB L = kMmLoads w + i: rows R =
+  // kMmRpl L + l / kMmLpr, lane l landing at slot s = l % kMmLpr of its row.
+  // Slot s holds the row's piece s ^ (R % 16), so the lane loads that piece.
+  // Rows past T / E read the last row (their sums are not stored).
+  int goff[kMmLoads];
 #pragma unroll
   for (int i = 0; i < kMmLoads; ++i) {
-    const int R = kMmRpl * (kMmLoads * w + i) + lane / kMmLpr, c = lane % kMmLpr;
+    const int R = kMmRpl * (kMmLoads * w + i) + lane / kMmLpr;
+    const int c = (lane % kMmLpr) ^ (R & 15);
     const int row = R < kMmTT ? min(t0 + R, T - 1) : min(e0 + R - kMmTT, E - 1);
     goff[i] = row * rowb + 16 * c;
-    loff[i] = R * kMmRowB + 16 * (c ^ (R & 15));
   }
-  uint4 ring[kMmP][kMmLoads];
-  auto load = [&](int ch, int slot) __attribute__((always_inline)) {
-    const int so = ch < nch ? ch * kMmRowB : 0x40000000;  // past the last chunk: out of range
+  auto issue = [&](int ch, int st) __attribute__((always_inline)) {
+    const int so = ch < nch ? ch * kMmRowB : 0x40000000;  // past the last chunk: out of range (zeros, no access)
+    uint8_t* sp = ring + st * kMmStage;
 #pragma unroll
     for (int i = 0; i < kMmLoads; ++i) {
       const bool ux = kMmRpl * (kMmLoads * w + i) < kMmTT;  // wave-uniform: token rows or router rows
-      ring[slot][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ux ? xrs : wrs, goff[i], so, 0));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ux ? xrs : wrs, (lds_void_t*)(sp + 1024 * (kMmLoads * w + i)), 16,
+                                               goff[i], so, 0, 0);
     }
   };
-  auto store = [&](int slot, int st) __attribute__((always_inline)) {
+  // The bias of the tiles this wave finishes (tiles w, w + kMmWaves, ...:
+  // experts 16 g + 4 (l / 16) + r), loaded now, before the ring's loads: a
+  // null bias is a buffer of no bytes (zeros, no access), so the loads are
+  // unconditional and land long before the end.
+  constexpr int kMmTilesPW = kMmTE * kMmTF / kMmWaves;
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(bias), 0,
+                                                                       bias != nullptr ? E * 2 : 0, 0x00020000);
+  uint16_t bias_raw[kMmTilesPW][4];
 #pragma unroll
-    for (int i = 0; i < kMmLoads; ++i) *reinterpret_cast<uint4*>(stage[st] + loff[i]) = ring[slot][i];
-  };
-  // acc[f][j]: the products of blocks j, j + 4, ... (four chains per logit,
-  // summed pairwise at the end: each chain adds a quarter of the blocks, so
-  // the fp32 error of a logit is about a quarter of one chain's)
-  f32x4_t acc[2][kMmKB];
+  for (int u = 0; u < kMmTilesPW; ++u)
 #pragma unroll
-  for (int f = 0; f < 2; ++f)
+    for (int r = 0; r < 4; ++r) {
+      const int e = e0 + 16 * ((w + kMmWaves * u) / kMmTF) + 4 * (lane >> 4) + r;
+      bias_raw[u][r] = __builtin_amdgcn_raw_buffer_load_b16(brs, 2 * min(e, E), 0, 0);  // e >= E: past the end
+    }
+  // acc[g][f]: chain w of experts 16 g .., tokens 16 f .. (the products of
+  // blocks w, w + 4, ... in block order)
+  f32x4_t acc[kMmTE][kMmTF];
 #pragma unroll
-    for (int j = 0; j < kMmKB; ++j) acc[f][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int g = 0; g < kMmTE; ++g)
+#pragma unroll
+    for (int f = 0; f < kMmTF; ++f) acc[g][f] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const int r16 = lane & 15, q = lane >> 4;
+  const int pz = 16 * ((4 * w + q) ^ r16);  // piece 4 w + q of a 16-aligned row + r16
   auto compute = [&](int st, int ch) __attribute__((always_inline)) {
-    const uint8_t* sp = stage[st];
+    if (kMmKB * ch + w >= nb) return;  // the last chunk's blocks past K (wave-uniform)
+    const uint8_t* sp = ring + st * kMmStage + pz;
+    gx_bf16x8 a[kMmTE], b[kMmTF];
 #pragma unroll
-    for (int j = 0; j < kMmKB; ++j) {
-      if (kMmKB * ch + j >= nb) break;  // the last chunk's blocks past K
-      // piece 4 j + q of the lane's row at its swizzled position (the rows
-      // read here are 16-aligned, so the swizzle is r16)
-      const int pz = 16 * ((4 * j + q) ^ r16);
-      const gx_bf16x8 a = *reinterpret_cast<const gx_bf16x8*>(sp + (kMmTT + 16 * w + r16) * kMmRowB + pz);
+    for (int g = 0; g < kMmTE; ++g) a[g] = *reinterpret_cast<const gx_bf16x8*>(sp + (kMmTT + 16 * g + r16) * kMmRowB);
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        const gx_bf16x8 b = *reinterpret_cast<const gx_bf16x8*>(sp + (16 * f + r16) * kMmRowB + pz);
-        acc[f][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[f][j], 0, 0, 0);
-      }
-    }
+    for (int f = 0; f < kMmTF; ++f) b[f] = *reinterpret_cast<const gx_bf16x8*>(sp + (16 * f + r16) * kMmRowB);
+#pragma unroll
+    for (int g = 0; g < kMmTE; ++g)
+#pragma unroll
+      for (int f = 0; f < kMmTF; ++f) acc[g][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[g], b[f], acc[g][f], 0, 0, 0);
   };
-  // chunk 0 into stage 0; chunks 1 .. kMmP in flight
-  load(0, 0);
-  store(0, 0);
+  // Ring of kMmS stages: at chunk c, chunks c .. c + kMmS - 2 are in flight;
+  // once the wave's loads of chunk c have landed (vmcnt) and every wave's
+  // (the barrier, which also ends every wave's reads of chunk c - 1), the
+  // stage of chunk c - 1 takes chunk c + kMmS - 1.
 #pragma unroll
-  for (int p = 1; p <= kMmP; ++p) load(p, p % kMmP);
-  __syncthreads();
-  for (int c0 = 0; c0 < nch; c0 += kMmP) {
-#pragma unroll
-    for (int u = 0; u < kMmP; ++u) {
-      const int c = c0 + u;  // chunk c in stage c % 2; chunk c + 1 in ring slot (c + 1) % kMmP
-      compute(u & 1, c);
-      store((u + 1) % kMmP, (u + 1) & 1);
-      load(c + 1 + kMmP, (u + 1) % kMmP);
-      __syncthreads();
-    }
+  for (int c = 0; c < kMmS - 1; ++c) issue(c, c);
+  int st = 0;
+  for (int c = 0; c < nch; ++c) {
+    mm_wait_vm<(kMmS - 2) * kMmLoads>();
+    __builtin_amdgcn_s_barrier();  // no fence: the wait above is the one this barrier needs
+    issue(c + kMmS - 1, st == 0 ? kMmS - 1 : st - 1);
+    compute(st, c);
+    st = st == kMmS - 1 ? 0 : st + 1;
   }
-  // acc[f][j][r]: expert 16 w + 4 (l / 16) + r, token 16 f + l % 16
-  const int eb = e0 + 16 * w + 4 * q;
-  float bv[4];
+  // The chains meet in LDS (after the trailing loads past the end have
+  // landed): wave w writes its chain, then takes tiles w, w + 4, ... and
+  // adds the four chains pairwise, then the bias.
+  mm_wait_vm<0>();
+  __syncthreads();
+  f32x4_t* xch = reinterpret_cast<f32x4_t*>(ring);  // [chain][tile][lane]
 #pragma unroll
-  for (int r = 0; r < 4; ++r) bv[r] = bias != nullptr && eb + r < E ? bf16_to_f32(bias[eb + r]) : 0.0f;
+  for (int g = 0; g < kMmTE; ++g)
 #pragma unroll
-  for (int f = 0; f < 2; ++f) {
+    for (int f = 0; f < kMmTF; ++f) xch[(w * kMmTE * kMmTF + g * kMmTF + f) * kWave + lane] = acc[g][f];
+  __syncthreads();
+  static_assert(kMmKB == 4 && (kMmTE * kMmTF) % kMmWaves == 0, "four chains; whole tiles per wave");
+#pragma unroll
+  for (int u = 0; u < kMmTilesPW; ++u) {
+    const int tile = w + kMmWaves * u, g = tile / kMmTF, f = tile % kMmTF;
+    f32x4_t ch[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ch[j] = xch[(j * kMmTE * kMmTF + tile) * kWave + lane];
+    // ch[j][r]: expert 16 g + 4 (l / 16) + r, token 16 f + l % 16
+    const int eb = e0 + 16 * g + 4 * q;
     const int t = t0 + 16 * f + r16;
     if (t >= T) continue;
-    static_assert(kMmKB == 4, "four chains");
     float v[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = ((acc[f][0][r] + acc[f][1][r]) + (acc[f][2][r] + acc[f][3][r])) + bv[r];
+    for (int r = 0; r < 4; ++r) v[r] = ((ch[0][r] + ch[1][r]) + (ch[2][r] + ch[3][r])) + bf16_to_f32(bias_raw[u][r]);
     const size_t o = static_cast<size_t>(t) * E + eb;
     if (eb + 4 <= E && (E & 3) == 0) {
       if constexpr (F32) *reinterpret_cast<float4*>(reinterpret_cast<float*>(logits) + o) = make_float4(v[0], v[1], v[2], v[3]);
@@ -1137,7 +1283,7 @@ hipError_t launch_logits(const RouteArgs& a, hipStream_t s, const KernelTimer& t
   } else if (mm_router_ok(a)) {  // many tokens: the matrix cores
     const int neh = (a.E + kMmEE - 1) / kMmEE, ntb = (a.T + kMmTT - 1) / kMmTT;
     const int grid = ((ntb + 7) / 8) * 8 * neh;
-    gx_launch(logits_mfma_kernel<F32>, dim3(grid), dim3(kRouteThreads), 0, s, t, a.x, a.W, a.b, a.T, a.E, a.H,
+    gx_launch(logits_mfma_kernel<F32>, dim3(grid), dim3(kMmThreads), 0, s, t, a.x, a.W, a.b, a.T, a.E, a.H,
               a.logits);
   } else {
     const int gx = (a.E + kLdsEPW - 1) / kLdsEPW, ntb = (a.T + kLdsTT - 1) / kLdsTT;
@@ -1176,6 +1322,19 @@ template <bool F32>
 void launch_topk_t(const void* logits, int T, int E, int k, int variant, int32_t* idx, float* w, int32_t* tpe,
                    hipStream_t s, const KernelTimer& t) {
   const int nv = (E + kWave - 1) / kWave;
+  const uintptr_t width = F32 ? 16 : 8;  // bytes of one topk16_kernel load
+  if (E % 4 == 0 && reinterpret_cast<uintptr_t>(logits) % width == 0) {
+    const int ntb = (T + 31) / 32;
+    const dim3 grid(((ntb + 7) / 8) * 16);
+#define GX_T16(NC_) gx_launch(topk16_kernel<F32, NC_>, grid, dim3(kRouteThreads), 0, s, t, logits, T, E, k, variant, \
+                              idx, w, tpe)
+    if (nv <= 1) GX_T16(1);
+    else if (nv == 2) GX_T16(2);
+    else if (nv == 3) GX_T16(3);
+    else GX_T16(4);
+#undef GX_T16
+    return;
+  }
   const dim3 grid((T + 3) / 4);
 #define GX_TK(NV_) gx_launch(topk_kernel<F32, NV_>, grid, dim3(kRouteThreads), 0, s, t, logits, T, E, k, variant, idx, \
                              w, tpe)

@@ -130,6 +130,31 @@ def test_topk_softmax(gpu, orc, torch_mod, T, k, fp32):
     assert np.array_equal(host(tpe), hist)
 
 
+@pytest.mark.parametrize("T,E,shift", [(300, 32, 0), (300, 256, 0), (77, 36, 0), (300, 30, 0), (1000, 128, 1),
+                                       (4100, 128, 0), (33, 4, 0), (50, 200, 0)])
+@pytest.mark.parametrize("k", [1, 2, 4, 8])
+@pytest.mark.parametrize("fp32", [False, True])
+def test_topk_softmax_expert_counts(gpu, orc, torch_mod, T, E, shift, k, fp32):
+    """The sixteen-lanes-a-token kernel (E % 4 == 0, logits aligned to its
+    16- / 8-byte loads) over expert counts and ragged token counts, and the
+    one-wave-a-token kernel it falls back to (E = 30, and logits one element
+    off the load alignment), against the oracle."""
+    torch = torch_mod
+    if k > E:
+        pytest.skip("k > E")
+    lg = _crafted_logits(T, E, 7 * T + E + k)
+    host_lg = lg if fp32 else moe_data.bf16(lg)
+    lf = lg if fp32 else orc.bf16_to_f32(host_lg)
+    flat = np.concatenate([np.zeros(shift, host_lg.dtype), host_lg.reshape(-1)])
+    logits = dev(flat, torch)[shift:].view(T, E)
+    tpe = torch.zeros(E, dtype=torch.int32, device="cuda")
+    idx, w = gpu.topk_softmax(logits, k, tokens_per_expert=tpe)
+    ridx, rw = orc.topk_softmax(lf, k)
+    assert np.array_equal(host(idx), ridx)
+    assert np.array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+    assert np.array_equal(host(tpe), np.bincount(ridx[ridx >= 0], minlength=E))
+
+
 MM_MIN_T = 64  # above this many tokens (and H % 32 == 0) the router runs on the matrix cores
 
 
