@@ -1221,7 +1221,10 @@ __global__ __launch_bounds__(kMmThreads) void logits_mfma_kernel(const uint16_t*
 #pragma unroll
     for (int r = 0; r < 4; ++r) v[r] = ((ch[0][r] + ch[1][r]) + (ch[2][r] + ch[3][r])) + bf16_to_f32(bias_raw[u][r]);
     const size_t o = static_cast<size_t>(t) * E + eb;
-    if (eb + 4 <= E && (E & 3) == 0) {
+    // one 16- (fp32) or 8-byte (bf16) store when the four logits are whole
+    // and aligned to it (the C ABI does not require aligned logits)
+    const bool vec = eb + 4 <= E && (E & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & (F32 ? 15 : 7)) == 0;
+    if (vec) {
       if constexpr (F32) *reinterpret_cast<float4*>(reinterpret_cast<float*>(logits) + o) = make_float4(v[0], v[1], v[2], v[3]);
       else *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(logits) + o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     } else {

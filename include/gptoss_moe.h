@@ -361,10 +361,12 @@ int gptoss_moe_layer_profile_records(gptoss_moe_layer* layer, gptoss_moe_prof_re
  * Up to 64 tokens every logit follows the reference's gemv_bf16 tree (its
  * T = 1 path, gemv_bf16.cu:57-129), bit-exact against the oracle.  Above 64
  * (when hidden % 32 == 0) the logits come from the matrix cores: fp32 sums of
- * exact bf16 products in the instruction's order, block by block, then the
- * bias, as the reference's hipBLASLt path for T > 1 sums in its own order;
- * within the fp32 error bound of the exact sum, deterministic, and
- * independent of the other tokens in the call. */
+ * exact bf16 products, four chains per logit (32-element blocks j, j + 4, ...
+ * in block order), added pairwise, then the bias, as the reference's
+ * hipBLASLt path for T > 1 sums in its own order; within the fp32 error bound
+ * of the exact sum, deterministic, and independent of the other tokens in the
+ * call.  router_b may be NULL (zero bias).  Logits need no alignment beyond
+ * their element size. */
 size_t gptoss_moe_route_scratch_bytes(int num_tokens, int num_experts, int top_k);
 int gptoss_moe_route(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
                      int num_tokens, int num_experts, int hidden, int top_k, int logits_fp32,

@@ -242,6 +242,43 @@ def test_route_router_topk(gpu, orc, torch_mod, T, fp32, E, H):
     assert np.array_equal(host(idx2), host(idx))
 
 
+@pytest.mark.parametrize("T,fp32,E,H", [(130, True, 128, 2880), (100, False, 20, 512), (9, True, 128, 2880),
+                                         (300, False, 128, 2880)])
+def test_route_null_bias_and_unaligned_logits(gpu, orc, torch_mod, T, fp32, E, H):
+    """A null router bias is a zero bias: the same bits as an explicit zero
+    bias on both logit orders (and, on the tree, the oracle's bits).  Logits
+    one element off the 16- / 8-byte store alignment get the same bits, and
+    the top-k over them (the one-wave-a-token kernel then) the same
+    selections and weights."""
+    torch = torch_mod
+    k = 4
+    rng = np.random.default_rng(3 * T + E)
+    x = moe_data.bf16(rng.normal(0, 1, (T, H)))
+    W = moe_data.bf16(rng.normal(0, 0.02, (E, H)))
+    zero = np.zeros(E, np.uint16)
+    xd, Wd = dev(x, torch), dev(W, torch)
+    l0, i0, w0 = gpu.route(xd, Wd, None, k, logits_fp32=fp32)
+    l1, i1, w1 = gpu.route(xd, Wd, dev(zero, torch), k, logits_fp32=fp32)
+    assert np.array_equal(host(l0).view(np.uint8), host(l1).view(np.uint8))
+    assert np.array_equal(host(i0), host(i1))
+    assert np.array_equal(host(w0).view(np.uint32), host(w1).view(np.uint32))
+    if T <= MM_MIN_T:
+        ref = orc.router(x, W, zero, logits_fp32=fp32)
+        assert np.array_equal(host(l0).view(np.uint8), ref.view(np.uint8))
+    # logits at an odd element offset inside a larger buffer
+    dt = torch.float32 if fp32 else torch.bfloat16
+    buf = torch.full((T * E + 1,), 7.0, dtype=dt, device="cuda")
+    lu = buf[1:].view(T, E)
+    iu = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    wu = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    gpu.route(xd, Wd, None, k, logits_fp32=fp32, out=(lu, iu, wu))
+    torch.cuda.synchronize()
+    assert float(buf[0].item()) == 7.0
+    assert np.array_equal(host(lu).view(np.uint8), host(l0).view(np.uint8))
+    assert np.array_equal(host(iu), host(i0))
+    assert np.array_equal(host(wu).view(np.uint32), host(w0).view(np.uint32))
+
+
 # 6144 x 4 slots: the largest plan whose indices are staged in LDS; 8192 x 4:
 # the plan reads them from global memory
 @pytest.mark.parametrize("T,k,E", [(1, 4, 128), (64, 4, 128), (4096, 4, 128), (6144, 4, 128), (8192, 4, 128),
