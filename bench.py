@@ -7,8 +7,11 @@ a batch of B decode tokens, E=128 experts, H=I=2880, top-4.  Weights are
 synthetic (uniform e2m1 codes, e8m0 scales 2^-8..2^-4, router ~N(0,0.02),
 zero non-null biases) and live in HBM; the timed steps rotate over
 `--copies` distinct weight copies and inputs so the 256 MB MALL cannot hold
-a step's weights.  The K timed steps are one hipGraph replay (wall interval
-from events around the replay).  Per-launch durations come from a second,
+a step's weights.  The K timed steps are one hipGraph replay (interval from
+events around the replay); before it the W eager warm-up steps run, and the
+same graph is replayed untimed for about 40 ms of back-to-back work, queued
+right ahead of the timed replay, so a short K is timed in the steady state
+that a long one reaches by itself.  Per-launch durations come from a second,
 eager pass of the same K steps in which the library records HIP events on
 its launch stream around each launch (events cannot be timed inside a graph
 replay on this runtime).
@@ -23,6 +26,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -66,6 +70,34 @@ def make_copy(g, torch, seed: int):
     return dict(tiled=(w1n, w1s, w2n, w2s), router_w=rw, router_b=rb, b1=b1, b2=b2)
 
 
+SETTLE_MS = 40.0  # untimed back-to-back GPU work before a timed replay
+
+
+def settle(torch, graph, s, ms: float = SETTLE_MS, max_replays: int = 200) -> int:
+    """Untimed replays of `graph` on stream s until about `ms` of back-to-back
+    GPU work has run, queued with no host wait at the end, so the timed
+    replay the caller queues next follows with no idle gap.  Returns the
+    number of replays.  Measured on MI355X: a 20-step decode graph at batch
+    32 replayed five times back to back read 210, 198, 187, 186 and 185 us per
+    step, while a 64-step graph built after it read 185 from its first
+    replay, and a replay after 5 ms of idle read ~3 % slow: the device
+    settles after some tens of ms of sustained work, which one replay of a
+    short graph does not give."""
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        e0.record(s)
+        graph.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    one = max(e0.elapsed_time(e1), 1e-3)
+    n = min(max_replays, max(0, int(math.ceil(ms / one)) - 1))
+    with torch.cuda.stream(s):
+        for _ in range(n):
+            graph.replay()
+    return n + 1
+
+
 def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, graph_timing: bool = True,
                 exact: bool = False):
     """Time `steps` graph-replayed layer forwards at batch T; returns a dict.
@@ -97,24 +129,25 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, gr
     torch.cuda.synchronize()
 
     # headline: the K steps captured in one hipGraph, timed over one replay
+    # that follows about SETTLE_MS of untimed replays with no idle gap (wall:
+    # host time of the settling and timed replays together)
     s = torch.cuda.Stream()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    n_settle = 0
     if graph_timing:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=s):
             for li, xi in plan:
                 layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
-        graph.replay()  # warm replay
-        torch.cuda.synchronize()
         wall0 = time.perf_counter()
+        n_settle = settle(torch, graph, s)
         with torch.cuda.stream(s):
             t0.record(s)
             graph.replay()
             t1.record(s)
         torch.cuda.synchronize()
         wall = time.perf_counter() - wall0
-        del graph
     else:
         wall0 = time.perf_counter()
         with torch.cuda.stream(s):
@@ -127,20 +160,27 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, gr
     total_ms = t0.elapsed_time(t1)
 
     # per-launch durations: the same K steps eagerly, each launch timed by HIP
-    # events stamped by its own dispatch (the library's profiling mode).  A
-    # bounded sleep kernel holds the stream while the host enqueues all K
-    # steps, so the launches run back to back as in the replay.
+    # events stamped by its own dispatch (the library's profiling mode).
+    # Untimed replays of the graph (about SETTLE_MS, settle) hold the stream
+    # while the host enqueues all K steps, so the launches run back to back
+    # as in the replay and in the same settled state (without a graph, a
+    # bounded sleep kernel holds it).
     per_layer = [sum(1 for li, _ in plan if li == j) for j in range(len(layers))]
     for j, L in enumerate(layers):
         L.set_profiling(per_layer[j])
+    if graph_timing:
+        settle(torch, graph, s)
     with torch.cuda.stream(s):
-        try:
-            torch.cuda._sleep(int(50e6))  # ~20 ms of spinning at 2.4 GHz
-        except Exception:
-            pass
+        if not graph_timing:
+            try:
+                torch.cuda._sleep(int(50e6))  # ~20 ms of spinning at 2.4 GHz
+            except Exception:
+                pass
         for li, xi in plan:
             layers[li].forward_prenormed(xs[xi], rs[xi], out=outs[xi])
     torch.cuda.synchronize()
+    if graph_timing:
+        del graph
     r_ms = w1_ms = w2_ms = c_ms = 0.0
     n_rec = 0
     for L in layers:
@@ -158,7 +198,7 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, gr
     w1_bytes = sum(u * W1_EXPERT_BYTES + T * H * 2 for u in U) / len(U)
     res = dict(batch=T, ms_per_step=ms_step, tokens_per_s=T / (ms_step / 1e3), experts_touched=u_mean,
                algorithmic_bytes_per_step=bytes_step, hbm_gbs=bytes_step / (ms_step / 1e3) / 1e9,
-               wall_s=wall, events_recorded=n_rec)
+               wall_s=wall, settle_replays=n_settle, events_recorded=n_rec)
     res["hbm_frac"] = res["hbm_gbs"] / HBM_PEAK_GBS
     if n_rec == steps:
         res["kernel_us"] = dict(route=1e3 * r_ms / steps, w1=1e3 * w1_ms / steps, w2=1e3 * w2_ms / steps,
@@ -264,8 +304,9 @@ def zipf_routing(seed: int, T: int, k: int, s: float = 1.1):
 
 def timed_graph(torch, fn, per_graph: int = 5, replays: int = 4, warm: int = 1):
     """Mean ms of fn() from replays of a hipGraph holding per_graph calls,
-    after `warm` untimed replays: steady state, without the clock ramp of
-    the first calls after the device idles."""
+    after `warm` untimed replays and then about SETTLE_MS of them (settle):
+    steady state, without the clock ramp of the first calls after the
+    device idles."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     fn()
@@ -277,6 +318,7 @@ def timed_graph(torch, fn, per_graph: int = 5, replays: int = 4, warm: int = 1):
     for _ in range(warm):
         graph.replay()
     torch.cuda.synchronize()
+    settle(torch, graph, s)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(s):
@@ -378,8 +420,7 @@ def bench_residual(g, torch, wc, T: int, steps: int = 64):
         with torch.cuda.graph(graph, stream=s):
             for _ in range(steps):
                 fn()
-        graph.replay()
-        torch.cuda.synchronize()
+        settle(torch, graph, s)
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(s):
