@@ -570,6 +570,8 @@ __global__ void special_scan_kernel(const uint8_t* __restrict__ ws, TiledGeom g,
   }
 }
 
+constexpr int kDownOnePerCuSlots = 64;
+
 template <bool kGated, int P, int D, int NC, bool kSpec, int BPP, bool kRoute = false, int kStg = 0>
 hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_t s, const KernelTimer& timer) {
   static const int per_cu = [] {  // resident work-groups per CU (a property of the kernel)
@@ -580,8 +582,19 @@ hipError_t launch_mc_t(const McParams& p, int max_items, int num_cus, hipStream_
       n = 1;
     return n;
   }();
-  const long resident = static_cast<long>(per_cu) * (num_cus > 0 ? num_cus : 256);
+  const int cus = num_cus > 0 ? num_cus : 256;
+  const long resident = static_cast<long>(per_cu) * cus;
   long grid = max_items < resident ? max_items : resident;
+  // The down product from kDownOnePerCuSlots slots on: one work-group per CU
+  // (each of its waves on a SIMD of its own, fewer streams in flight).
+  // Measured (GPT-OSS-120B, P=3, D=10, five resident per CU, per-dispatch
+  // events): down at B=64 74.6-75.1 against 76.6-77.0 us, B=32 56.6-56.8
+  // against 57.9-58.3, B=16 37.9-38.1 against 38.3-38.4 (four runs, two
+  // boxes); B=48 even; at B=8 (32 slots) slower, 24.6 against 21.2.  Grids
+  // of 512, 640 and 768 work-groups were no faster, 384 slower (88 us at
+  // B=64); gate_up with one per CU was slower (150.5 against 147.5 us).
+  if constexpr (!kGated)
+    if (p.slots >= kDownOnePerCuSlots && grid > cus) grid = cus;
   grid = (grid + 7) & ~7L;  // a multiple of 8 for the XCD-grouped block order
   if constexpr (kRoute) grid += 8;  // work-groups past the items: they write the one-token plan
   McParams q = p;
