@@ -495,8 +495,10 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* __restric
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  // every slot's map entry and weight, then every expert row, in flight at
-  // once (two dependent round trips in all, not two per slot)
+  // every slot's map entry and weight and the residual piece, then every
+  // expert row, in flight at once: two dependent round trips in all (the
+  // residual read after the rows would make a third; measured on the decode
+  // steps, the two forms time the same)
   int gm[kMaxTopK];
   float ws[kMaxTopK];
 #pragma unroll
@@ -504,6 +506,8 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* __restric
     gm[s] = s < k ? gather_map[t * k + s] : -1;
     ws[s] = s < k ? w[t * k + s] : 0.0f;
   }
+  uint4 rv = make_uint4(0u, 0u, 0u, 0u);
+  if (residual != nullptr) rv = *reinterpret_cast<const uint4*>(residual + static_cast<size_t>(t) * H + c * 8);
   uint4 v[kMaxTopK];
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s)
@@ -520,8 +524,7 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* __restric
     }
   }
   if (residual != nullptr) {
-    const uint4 v = *reinterpret_cast<const uint4*>(residual + static_cast<size_t>(t) * H + c * 8);
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t d[4] = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       acc[2 * i] = acc[2 * i] + __uint_as_float(d[i] << 16);
