@@ -242,6 +242,47 @@ def test_route_router_topk(gpu, orc, torch_mod, T, fp32, E, H):
     assert np.array_equal(host(idx2), host(idx))
 
 
+@pytest.mark.parametrize("T,fp32", [(4096, True), (300, False), (64, False)])
+def test_route_graph_replays(gpu, orc, torch_mod, T, fp32):
+    """The router's launches (the matrix-core logits and the sixteen-lane
+    top-k above 64 tokens, the tree below) captured in one hipGraph: every
+    replay, with eager work and synchronisations between the replays and
+    new inputs copied into the captured buffers, gives the eager call's
+    bits."""
+    torch = torch_mod
+    E, H, k = 128, 2880, 4
+    rng = np.random.default_rng(11 + T)
+    xs = [moe_data.bf16(rng.normal(0, 1, (T, H))) for _ in range(3)]
+    W = dev(moe_data.bf16(rng.normal(0, 0.02, (E, H))), torch)
+    b = dev(moe_data.bf16(rng.normal(0, 0.02, E)), torch)
+    x = dev(xs[0], torch)
+    dt = torch.float32 if fp32 else torch.bfloat16
+    logits = torch.empty((T, E), dtype=dt, device="cuda")
+    idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    scratch = gpu.route_scratch(T, E, k)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        gpu.route(x, W, b, k, logits_fp32=fp32, out=(logits, idx, w), scratch=scratch, stream=s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        gpu.route(x, W, b, k, logits_fp32=fp32, out=(logits, idx, w), scratch=scratch, stream=s)
+    for rep, xn in enumerate(xs * 2):
+        x.copy_(dev(xn, torch))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (host(logits).copy(), host(idx).copy(), host(w).copy())
+        el, ei, ew = gpu.route(dev(xn, torch), W, b, k, logits_fp32=fp32)  # eager, fresh buffers
+        torch.cuda.synchronize()
+        assert np.array_equal(got[0].view(np.uint8), host(el).view(np.uint8)), rep
+        assert np.array_equal(got[1], host(ei)), rep
+        assert np.array_equal(got[2].view(np.uint32), host(ew).view(np.uint32)), rep
+    del graph
+
+
 @pytest.mark.parametrize("T,fp32,E,H", [(130, True, 128, 2880), (100, False, 20, 512), (9, True, 128, 2880),
                                          (300, False, 128, 2880)])
 def test_route_null_bias_and_unaligned_logits(gpu, orc, torch_mod, T, fp32, E, H):
