@@ -12,6 +12,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for p in (ROOT, os.path.join(ROOT, "oracle"), os.path.join(ROOT, "hip-kernels_amd"), os.path.dirname(__file__)):
     if p not in sys.path:
         sys.path.insert(0, p)
+# GPTOSS_PYBIND_DIR: another build of the `gptoss` module (the sanitizer
+# build of tests/sanitize), imported ahead of the in-tree one
+if os.environ.get("GPTOSS_PYBIND_DIR"):
+    sys.path.insert(0, os.environ["GPTOSS_PYBIND_DIR"])
 
 
 def pytest_configure(config):
