@@ -148,9 +148,9 @@ struct Step {
 // each item's token chunks in order; each step applies the R tiles' weights
 // to up to TC tokens.  Lane l of wave p owns row l of each tile and runs, per
 // token, one ascending fmaf chain over K-part p (the canonical dot); the part
-// sums are added in part order by threads 0..R*64-1, which then add the bias
-// and emit (gate_up: bf16 gate/up values, clamped SwiGLU on lane pairs, bf16
-// activations; down: bf16 expert outputs).
+// sums are added in part order across the work-group, which then adds the
+// bias and emits (gate_up: bf16 gate/up values, clamped SwiGLU on lane pairs,
+// bf16 activations; down: bf16 expert outputs).
 //
 // Streaming: the weights of a step move through a ring of D blocks per row
 // held in VGPRs; consuming block i issues block i + D, which past the end of
@@ -248,15 +248,17 @@ void expert_stream_kernel(StreamParams a) {
     }
   };
 
-  // Raw bf16 bias of the row this thread emits for step s (rows of a missing
-  // tile: clamped, not emitted).  Converted only where it is used, so its
-  // wait never covers the weight loads issued after it.
-  auto bias_raw = [&](const Step& s) -> uint16_t {
+  // Raw bf16 bias of row rr of step s's tile group (rows of a missing tile:
+  // clamped, not emitted).  Each thread prefetches the bias of its own row
+  // rt = tid % (R*64), converted only where it is used, so its wait never
+  // covers the weight loads issued after it.
+  auto bias_raw = [&](const Step& s, int rr) -> uint16_t {
     if (a.bias == nullptr || !s.valid) return 0;
-    const int row = min(s.tp * R * kTileRows + static_cast<int>(threadIdx.x) % (R * kTileRows), N - 1);
+    const int row = min(s.tp * R * kTileRows + rr, N - 1);
     return a.bias[static_cast<size_t>(s.e) * N + row];
   };
-  uint16_t braw = bias_raw(cur);
+  const int rt = static_cast<int>(threadIdx.x) % (R * kTileRows);
+  uint16_t braw = bias_raw(cur, rt);
 
   // Prologue: the first step's scales, activations and first kD blocks.
   uint32_t sc[R][kMaxBpp / 4];
@@ -297,6 +299,14 @@ void expert_stream_kernel(StreamParams a) {
   }
   if (static_cast<int>(threadIdx.x) < kMaxExperts)
     sm.hdr[threadIdx.x] = make_int2(hv.x < 0 ? -1 : (hv.x | (hv.z << 8)), hv.y);
+  // A block of 64 x parts threads holds fewer threads than records when K
+  // splits into one to three parts and more experts are active: the rest of
+  // the records, here (their wait also covers the weight loads above).
+  for (int i = static_cast<int>(threadIdx.x + blockDim.x); i < min(a.max_active, kMaxExperts);
+       i += static_cast<int>(blockDim.x)) {
+    const int4 h = reinterpret_cast<const int4*>(a.tasks)[static_cast<size_t>(i) * (kTaskInts / 4)];
+    sm.hdr[i] = make_int2(h.x < 0 ? -1 : (h.x | (h.z << 8)), h.y);
+  }
   if constexpr (kGated && kTok > 1)
     if (static_cast<int>(threadIdx.x) < a.slots) sm.tok[threadIdx.x] = tv;
   __syncthreads();
@@ -381,7 +391,7 @@ void expert_stream_kernel(StreamParams a) {
     for (int i = 0; i < kLoop; ++i) {
       if (i == kLoop - kD) {
         // the next step's bias, scales and activations go ahead of its blocks
-        nbraw = bias_raw(nxt);
+        nbraw = bias_raw(nxt, rt);
         load_sc(nxt, nsc);
         issue_x(nxt, ntok, xl);
       }
@@ -446,17 +456,21 @@ void expert_stream_kernel(StreamParams a) {
         if (m < mc) ps[(m * R + r) * kTileRows + lane] = acc[r][m];
     __syncthreads();
     // Reduction over the parts, spread over the whole work-group: output q is
-    // token q / (R*64), row rr = q % (R*64) == tid % (R*64) (R*64 divides the
-    // block size), so each thread keeps one row and its bias, and a wave's
-    // lanes hold 64 consecutive rows (gate/up pairs on adjacent lanes).
+    // token q / (R*64), row rr = q % (R*64), and a wave's lanes hold 64
+    // consecutive rows (gate/up pairs on adjacent lanes).  Where R*64
+    // divides the block (64 * parts threads), rr is the thread's own row rt
+    // on every pass and its prefetched bias serves; otherwise (an odd part
+    // count with R = 2) a pass whose rows are not rt loads their bias itself.
+    // rr - rt is the same on every lane of a wave, so the branch is uniform.
     const size_t row0 = static_cast<size_t>(cur.tp) * R * kTileRows;
-    const bool row_ok = cur.tp * R + static_cast<int>(threadIdx.x % (R * kTileRows)) / kTileRows < ntiles;
     for (int q = threadIdx.x; q < mc * R * kTileRows; q += blockDim.x) {
       const int m = q / (R * kTileRows), rr = q - m * (R * kTileRows);
+      const bool row_ok = cur.tp * R + rr / kTileRows < ntiles;
+      const uint16_t bq = rr == rt ? braw : bias_raw(cur, rr);
       float v = (&sm.x[0][0][0])[q];
       for (int pp = 1; pp < g.parts; ++pp) v = v + (&sm.x[pp][0][0])[q];
       const size_t slot = static_cast<size_t>(cur.off + cur.c * TC + m);
-      const uint16_t h = f32_to_bf16(v + bf16_to_f32(braw));
+      const uint16_t h = f32_to_bf16(v + bf16_to_f32(bq));
       if constexpr (kGated) {
         if (row_ok && a.gate_up != nullptr) a.gate_up[slot * N + row0 + rr] = h;
         const float gu = bf16_to_f32(h);

@@ -85,6 +85,36 @@ def test_mc_layer_small_stagewise(gpu, orc, torch_mod, T, bias):
     check_layer_out(out, ref, f"mc small T={T} bias={bias} out vs oracle")
 
 
+@pytest.mark.parametrize("T,H,I", [(40, 320, 96), (20, 640, 160), (64, 128, 224), (3, 320, 96)])
+def test_mc_layer_odd_block_counts(gpu, orc, torch_mod, T, H, I):
+    """E=8, k=4 with K/32 = 10, 3, 20, 5, 4 and 7 blocks per row (the
+    generic one-part shapes take the ring depth that divides it) and output
+    tiles N / 64 = 3, 5 and 7; every stage against the oracle on the GPU's
+    inputs."""
+    torch = torch_mod
+    E, k = 8, 4
+    w = moe_data.make_layer(80 + T + H, E, H, I, bias="random")
+    x, res = moe_data.make_tokens(80 + T + H, T, H)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=64, exact=False)
+    L.layer.set_trace_gate_up(True)
+    say("mc odd block counts", T, H, I)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    torch.cuda.synchronize()
+    ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    got = _trace_arrays(gpu, L.layer, T, k, E, H, I, torch, True)
+    assert np.array_equal(got["idx"], tr["idx"])
+    check_single_rounding(got["gate_up"], tr["gate_up"], f"mc odd T={T} H={H} gate_up")
+    assert np.array_equal(got["act"], orc.swiglu_rows(got["gate_up"], I))
+    offs = np.concatenate([[0], np.cumsum(np.bincount(tr["idx"].ravel(), minlength=E))])
+    ylocal = np.zeros_like(got["y"])
+    for e in range(E):
+        a, b = int(offs[e]), int(offs[e + 1])
+        if b > a:
+            ylocal[a:b] = orc.mxfp4_gemv(got["act"][a:b], w["w2_packed"][e], w["w2_scales"][e], w["w2_bias"][e], H, I)
+    check_single_rounding(got["y"], ylocal, f"mc odd T={T} H={H} y (same activations)")
+    check_layer_out(out, ref, f"mc odd T={T} H={H} I={I} out vs oracle")
+
+
 @pytest.fixture(scope="module")
 def pair120(gpu, torch_mod):
     """One tiled copy of GPT-OSS-120B-shaped weights (E=128, H=I=2880) under

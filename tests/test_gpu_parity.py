@@ -449,6 +449,37 @@ def test_layer_small_with_intermediates(gpu, orc, torch_mod, T, bias):
     assert_bf16_parity(out, ref, f"layer small T={T} bias={bias}")
 
 
+@pytest.mark.parametrize("T,E,H,I", [(40, 8, 320, 96), (20, 8, 640, 160), (64, 128, 128, 224), (3, 8, 320, 96)])
+def test_layer_odd_part_counts(gpu, orc, torch_mod, T, E, H, I):
+    """Products whose K splits into an odd number of parts (gate_up K = H:
+    320 -> 5 parts of 2 blocks, 640 -> 5 of 4; down K = I: 96 -> 3 parts of
+    1 block, 160 -> 5 of 1).  The exact kernels' work-group then has 64 x
+    parts threads, which is not a multiple of the two-tile row group (128
+    rows) taken above 64 slots, so the part-sum reduction's later passes emit
+    rows other than the one each thread's prefetched bias belongs to.  The
+    output tiles (N / 64 = 3, 5 or 7) leave the last row group one tile
+    short.  I = 224 (7 blocks, one part: 64 threads) with up to 128 active
+    experts also has more task records than threads.  T = 3 (12 slots, one
+    tile per group) is the control.  Gate_up values, activations, expert
+    outputs and the layer output are bit-exact."""
+    torch = torch_mod
+    k = 4
+    w = moe_data.make_layer(70 + T + H, E, H, I, bias="random")
+    x, res = moe_data.make_tokens(70 + T + H, T, H)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=64)
+    L.layer.set_trace_gate_up(True)
+    say("odd part counts", T, E, H, I)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    torch.cuda.synchronize()
+    ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    got = _trace_arrays(gpu, L.layer, T, k, E, H, I, torch, True)
+    assert np.array_equal(got["idx"], tr["idx"])
+    assert np.array_equal(got["gate_up"], tr["gate_up"])
+    assert np.array_equal(got["act"], tr["act"])
+    assert np.array_equal(got["y"], tr["y"])
+    assert_bf16_parity(out, ref, f"odd part counts T={T} H={H} I={I}")
+
+
 def test_layer_golden_fixture(gpu, torch_mod):
     """The committed fixture (tests/golden/moe_tiny.npz) reproduced on the GPU."""
     torch = torch_mod
