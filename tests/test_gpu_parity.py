@@ -172,7 +172,8 @@ def _mm_router_bound(orc, x, W, b):
 @pytest.mark.parametrize("T,fp32,E,H", [(1, False, 128, 2880), (8, False, 128, 2880), (64, False, 128, 2880),
                                          (9, True, 128, 2880), (4096, True, 128, 2880), (100, False, 20, 512),
                                          (300, True, 36, 4104), (130, True, 256, 2880), (65, True, 128, 2880),
-                                         (1000, False, 128, 2880)])
+                                         (1000, False, 128, 2880), (5, False, 30, 2880), (100, True, 30, 512),
+                                         (70, False, 7, 192)])
 def test_route_router_topk(gpu, orc, torch_mod, T, fp32, E, H):
     """Router + top-k; T=4096 fp32 is BASELINE config 1.
     Up to 64 tokens (and for H % 32 != 0: H = 4104, three chunks per chain)
@@ -185,7 +186,9 @@ def test_route_router_topk(gpu, orc, torch_mod, T, fp32, E, H):
     two candidates for the k-th place lie within the bound of each other
     (none in these cases) with weights within 1e-6 (the config-1 bar).  The
     many-token cases also cover partial tiles (T, E not multiples of the
-    tiles), a short hidden size and 256 experts."""
+    tiles), a short hidden size and 256 experts; E = 30 and 7 (not a multiple
+    of the four experts a tree work-group or a logit store covers) run on
+    both orders."""
     torch = torch_mod
     k = 4
     rng = np.random.default_rng(T + E + H)
@@ -522,7 +525,8 @@ def test_fused_residual_rmsnorm_stage(gpu, orc, torch_mod, T, H):
 
 @pytest.mark.parametrize("T,E,H,I", [(1, 16, 192, 128), (4, 16, 192, 128), (5, 16, 192, 128), (8, 16, 192, 128),
                                      (9, 16, 192, 128), (64, 16, 192, 128), (100, 16, 192, 128),
-                                     (2, 32, 2880, 2880), (8, 32, 2880, 2880), (64, 32, 2880, 2880)])
+                                     (2, 32, 2880, 2880), (8, 32, 2880, 2880), (64, 32, 2880, 2880),
+                                     (9, 6, 128, 128), (40, 30, 192, 128)])
 def test_layer_forward_residual(gpu, orc, torch_mod, T, E, H, I):
     """forward_residual = fused_residual_rmsnorm_forward + forward_prenormed:
     the new residual bit-exact, the router's logits bit-exact (the norm
