@@ -85,19 +85,22 @@ def test_mc_layer_small_stagewise(gpu, orc, torch_mod, T, bias):
     check_layer_out(out, ref, f"mc small T={T} bias={bias} out vs oracle")
 
 
-@pytest.mark.parametrize("T,H,I", [(40, 320, 96), (20, 640, 160), (64, 128, 224), (3, 320, 96)])
-def test_mc_layer_odd_block_counts(gpu, orc, torch_mod, T, H, I):
-    """E=8, k=4 with K/32 = 10, 3, 20, 5, 4 and 7 blocks per row (the
-    generic one-part shapes take the ring depth that divides it) and output
-    tiles N / 64 = 3, 5 and 7; every stage against the oracle on the GPU's
-    inputs."""
+@pytest.mark.parametrize("T,E,H,I", [(40, 8, 320, 96), (20, 8, 640, 160), (64, 8, 128, 224), (3, 8, 320, 96),
+                                     (1, 30, 128, 128), (2, 30, 128, 128), (1, 6, 192, 128), (9, 6, 128, 128),
+                                     (40, 30, 192, 128)])
+def test_mc_layer_odd_block_counts(gpu, orc, torch_mod, T, E, H, I):
+    """k=4 with K/32 = 10, 3, 20, 5, 4, 6 and 7 blocks per row (the generic
+    one-part shapes take the ring depth that divides it), output tiles
+    N / 64 = 3, 5 and 7, and E = 6 and 30 (not a multiple of the 64 experts
+    a routing wave covers) at one, two and more tokens; every stage against
+    the oracle on the GPU's inputs."""
     torch = torch_mod
-    E, k = 8, 4
+    k = 4
     w = moe_data.make_layer(80 + T + H, E, H, I, bias="random")
     x, res = moe_data.make_tokens(80 + T + H, T, H)
     L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=64, exact=False)
     L.layer.set_trace_gate_up(True)
-    say("mc odd block counts", T, H, I)
+    say("mc odd block counts", T, E, H, I)
     out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
     torch.cuda.synchronize()
     ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
