@@ -239,6 +239,42 @@ def test_layer_prefill_path_vs_oracle(gpu, orc, torch_mod, mode):
     check_layer_out(out, ref, f"prefill layer out (mode {mode})", over, steps)
 
 
+@pytest.mark.parametrize("T,E,H,I", [(200, 256, 128, 128), (150, 30, 192, 96), (129, 7, 320, 160)])
+def test_layer_prefill_shapes(gpu, orc, torch_mod, T, E, H, I):
+    """The default prefill path (bf16 products) over expert counts and
+    shapes the GPT-OSS layers do not have: 256 experts (the most a layer
+    takes; most hold a partial m-tile of a few rows), E = 30 and 7 (not a
+    multiple of four), K = 96 and 160 (three and five blocks), gate_up
+    n-tiles of 192 and 320 rows (a partial 256-row work-group tile), and
+    T = 129, one token past the prefill threshold.  Indices bit-identical,
+    SwiGLU of the GPU's gate_up bit-identical, the stages within one bf16
+    step of the oracle's, the output within the matrix-core tolerance."""
+    torch = torch_mod
+    k = 4
+    w = moe_data.make_layer(90 + E, E, H, I, bias="random")
+    x, res = moe_data.make_tokens(90 + E, T, H)
+    L = DeviceLayer(gpu, torch, w, E, k, H, I, max_tokens=T, via_tables=False)
+    assert L.layer.cfg.prefill_min_tokens <= T
+    L.layer.set_trace_gate_up(True)
+    say("prefill shapes", T, E, H, I)
+    out = host(L.layer.forward_prenormed(dev(x, torch), dev(res, torch)))
+    torch.cuda.synchronize()
+    ref, tr = orc.moe_forward(w, x, res, E, k, H, I, trace=True)
+    got = _layer_trace(gpu, L.layer, T, k, H, I)
+    assert np.array_equal(got["idx"], tr["idx"])
+    check_single_rounding(got["gate_up"], tr["gate_up"], f"prefill shapes E={E} gate_up")
+    assert np.array_equal(got["act"], orc.swiglu_rows(got["gate_up"], I))
+    ylocal = np.zeros_like(got["y"])
+    offs = np.concatenate([[0], np.cumsum(np.bincount(tr["idx"].ravel(), minlength=E))])
+    for e in range(E):
+        a, b = int(offs[e]), int(offs[e + 1])
+        if b > a:
+            ylocal[a:b] = orc.mxfp4_gemv(got["act"][a:b], w["w2_packed"][e], w["w2_scales"][e], w["w2_bias"][e], H, I)
+    check_single_rounding(got["y"], ylocal, f"prefill shapes E={E} y (same activations)")
+    assert np.array_equal(out, orc.combine(got["y"], tr["gather_map"], tr["w"], res, T, k, H))
+    check_layer_out(out, ref, f"prefill shapes T={T} E={E} H={H} I={I}")
+
+
 @pytest.mark.parametrize("mode", [0, 1, 2])
 def test_layer_prefill_special_scales(gpu, orc, torch_mod, mode):
     """e8m0 codes 0 (+0) and 255 (+inf) in some experts' W1 and W2 blocks, on
