@@ -19,7 +19,9 @@ replay on this runtime).
 The headline `value` is tokens/s at the largest batch (64); every batch of
 the sweep is reported under `sweep`.  `roofline` is for the dominant kernel
 (the gate_up + SwiGLU launch) at the headline batch; its `traffic` is read
-from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary.  `cpu_baseline`
+from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, and
+`frac_of_measured_read_ceiling` compares it with the rate a plain streaming
+read reaches on the same device in the same run (leg `read_ceiling`).  `cpu_baseline`
 is the C oracle (oracle/moe_oracle.c) timed on this host on a bounded sample.
 """
 from __future__ import annotations
@@ -270,6 +272,57 @@ def bench_launch_floor(torch, chain: int = 200, sizes=(64, 1 << 20)):
         res[str(n)] = {"us_per_kernel": us, "us_per_4": 4 * us, "us_per_5": 5 * us}
         del graph
     return {"dependent_kernels_by_floats": res, "kernel": "torch add_ (fp32)", "chain": chain}
+
+
+def bench_read_ceiling(torch, mib: int = 1024, reps: int = 20):
+    """The HBM read rate a plain streaming kernel reaches on this device: the
+    practical ceiling of the decode streams, which read every touched
+    expert's weights once (the published 8 TB/s is the interface's peak, not
+    what a read reaches).  The kernel (tests/hw/hbm_read_probe.hip) makes one
+    pass of 16-byte nontemporal loads over `mib` MiB (about the gate_up
+    launch's 1.0 GB at batch 64).  It sweeps the grid and the loads in
+    flight per lane.  Each point is `reps` back-to-back launches timed with
+    events on the launch stream, after ~40 ms of untimed launches.  The leg
+    reports every point and the best."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "tests", "hw", "libhbm_read_probe.so"))
+    lib.hbm_read_probe.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+    lib.hbm_read_probe.restype = ctypes.c_int
+    nbytes = mib << 20
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+
+    def launch(grid, unroll):
+        rc = lib.hbm_read_probe(buf.data_ptr(), nbytes, grid, unroll, sink.data_ptr(), s.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"hbm_read_probe failed ({rc})")
+
+    # settle: ~40 ms of back-to-back reads (about 0.15 ms each)
+    for _ in range(int(SETTLE_MS / 0.15)):
+        launch(2 * cus, 4)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    points = []
+    for unroll in (4, 8):
+        for per_cu in (1.5, 2, 3, 4):
+            grid = int(per_cu * cus)
+            for _ in range(2):
+                launch(grid, unroll)
+            e0.record(s)
+            for _ in range(reps):
+                launch(grid, unroll)
+            e1.record(s)
+            e1.synchronize()
+            gbs = nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+            points.append(dict(grid=grid, loads_in_flight_per_lane=unroll, gbs=gbs))
+    best = max(points, key=lambda p: p["gbs"])
+    return dict(kernel="read_kernel (tests/hw/hbm_read_probe.hip): 16-byte nontemporal loads, one pass",
+                buffer_bytes=nbytes, best_gbs=best["gbs"], best=best, frac_of_published_peak=best["gbs"] / HBM_PEAK_GBS,
+                points=points)
 
 
 def copy_calibration(torch, mib: int = 256, reps: int = 4):
@@ -688,7 +741,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true",
                     help="decode sweep only (skip the exact-path, prefill, router and 36-layer stack legs)")
     ap.add_argument("--stack-layers", type=int, default=36)
-    ap.add_argument("--leg", choices=("prefill", "router", "stack", "floor"),
+    ap.add_argument("--leg", choices=("prefill", "router", "stack", "floor", "read_ceiling"),
                     help="only run this leg of the bench and print its JSON (profiler runs)")
     args = ap.parse_args()
 
@@ -711,6 +764,8 @@ def main():
             res = bench_router(g, torch)
         elif args.leg == "floor":
             res = bench_launch_floor(torch)
+        elif args.leg == "read_ceiling":
+            res = bench_read_ceiling(torch)
         else:
             res = bench_stack(g, torch, layers=args.stack_layers)
         print(json.dumps({"leg": args.leg, **res}), flush=True)
@@ -777,6 +832,12 @@ def main():
         log("launch floor: dependent one-wave kernels in a hipGraph")
         extra["launch_floor"] = bench_launch_floor(torch)
         log(json.dumps(extra["launch_floor"]))
+        log("HBM read ceiling: a plain streaming read of 1 GiB")
+        extra["read_ceiling"] = bench_read_ceiling(torch)
+        log(json.dumps(extra["read_ceiling"]))
+        if rf is not None:
+            # the dominant kernel against what a plain read reaches here
+            rf["frac_of_measured_read_ceiling"] = rf["achieved"] / extra["read_ceiling"]["best_gbs"]
         log("residual add + RMSNorm in front of the MoE (B=1, 4, 64)")
         extra["residual_norm"] = [bench_residual(g, torch, copies[0], T) for T in (1, 4, 64)]
         log(json.dumps(extra["residual_norm"]))
