@@ -741,7 +741,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true",
                     help="decode sweep only (skip the exact-path, prefill, router and 36-layer stack legs)")
     ap.add_argument("--stack-layers", type=int, default=36)
-    ap.add_argument("--leg", choices=("prefill", "router", "stack", "floor", "read_ceiling"),
+    ap.add_argument("--leg", choices=("prefill", "router", "stack", "floor", "read_ceiling", "decode_exact"),
                     help="only run this leg of the bench and print its JSON (profiler runs)")
     args = ap.parse_args()
 
@@ -766,6 +766,12 @@ def main():
             res = bench_launch_floor(torch)
         elif args.leg == "read_ceiling":
             res = bench_read_ceiling(torch)
+        elif args.leg == "decode_exact":
+            # the exact decode kernels at the largest batch of --batches
+            T = max(int(b) for b in args.batches.split(","))
+            copies = [make_copy(g, torch, 1000 + c) for c in range(args.copies)]
+            res = bench_batch(g, torch, copies, T, args.steps, args.warmup, seed=T, graph_timing=not args.no_graph,
+                              exact=True)
         else:
             res = bench_stack(g, torch, layers=args.stack_layers)
         print(json.dumps({"leg": args.leg, **res}), flush=True)
