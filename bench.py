@@ -839,9 +839,12 @@ def main():
         extra["launch_floor"] = bench_launch_floor(torch)
         log(json.dumps(extra["launch_floor"]))
         log("HBM read ceiling: a plain streaming read of 1 GiB")
-        extra["read_ceiling"] = bench_read_ceiling(torch)
+        try:
+            extra["read_ceiling"] = bench_read_ceiling(torch)
+        except OSError as e:  # the probe library (tests/hw) is not built: the line goes out without it
+            extra["read_ceiling"] = {"error": str(e)}
         log(json.dumps(extra["read_ceiling"]))
-        if rf is not None:
+        if rf is not None and "best_gbs" in extra["read_ceiling"]:
             # the dominant kernel against what a plain read reaches here
             rf["frac_of_measured_read_ceiling"] = rf["achieved"] / extra["read_ceiling"]["best_gbs"]
         log("residual add + RMSNorm in front of the MoE (B=1, 4, 64)")
