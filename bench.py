@@ -43,32 +43,31 @@ MXFP4_PEAK_TFLOPS = 10100.0  # dense MXFP4 (fp4 x fp4) matrix-core peak
 # algorithmic bytes per touched expert: W1 nibbles + scales + bias, W2 nibbles + scales + bias
 W1_EXPERT_BYTES = 2 * I * H // 2 + 2 * I * H // 32 + 2 * I * 2
 W2_EXPERT_BYTES = H * I // 2 + H * I // 32 + H * 2
-ROUTER_BYTES = E * H * 2 + E * 2
 
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def layer_bytes(U: int, T: int) -> int:
+def layer_bytes(U: int, T: int, experts: int = E) -> int:
     """Algorithmic HBM bytes of one layer forward: each touched expert's MXFP4
     weights, scales and biases once, the router, and x / residual / out."""
-    return U * (W1_EXPERT_BYTES + W2_EXPERT_BYTES) + ROUTER_BYTES + T * H * 2 * 3
+    return U * (W1_EXPERT_BYTES + W2_EXPERT_BYTES) + experts * H * 2 + experts * 2 + T * H * 2 * 3
 
 
-def make_copy(g, torch, seed: int):
+def make_copy(g, torch, seed: int, experts: int = E):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     n1, s1 = g.tiled_size(2 * I, H)
     n2, s2 = g.tiled_size(H, I)
-    w1n = torch.randint(0, 256, (E * n1,), dtype=torch.uint8, device="cuda", generator=gen)
-    w1s = torch.randint(119, 124, (E * s1,), dtype=torch.uint8, device="cuda", generator=gen)
-    w2n = torch.randint(0, 256, (E * n2,), dtype=torch.uint8, device="cuda", generator=gen)
-    w2s = torch.randint(119, 124, (E * s2,), dtype=torch.uint8, device="cuda", generator=gen)
-    rw = (torch.randn((E, H), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
-    rb = (torch.randn((E,), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
-    b1 = torch.zeros((E, 2 * I), dtype=torch.bfloat16, device="cuda")
-    b2 = torch.zeros((E, H), dtype=torch.bfloat16, device="cuda")
+    w1n = torch.randint(0, 256, (experts * n1,), dtype=torch.uint8, device="cuda", generator=gen)
+    w1s = torch.randint(119, 124, (experts * s1,), dtype=torch.uint8, device="cuda", generator=gen)
+    w2n = torch.randint(0, 256, (experts * n2,), dtype=torch.uint8, device="cuda", generator=gen)
+    w2s = torch.randint(119, 124, (experts * s2,), dtype=torch.uint8, device="cuda", generator=gen)
+    rw = (torch.randn((experts, H), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    rb = (torch.randn((experts,), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    b1 = torch.zeros((experts, 2 * I), dtype=torch.bfloat16, device="cuda")
+    b2 = torch.zeros((experts, H), dtype=torch.bfloat16, device="cuda")
     return dict(tiled=(w1n, w1s, w2n, w2s), router_w=rw, router_b=rb, b1=b1, b2=b2)
 
 
@@ -101,13 +100,13 @@ def settle(torch, graph, s, ms: float = SETTLE_MS, max_replays: int = 200) -> in
 
 
 def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, graph_timing: bool = True,
-                exact: bool = False):
+                exact: bool = False, experts: int = E):
     """Time `steps` graph-replayed layer forwards at batch T; returns a dict.
     Without graph_timing the headline interval is the eager pass (profiler
     runs that count per-dispatch hardware counters)."""
     layers = []
     for c, wc in enumerate(copies):
-        cfg = g.default_config(E, T, decode_exact=exact)
+        cfg = g.default_config(experts, T, decode_exact=exact)
         L = g.MoELayer().init(cfg, 0, wc["router_w"], wc["router_b"], wc["b1"], wc["b2"], tiled=wc["tiled"])
         layers.append(L)
     gen = torch.Generator(device="cuda")
@@ -196,7 +195,7 @@ def bench_batch(g, torch, copies, T: int, steps: int, warmup: int, seed: int, gr
         L.destroy()
     ms_step = total_ms / steps
     u_mean = sum(U) / len(U)
-    bytes_step = sum(layer_bytes(u, T) for u in U) / len(U)
+    bytes_step = sum(layer_bytes(u, T, experts) for u in U) / len(U)
     w1_bytes = sum(u * W1_EXPERT_BYTES + T * H * 2 for u in U) / len(U)
     res = dict(batch=T, ms_per_step=ms_step, tokens_per_s=T / (ms_step / 1e3), experts_touched=u_mean,
                algorithmic_bytes_per_step=bytes_step, hbm_gbs=bytes_step / (ms_step / 1e3) / 1e9,
@@ -272,6 +271,19 @@ def bench_launch_floor(torch, chain: int = 200, sizes=(64, 1 << 20)):
         res[str(n)] = {"us_per_kernel": us, "us_per_4": 4 * us, "us_per_5": 5 * us}
         del graph
     return {"dependent_kernels_by_floats": res, "kernel": "torch add_ (fp32)", "chain": chain}
+
+
+def bench_cfg0(g, torch, steps: int, warmup: int, copies: int = 8):
+    """BASELINE config 0 on the GPU: one GPT-OSS-20B-shaped layer (32
+    experts, H = I = 2880, top-4) at batch 1, timed as the decode sweep is
+    (graph replay over `copies` weight copies, settled, per-launch events).
+    The config is the reference's CPU case; the CPU figure for it is in
+    `cpu_baseline.per_config`."""
+    cps = [make_copy(g, torch, 3000 + c, experts=32) for c in range(copies)]
+    torch.cuda.synchronize()
+    res = bench_batch(g, torch, cps, 1, steps, warmup, seed=1, experts=32)
+    res["experts"] = 32
+    return res
 
 
 def bench_read_ceiling(torch, mib: int = 1024, reps: int = 20):
@@ -741,7 +753,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true",
                     help="decode sweep only (skip the exact-path, prefill, router and 36-layer stack legs)")
     ap.add_argument("--stack-layers", type=int, default=36)
-    ap.add_argument("--leg", choices=("prefill", "router", "stack", "floor", "read_ceiling", "decode_exact"),
+    ap.add_argument("--leg", choices=("prefill", "router", "stack", "floor", "read_ceiling", "decode_exact", "cfg0"),
                     help="only run this leg of the bench and print its JSON (profiler runs)")
     args = ap.parse_args()
 
@@ -766,6 +778,8 @@ def main():
             res = bench_launch_floor(torch)
         elif args.leg == "read_ceiling":
             res = bench_read_ceiling(torch)
+        elif args.leg == "cfg0":
+            res = bench_cfg0(g, torch, args.steps, args.warmup)
         elif args.leg == "decode_exact":
             # the exact decode kernels at the largest batch of --batches
             T = max(int(b) for b in args.batches.split(","))
@@ -838,6 +852,9 @@ def main():
         log("launch floor: dependent one-wave kernels in a hipGraph")
         extra["launch_floor"] = bench_launch_floor(torch)
         log(json.dumps(extra["launch_floor"]))
+        log("config 0 on the GPU: GPT-OSS-20B shape (32 experts), batch 1")
+        extra["cfg0_gptoss20b_b1"] = bench_cfg0(g, torch, args.steps, args.warmup)
+        log(json.dumps(extra["cfg0_gptoss20b_b1"]))
         log("HBM read ceiling: a plain streaming read of 1 GiB")
         try:
             extra["read_ceiling"] = bench_read_ceiling(torch)
