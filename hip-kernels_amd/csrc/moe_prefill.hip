@@ -152,12 +152,17 @@ struct TileList {
   int F, P1, P2, P3;       // totals (every lane)
 };
 
-__device__ __forceinline__ TileList make_tile_list(const int32_t* __restrict__ offsets, int E, int lane) {
-  TileList L;
-  int o[kExpertsPerLane + 1];
+// The offsets a lane reads for make_tile_list, all in flight at once.
+__device__ __forceinline__ void load_tile_offsets(const int32_t* __restrict__ offsets, int E, int lane,
+                                                  int (&o)[kExpertsPerLane + 1]) {
   const int e0 = lane * kExpertsPerLane;
 #pragma unroll
-  for (int i = 0; i <= kExpertsPerLane; ++i) o[i] = offsets[min(e0 + i, E)];  // all in flight at once
+  for (int i = 0; i <= kExpertsPerLane; ++i) o[i] = offsets[min(e0 + i, E)];
+}
+
+__device__ __forceinline__ TileList make_tile_list(const int (&o)[kExpertsPerLane + 1], int E, int lane) {
+  TileList L;
+  const int e0 = lane * kExpertsPerLane;
   int lf = 0, l1 = 0, l2 = 0, l3 = 0;
 #pragma unroll
   for (int i = 0; i < kExpertsPerLane; ++i) {
@@ -970,6 +975,10 @@ __global__ __launch_bounds__(kW * kWave, WgShape<kW>::kPerCU) void grouped_mfma_
   int k = 0;  // queues found empty
   for (int round = 0;; ++round) {
     const int x = (x0 + k) & 7;
+    // The tile list's loads go out ahead of the take, so the tile switch
+    // waits for the longer of the two round trips rather than their sum.
+    int toff[kExpertsPerLane + 1];
+    load_tile_offsets(a.offsets, a.E, lane, toff);
     int t;
     if (persistent) {
       if (threadIdx.x == 0) word[round & 1] = atomicAdd(&a.queue[kQueueStride * x], 1);
@@ -979,7 +988,7 @@ __global__ __launch_bounds__(kW * kWave, WgShape<kW>::kPerCU) void grouped_mfma_
       if (round > 0) break;
       t = vb >> 3;
     }
-    const TileList L = make_tile_list(a.offsets, a.E, lane);
+    const TileList L = make_tile_list(toff, a.E, lane);
     int lenF;
     if (t >= queue_len(L, a.nwt, x, lenF)) {
       if (!persistent) break;
@@ -1014,10 +1023,12 @@ __global__ __launch_bounds__(kMxW * kWave, 1) void grouped_mx_kernel(GroupedPara
   int k = 0;  // queues found empty
   for (int round = 0;; ++round) {
     const int x = (x0 + k) & 7;
+    int toff[kExpertsPerLane + 1];
+    load_tile_offsets(a.offsets, a.E, lane, toff);  // ahead of the take, as in grouped_mfma_kernel
     if (threadIdx.x == 0) word[round & 1] = atomicAdd(&a.queue[kQueueStride * x], 1);
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(word[round & 1]);
-    const TileList L = make_tile_list(a.offsets, a.E, lane);
+    const TileList L = make_tile_list(toff, a.E, lane);
     int lenF;
     if (t >= queue_len(L, a.nwt, x, lenF)) {
       k = next_queue(a.queue, word, x0, k, L, a.nwt);
