@@ -16,7 +16,9 @@
 // * Work items are (active expert, 64-row tile) pairs of the routing plan's
 //   task records; a work-group of P waves takes items v, v + G, ... (G = grid,
 //   v the XCD-grouped block index, so one XCD's work-groups cover a
-//   contiguous item range and share the items' token rows in their L2).
+//   contiguous item range and share the items' token rows in their L2);
+//   gate_up's last, partial round takes item r G + b (b the block index),
+//   which spreads the round's items over the XCDs and CUs.
 //   Wave p reduces over K-part p (nb / P blocks of 32); the P partial sums
 //   meet in LDS and are added in part order (deterministic).
 // * Per block, lane l issues one 16-byte nontemporal load of slot l of the
@@ -218,11 +220,21 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     nact = __builtin_amdgcn_readfirstlane(*a.n_active);
   }
   const int n_items = nact * ntiles;
-  if (v >= n_items) {  // the whole work-group, before any further barrier
+  // Item of round r: r G + v while every work-group has one (r < kfull).
+  // gate_up takes r G + vb in the last, partial round, whose items then
+  // spread over the XCDs and over distinct CUs instead of filling the first
+  // XCDs' ranges (two boxes, three interleaved pairs each: B=16 gate_up
+  // 73.5-74.6 -> 71.3-73.0 us, B=64 148.4-153.7 -> 147.3-149.0, B=8 and 32
+  // even); down keeps v there (at 64 and 32 tokens it measured 0.3-0.7 us
+  // slower in block order, even at 8).
+  const int kfull = n_items / G;
+  auto round_item = [&](int r) { return r * G + (kGated && r >= kfull ? vb : v); };
+  const int q0 = round_item(0);
+  if (q0 >= n_items) {  // the whole work-group, before any further barrier
     if constexpr (kRoute)
       if (r1_publish)
-        route_one_token_publish_k(r1, a.r_k, a.r_E, a.r_variant, a.r_plan, v - n_items, G - n_items, a.r_idx, a.r_w,
-                                  lane);
+        route_one_token_publish_k(r1, a.r_k, a.r_E, a.r_variant, a.r_plan, q0 - n_items, G - n_items, a.r_idx,
+                                  a.r_w, lane);
     return;
   }
 
@@ -250,6 +262,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   const int lo16 = lane & 15, g16 = lane >> 4;
   const uint32_t voffA = static_cast<uint32_t>(lane) * 16, voffS = static_cast<uint32_t>(lo16) * 4;
 
+  int qr = 1, qa = round_item(1);  // the next item and its round
   auto step_of = [&](int q, int cg) -> McStep {
     McStep s;
     s.valid = q < n_items;
@@ -268,7 +281,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
   };
   auto next_of = [&](const McStep& s) -> McStep {
     if ((s.cg + 1) * kTok < s.M) return step_of(s.q, s.cg + 1);
-    return step_of(s.q + G, 0);
+    return step_of(qa, 0);
   };
   // Input rows of the B operand for this lane's column of each chunk:
   // gate_up gathers the slot's token, down reads the slot's activation row.
@@ -372,7 +385,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
     }
   };
 
-  McStep cur = step_of(v, 0);
+  McStep cur = step_of(q0, 0);
   McSrc<NC> cs;
   Staged st0;
   {
@@ -546,6 +559,7 @@ __global__ __launch_bounds__(P * kWave) void mc_stream_kernel(McParams a) {
 #pragma unroll
       for (int u = 0; u < D; ++u) issue_lds(u, u);
     }
+    if (nxt.cg == 0) qa = round_item(++qr);  // nxt starts item qa
     cur = nxt;
     cs = ns;
   }
